@@ -1,0 +1,203 @@
+"""``attention`` on gfx950 HIP kernels (bf16/fp16 MFMA; fp32 SIMT).
+
+Drop-in for alkinun/helion ``tritium/ops/attention.py``: same signature
+(``attention(q, k, v, *, is_causal=True)`` 739-757), validation and messages
+(``_check_attention_inputs`` 220-281), autograd (``_AttentionAutograd``
+705-736), GQA, ``q_len != kv_len``, strided q/k/v (the module path passes
+``transpose(1, 2)`` views, helion/nn.py:212-220) and the KV-cache
+``q_len == 1`` call (helion/nn.py:275-280).
+
+Differences:
+
+* ``dq``, ``dk`` and ``dv`` are written with their own strides.  The
+  reference stores ``dq`` as if it were contiguous while allocating it with
+  q's strides (attention.py:625-629 vs 645), which permutes it for the
+  module's transposed views; here it is correct for any layout;
+* ``dk``/``dv`` are reduced in registers (no fp32 atomics) and the results are
+  bitwise deterministic;
+* head_dim above 1024 is rejected (the reference's autotuned Triton kernel
+  has no fixed bound, but its register tiles would not fit either).
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+
+from . import _lib
+from ._utils import FLOAT_DTYPES, check_cuda_tensor, check_supported_dtype, requires_autograd
+
+SUPPORTED_DTYPES = FLOAT_DTYPES
+MAX_HEAD_DIM = 1024
+
+
+def _check_attention_inputs(q, k, v) -> tuple[int, int, int, int, int, int]:
+    """attention.py:220-281."""
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        check_cuda_tensor(name, t)
+        check_supported_dtype(name, t, SUPPORTED_DTYPES)
+    if q.dim() != 4:
+        raise ValueError("q must be a 4D tensor shaped (batch, n_heads, q_seq_len, head_dim).")
+    batch, n_heads, q_len, head_dim = q.shape
+    n_kv_heads = k.shape[1] if k.dim() == 4 else 0
+    kv_len = k.shape[2] if k.dim() == 4 else 0
+    for name, t in (("k", k), ("v", v)):
+        if t.dim() != 4:
+            raise ValueError(
+                f"{name} must be a 4D tensor shaped (batch, n_kv_heads, kv_seq_len, head_dim)."
+            )
+        if t.shape[0] != batch:
+            raise ValueError(f"Shape mismatch: {name} has batch {t.shape[0]}, expected {batch}.")
+        if t.shape[2] != kv_len:
+            raise ValueError(
+                f"Shape mismatch: {name} has seq_len {t.shape[2]}, expected {kv_len}."
+            )
+        if t.shape[3] != head_dim:
+            raise ValueError(
+                f"Shape mismatch: {name} has head_dim {t.shape[3]}, expected {head_dim}."
+            )
+        if t.shape[1] != n_kv_heads:
+            raise ValueError(
+                f"Shape mismatch: {name} has {t.shape[1]} kv heads, expected {n_kv_heads}."
+            )
+        if t.dtype != q.dtype:
+            raise ValueError(f"Dtype mismatch: {name} has dtype {t.dtype}, q has dtype {q.dtype}.")
+        if t.device != q.device:
+            raise ValueError(f"Device mismatch: {name} is on {t.device}, q is on {q.device}.")
+    if n_kv_heads == 0 or n_heads % n_kv_heads != 0:
+        raise ValueError(
+            f"n_heads ({n_heads}) must be divisible by n_kv_heads ({n_kv_heads})."
+        )
+    if head_dim < 16 or (head_dim & (head_dim - 1)) != 0:
+        raise ValueError(f"head_dim must be a power of 2 >= 16, got {head_dim}.")
+    if head_dim > MAX_HEAD_DIM:
+        raise ValueError(f"head_dim must be <= {MAX_HEAD_DIM}, got {head_dim}.")
+    return batch, n_heads, n_kv_heads, q_len, kv_len, head_dim
+
+
+def _unit_last(t: torch.Tensor) -> torch.Tensor:
+    """The kernels address rows through (batch, head, seq) strides; head_dim
+    must be the unit-stride dimension."""
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def _strides(*ts: torch.Tensor) -> torch.Tensor:
+    vals: list[int] = []
+    for t in ts:
+        vals.extend(t.stride()[:3])
+    return torch.tensor(vals, dtype=torch.int64)
+
+
+def _attention_forward(q, k, v, is_causal: bool):
+    """attention.py:284-351."""
+    batch, n_heads, n_kv_heads, q_len, kv_len, head_dim = _check_attention_inputs(q, k, v)
+    q, k, v = _unit_last(q), _unit_last(k), _unit_last(v)
+    o = torch.empty_like(q)
+    if o.stride(-1) != 1:
+        o = torch.empty(q.shape, device=q.device, dtype=q.dtype)
+    lse = torch.empty((batch, n_heads, q_len), device=q.device, dtype=torch.float32)
+    if q_len == 0 or batch == 0:
+        return o, lse
+    strides = _strides(q, k, v, o)
+    _lib.call(
+        "tritium_attention_fwd",
+        q.data_ptr(),
+        k.data_ptr(),
+        v.data_ptr(),
+        o.data_ptr(),
+        lse.data_ptr(),
+        batch,
+        n_heads,
+        n_kv_heads,
+        q_len,
+        kv_len,
+        head_dim,
+        strides.data_ptr(),
+        int(bool(is_causal)),
+        _lib.dtype_code(q.dtype),
+        _lib.stream_of(q),
+    )
+    return o, lse
+
+
+def _attention_backward_impl(do, q, k, v, o, lse, is_causal: bool):
+    """attention.py:632-702, with correct strided outputs and no atomics."""
+    batch, n_heads, n_kv_heads, q_len, kv_len, head_dim = _check_attention_inputs(q, k, v)
+    q, k, v, o, do = (_unit_last(t) for t in (q, k, v, o, do))
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    if q_len == 0 or batch == 0 or kv_len == 0:
+        return dq.zero_(), dk.zero_(), dv.zero_()
+    delta = torch.empty((batch * n_heads * q_len,), device=q.device, dtype=torch.float32)
+    strides = _strides(q, k, v, o, do, dq, dk, dv)
+    _lib.call(
+        "tritium_attention_bwd",
+        do.data_ptr(),
+        q.data_ptr(),
+        k.data_ptr(),
+        v.data_ptr(),
+        o.data_ptr(),
+        lse.data_ptr(),
+        dq.data_ptr(),
+        dk.data_ptr(),
+        dv.data_ptr(),
+        delta.data_ptr(),
+        batch,
+        n_heads,
+        n_kv_heads,
+        q_len,
+        kv_len,
+        head_dim,
+        strides.data_ptr(),
+        int(bool(is_causal)),
+        _lib.dtype_code(q.dtype),
+        _lib.stream_of(q),
+    )
+    return dq, dk, dv
+
+
+class _AttentionAutograd(torch.autograd.Function):
+    """attention.py:705-736."""
+
+    @staticmethod
+    def forward(ctx: Any, q, k, v, is_causal: bool):
+        o, lse = _attention_forward(q, k, v, is_causal)
+        ctx.save_for_backward(q, k, v, o, lse)
+        ctx.is_causal = is_causal
+        return o
+
+    @staticmethod
+    def backward(ctx: Any, *grad_outputs: torch.Tensor):
+        do = grad_outputs[0]
+        q, k, v, o, lse = ctx.saved_tensors
+        if not do.is_contiguous():
+            do = do.contiguous()
+        dq, dk, dv = _attention_backward_impl(do, q, k, v, o, lse, ctx.is_causal)
+        return (
+            dq if ctx.needs_input_grad[0] else None,
+            dk if ctx.needs_input_grad[1] else None,
+            dv if ctx.needs_input_grad[2] else None,
+            None,
+        )
+
+
+def attention(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    *,
+    is_causal: bool = True,
+) -> torch.Tensor:
+    """Compute scaled dot-product attention over the last two dimensions.
+
+    q: (batch, n_heads, q_seq_len, head_dim); k, v: (batch, n_kv_heads,
+    kv_seq_len, head_dim) with n_heads divisible by n_kv_heads (GQA).
+    head_dim must be a power of 2 >= 16.  The causal mask is top-left aligned
+    (query i sees keys 0..i), as in attention.py:112-113.
+    """
+    if not requires_autograd(q, k, v):
+        o, _ = _attention_forward(q, k, v, is_causal)
+        return o
+    return _AttentionAutograd.apply(q, k, v, is_causal)

@@ -1,0 +1,173 @@
+// Fused AdamW for gfx950: one tensor per launch, or a whole parameter list in
+// ONE launch driven by a device-side descriptor table.
+//
+// Reference arithmetic: alkinun/helion tritium/ops/adamw.py:40-54 -- fp32
+// moments, decoupled weight decay on the pre-update parameter, then
+// p -= (lr / bc1) * m / (sqrt(v / bc2) + eps); bias corrections come from
+// the host (adamw.py:133-134).
+//
+// Each block updates one CHUNK of one tensor with 16-byte accesses (4 fp32 or
+// 8 fp16/bf16 parameters per access).  28 bytes move per fp32 parameter
+// (read p, g, m, v; write p, m, v) -- the whole step is one HBM pass.
+//
+// Multi-tensor table (int64, kDescWords per tensor, built by the host):
+//   [param_ptr, grad_ptr, exp_avg_ptr, exp_avg_sq_ptr, numel, flags,
+//    first_chunk]
+// flags = dtype code | (1 << 8 if all four pointers are 16-byte aligned).
+// first_chunk is the exclusive prefix sum of per-tensor chunk counts; block b
+// finds its tensor by binary search over it.
+#include "common.h"
+#include "../../include/tritium_hip.h"
+
+namespace tri {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kVecPerThread = 2;
+constexpr int64_t kChunk = (int64_t)kBlock * kVecPerThread * 8;  // 4096 elements
+
+struct Hyper {
+  float lr, beta1, beta2, eps, weight_decay, bc1, bc2;
+};
+
+__device__ __forceinline__ void adam_update(float& p, float g, float& m, float& v,
+                                            const Hyper& h, float lr_wd, float step_size) {
+  m = h.beta1 * m + (1.0f - h.beta1) * g;
+  v = h.beta2 * v + (1.0f - h.beta2) * g * g;
+  p = p - lr_wd * p;
+  const float denom = sqrtf(v / h.bc2) + h.eps;
+  p = p - step_size * m / denom;
+}
+
+// Update elements [start, start + kChunk) of one tensor (clipped to n).
+template <typename T>
+__device__ __forceinline__ void adam_chunk(T* __restrict__ p, const T* __restrict__ g,
+                                           float* __restrict__ m, float* __restrict__ v,
+                                           int64_t n, int64_t start, bool vec_ok,
+                                           const Hyper& h) {
+  const float lr_wd = h.lr * h.weight_decay;
+  const float step_size = h.lr / h.bc1;
+  constexpr int VEC = 16 / sizeof(T);
+  const int64_t end = min(start + kChunk, n);
+  if (vec_ok) {
+    // chunk starts are multiples of kChunk, hence of VEC; only the last chunk
+    // of a tensor can end inside a vector (handled element-wise below)
+    const int64_t vec_end = start + ((end - start) / VEC) * VEC;
+    constexpr int NVEC = (int)(kChunk / VEC / kBlock);
+    float pv[NVEC][VEC], gv[NVEC][VEC], mv[NVEC][VEC], vv[NVEC][VEC];
+#pragma unroll
+    for (int u = 0; u < NVEC; ++u) {
+      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
+      if (e < vec_end) {
+        load_f32<T, VEC>(p + e, pv[u]);
+        load_f32<T, VEC>(g + e, gv[u]);
+        load_f32<float, VEC>(m + e, mv[u]);
+        load_f32<float, VEC>(v + e, vv[u]);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < NVEC; ++u) {
+      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
+      if (e < vec_end) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) adam_update(pv[u][i], gv[u][i], mv[u][i], vv[u][i], h, lr_wd, step_size);
+        store_f32<float, VEC>(m + e, mv[u]);
+        store_f32<float, VEC>(v + e, vv[u]);
+        store_f32<T, VEC>(p + e, pv[u]);
+      }
+    }
+    for (int64_t e = vec_end + threadIdx.x; e < end; e += kBlock) {
+      float pp = to_f32(p[e]), mm = m[e], vv2 = v[e];
+      adam_update(pp, to_f32(g[e]), mm, vv2, h, lr_wd, step_size);
+      m[e] = mm;
+      v[e] = vv2;
+      p[e] = from_f32<T>(pp);
+    }
+  } else {
+    for (int64_t e = start + threadIdx.x; e < end; e += kBlock) {
+      float pp = to_f32(p[e]), mm = m[e], vv2 = v[e];
+      adam_update(pp, to_f32(g[e]), mm, vv2, h, lr_wd, step_size);
+      m[e] = mm;
+      v[e] = vv2;
+      p[e] = from_f32<T>(pp);
+    }
+  }
+}
+
+template <typename T>
+__global__ void __launch_bounds__(kBlock)
+adamw_single_kernel(T* __restrict__ p, const T* __restrict__ g, float* __restrict__ m,
+                    float* __restrict__ v, int64_t n, int vec_ok, Hyper h) {
+  adam_chunk<T>(p, g, m, v, n, (int64_t)blockIdx.x * kChunk, vec_ok != 0, h);
+}
+
+constexpr int kDescWords = 7;
+
+__global__ void __launch_bounds__(kBlock)
+adamw_multi_kernel(const int64_t* __restrict__ table, int n_tensors, Hyper h) {
+  // binary search: last tensor whose first_chunk <= blockIdx.x
+  const int64_t b = blockIdx.x;
+  int lo = 0, hi = n_tensors - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (table[mid * kDescWords + 6] <= b) lo = mid; else hi = mid - 1;
+  }
+  const int64_t* d = table + lo * kDescWords;
+  const int64_t n = d[4];
+  const int flags = (int)d[5];
+  const int64_t start = (b - d[6]) * kChunk;
+  if (start >= n) return;
+  const bool vec_ok = (flags >> 8) & 1;
+  switch (flags & 0xff) {
+    case kF32:
+      adam_chunk<float>((float*)d[0], (const float*)d[1], (float*)d[2], (float*)d[3], n, start, vec_ok, h);
+      break;
+    case kF16:
+      adam_chunk<f16_t>((f16_t*)d[0], (const f16_t*)d[1], (float*)d[2], (float*)d[3], n, start, vec_ok, h);
+      break;
+    case kBF16:
+      adam_chunk<bf16_t>((bf16_t*)d[0], (const bf16_t*)d[1], (float*)d[2], (float*)d[3], n, start, vec_ok, h);
+      break;
+    default:
+      break;
+  }
+}
+
+Hyper make_hyper(float lr, float beta1, float beta2, float eps, float wd, double bc1, double bc2) {
+  return Hyper{lr, beta1, beta2, eps, wd, (float)bc1, (float)bc2};
+}
+
+}  // namespace
+}  // namespace tri
+
+using namespace tri;
+
+extern "C" int64_t tritium_adamw_chunk_elements(void) { return kChunk; }
+
+extern "C" int tritium_adamw_step(void* param, const void* grad, float* exp_avg, float* exp_avg_sq,
+                                  int64_t n, float lr, float beta1, float beta2, float eps,
+                                  float weight_decay, double bias_correction1,
+                                  double bias_correction2, int dtype, void* stream) {
+  if (n < 0) return fail(TRI_EINVAL, "adamw: negative numel");
+  if (n == 0) return TRI_OK;
+  const Hyper h = make_hyper(lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2);
+  const int vec_ok = aligned16(param) && aligned16(grad) && aligned16(exp_avg) && aligned16(exp_avg_sq);
+  const int64_t blocks = cdiv(n, kChunk);
+  if (blocks >= ((int64_t)1 << 31)) return fail(TRI_EINVAL, "adamw: tensor too large");
+  TRI_DISPATCH_FLOAT(dtype, T,
+    adamw_single_kernel<T><<<(unsigned)blocks, kBlock, 0, (hipStream_t)stream>>>(
+        (T*)param, (const T*)grad, exp_avg, exp_avg_sq, n, vec_ok, h));
+  return check_launch("adamw step");
+}
+
+extern "C" int tritium_adamw_step_multi(const int64_t* table, int n_tensors, int64_t total_chunks,
+                                        float lr, float beta1, float beta2, float eps,
+                                        float weight_decay, double bias_correction1,
+                                        double bias_correction2, void* stream) {
+  if (n_tensors < 0 || total_chunks < 0) return fail(TRI_EINVAL, "adamw multi: bad table size");
+  if (n_tensors == 0 || total_chunks == 0) return TRI_OK;
+  if (total_chunks >= ((int64_t)1 << 31)) return fail(TRI_EINVAL, "adamw multi: too many chunks");
+  const Hyper h = make_hyper(lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2);
+  adamw_multi_kernel<<<(unsigned)total_chunks, kBlock, 0, (hipStream_t)stream>>>(table, n_tensors, h);
+  return check_launch("adamw multi-tensor step");
+}

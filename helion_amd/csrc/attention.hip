@@ -1,0 +1,899 @@
+// Scaled dot-product attention (causal or not, GQA, q_len != kv_len) for gfx950.
+//
+// Reference arithmetic: alkinun/helion tritium/ops/attention.py:69-141
+// (forward: scale = head_dim^-0.5 applied to q.k, top-left causal mask
+// q_pos >= kv_pos, online softmax, lse = m + ln l) and 399-629 (backward:
+// P = exp(s - lse), dP = dO v^T, D_i = rowsum(P dP), dS = P (dP - D_i),
+// dV = P^T dO, dQ = dS k * scale, dK = dS^T q * scale).
+//
+// bf16 / fp16 inputs with head_dim in {16, 32, 64, 128} run on the MFMA path
+// (v_mfma_f32_32x32x16_{bf16,f16}, fp32 accumulation):
+//
+//  forward   one workgroup = 4 wavefronts = 128 query rows of one (batch, head);
+//            a wavefront computes S^T = K Q^T for its 32 query rows against a
+//            64-row K/V tile staged in LDS, so each lane owns ONE query column:
+//            the online-softmax max needs a single lane^32 exchange and P^T
+//            feeds the next MFMA (O^T = V^T P^T) straight from registers.  V is
+//            stored transposed in LDS so that operand is two 8-byte LDS reads.
+//  backward  (1) delta = rowsum(dO * O) pre-pass; (2) KV-parallel dK/dV kernel:
+//            a wavefront owns 32 kv rows (K, V fragments in registers) and
+//            sweeps the query tiles that can see them, accumulating dV^T and
+//            dK^T in registers (GQA: all query heads of the group), written
+//            once in the output dtype; (3) Q-parallel dQ kernel.  No atomics,
+//            results are bitwise deterministic.
+//
+// fp32 inputs (and head_dim outside the MFMA set, up to 1024) run on a SIMT
+// path: one wavefront per row, exact fp32 arithmetic.
+//
+// Workgroup order is XCD-aware: the 8 XCDs receive workgroups round-robin, so
+// block ids are remapped to give every XCD a contiguous range of
+// (batch, head)s (their K/V stay in that XCD's L2), heaviest causal tiles
+// first.
+#include <math.h>
+
+#include <type_traits>
+
+#include "common.h"
+#include "../../include/tritium_hip.h"
+
+namespace tri {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr int kXcds = 8;
+
+template <typename T> struct Mfma;
+template <> struct Mfma<bf16_t> {
+  typedef bf16x8_t V;
+  static __device__ __forceinline__ f32x16 mma(V a, V b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<f16_t> {
+  typedef f16x8_t V;
+  static __device__ __forceinline__ f32x16 mma(V a, V b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// 8 consecutive elements (16 bytes, 16-byte aligned).
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::V ld8(const T* p) {
+  return *reinterpret_cast<const typename Mfma<T>::V*>(p);
+}
+
+// Elements p0[0..3] followed by p1[0..3] (two 8-byte aligned reads).
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::V ld4x2(const T* p0, const T* p1) {
+  const uint2 a = *reinterpret_cast<const uint2*>(p0);
+  const uint2 b = *reinterpret_cast<const uint2*>(p1);
+  uint4 u;
+  u.x = a.x; u.y = a.y; u.z = b.x; u.w = b.y;
+  return __builtin_bit_cast(typename Mfma<T>::V, u);
+}
+
+template <typename T>
+__device__ __forceinline__ typename Mfma<T>::V zero8() {
+  return __builtin_bit_cast(typename Mfma<T>::V, make_uint4(0, 0, 0, 0));
+}
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) z[i] = 0.f;
+  return z;
+}
+
+// Workgroup id -> work id such that each XCD (block id mod 8) processes a
+// contiguous range of work ids.
+__device__ __forceinline__ int xcd_remap(int bid, int n) {
+  if (n % kXcds != 0) return bid;
+  return (bid % kXcds) * (n / kXcds) + bid / kXcds;
+}
+
+struct FwdArgs {
+  const void* q; const void* k; const void* v; void* o; float* lse;
+  int64_t sq_b, sq_h, sq_s, sk_b, sk_h, sk_s, sv_b, sv_h, sv_s, so_b, so_h, so_s;
+  int B, H, Hkv, Tq, Tkv, n_tiles, causal;
+  float scale;  // head_dim ** -0.5
+};
+
+struct BwdArgs {
+  const void* q; const void* k; const void* v; const void* o; const void* dout;
+  const float* lse; float* delta; void* dq; void* dk; void* dv;
+  int64_t sq_b, sq_h, sq_s, sk_b, sk_h, sk_s, sv_b, sv_h, sv_s, so_b, so_h, so_s;
+  int64_t sdo_b, sdo_h, sdo_s, sdq_b, sdq_h, sdq_s, sdk_b, sdk_h, sdk_s, sdv_b, sdv_h, sdv_s;
+  int B, H, Hkv, Tq, Tkv, n_tiles, causal;
+  float scale;
+};
+
+// Copy a ROWS x D tile of T (row stride `ld` elements in global memory,
+// rows >= valid_rows read as zero) into LDS twice: row-major (`rm`, row
+// stride RLD) and transposed (`tr`, row stride TLD, one row per d).  Each
+// thread moves 4 rows x 8 columns: four 16-byte global loads, four 16-byte
+// row-major LDS writes, eight 8-byte transposed LDS writes.
+template <typename T, int ROWS, int D, int RLD, int TLD, bool RM, bool TR>
+__device__ __forceinline__ void stage_tile(const T* __restrict__ g, int64_t ld, int valid_rows,
+                                           T* rm, T* tr) {
+  constexpr int CH = D / 8;
+  constexpr int ITEMS = (ROWS / 4) * CH;
+  for (int it = threadIdx.x; it < ITEMS; it += 256) {
+    const int r4 = it / CH, cc = it % CH;
+    Pack<T, 8> rows[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int r = r4 * 4 + i;
+      if (r < valid_rows) {
+        rows[i] = *reinterpret_cast<const Pack<T, 8>*>(g + (int64_t)r * ld + cc * 8);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) rows[i].v[j] = (T)0.f;
+      }
+      if (RM) *reinterpret_cast<Pack<T, 8>*>(rm + r * RLD + cc * 8) = rows[i];
+    }
+    if (TR) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        Pack<T, 4> col;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) col.v[i] = rows[i].v[j];
+        *reinterpret_cast<Pack<T, 4>*>(tr + (cc * 8 + j) * TLD + r4 * 4) = col;
+      }
+    }
+  }
+}
+
+// Zero rows [D, DP) of a transposed LDS tile (head_dim < 32 pads to 32).
+template <typename T, int D, int DP, int TLD>
+__device__ __forceinline__ void zero_pad_rows(T* tr) {
+  for (int i = threadIdx.x; i < (DP - D) * TLD; i += 256) tr[D * TLD + i] = (T)0.f;
+}
+
+// Store 4 consecutive values (one C-fragment quad) as 4 elements of T.
+template <typename T>
+__device__ __forceinline__ void store4(T* p, float a, float b, float c, float d) {
+  Pack<T, 4> pk;
+  pk.v[0] = (T)a; pk.v[1] = (T)b; pk.v[2] = (T)c; pk.v[3] = (T)d;
+  *reinterpret_cast<Pack<T, 4>*>(p) = pk;
+}
+
+// ------------------------------------------------------------ MFMA forward --
+constexpr int kFwdBM = 128;
+constexpr int kFwdBN = 64;
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256)
+attn_fwd_mfma(FwdArgs a) {
+  typedef Mfma<T> M;
+  typedef typename M::V V;
+  constexpr int KS = D / 16;
+  constexpr int DP = D < 32 ? 32 : D;
+  constexpr int MT = DP / 32;
+  constexpr int KLD = D + 8;
+  constexpr int VLD = kFwdBN + 8;
+  __shared__ __attribute__((aligned(16))) T K_s[kFwdBN * KLD];
+  __shared__ __attribute__((aligned(16))) T Vt_s[DP * VLD];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = w / a.n_tiles;
+  const int qt = a.n_tiles - 1 - (w % a.n_tiles);
+  const int b = bh / a.H, h = bh % a.H;
+  const int hk = h / (a.H / a.Hkv);
+  const T* qp = (const T*)a.q + b * a.sq_b + h * a.sq_h;
+  const T* kp = (const T*)a.k + b * a.sk_b + hk * a.sk_h;
+  const T* vp = (const T*)a.v + b * a.sv_b + hk * a.sv_h;
+  T* op = (T*)a.o + b * a.so_b + h * a.so_h;
+  const int q0 = qt * kFwdBM;
+  const int qw0 = q0 + wave * 32;
+  const int qrow = qw0 + l32;
+  const bool qvalid = qrow < a.Tq;
+  const float sl2 = a.scale * kLog2e;
+
+  if (D < DP) {
+    zero_pad_rows<T, D, DP, VLD>(Vt_s);
+  }
+
+  V qf[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+    qf[s] = qvalid ? ld8(qp + (int64_t)qrow * a.sq_s + 16 * s + 8 * g) : zero8<T>();
+
+  f32x16 o[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) o[mt] = zero16();
+  float m = -INFINITY, l = 0.f;
+
+  const int kv_end = a.causal ? min(a.Tkv, q0 + kFwdBM) : a.Tkv;
+  for (int kv0 = 0; kv0 < kv_end; kv0 += kFwdBN) {
+    __syncthreads();
+    const int valid = min(kFwdBN, a.Tkv - kv0);
+    stage_tile<T, kFwdBN, D, KLD, VLD, true, false>(kp + (int64_t)kv0 * a.sk_s, a.sk_s, valid,
+                                                    K_s, nullptr);
+    stage_tile<T, kFwdBN, D, KLD, VLD, false, true>(vp + (int64_t)kv0 * a.sv_s, a.sv_s, valid,
+                                                    nullptr, Vt_s);
+    __syncthreads();
+
+    f32x16 s[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      s[u] = zero16();
+#pragma unroll
+      for (int st = 0; st < KS; ++st) {
+        const V kf = ld8(K_s + (32 * u + l32) * KLD + 16 * st + 8 * g);
+        s[u] = M::mma(kf, qf[st], s[u]);
+      }
+    }
+    // s[u][r] = S^T[kv0 + 32u + 8(r/4) + 4g + r%4][qrow]
+    const bool need_mask = (kv0 + kFwdBN > a.Tkv) || (a.causal && kv0 + kFwdBN - 1 > qw0);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = s[u][r] * sl2;
+        if (need_mask) {
+          const int kv = kv0 + 32 * u + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (kv >= a.Tkv || (a.causal && kv > qrow)) x = -INFINITY;
+        }
+        s[u][r] = x;
+        mx = fmaxf(mx, x);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m - m_use);
+    m = m_new;
+    float rs = 0.f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = exp2f(s[u][r] - m_use);
+        s[u][r] = p;
+        rs += p;
+      }
+    }
+    l = l * alpha + rs;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[mt][r] *= alpha;
+
+#pragma unroll
+    for (int t = 0; t < kFwdBN / 16; ++t) {
+      V pb;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pb[j] = (T)s[t >> 1][8 * (t & 1) + j];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const T* vr = Vt_s + (32 * mt + l32) * VLD + 16 * t + 4 * g;
+        o[mt] = M::mma(ld4x2<T>(vr, vr + 8), pb, o[mt]);
+      }
+    }
+  }
+
+  const float lt = l + __shfl_xor(l, 32, 64);
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  if (qvalid) {
+    T* orow = op + (int64_t)qrow * a.so_s;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d0 = 32 * mt + 8 * rr + 4 * g;
+        if (d0 < D)
+          store4<T>(orow + d0, o[mt][4 * rr] * inv, o[mt][4 * rr + 1] * inv,
+                    o[mt][4 * rr + 2] * inv, o[mt][4 * rr + 3] * inv);
+      }
+    }
+    if (g == 0) a.lse[(int64_t)bh * a.Tq + qrow] = (m + log2f(lt)) * kLn2;
+  }
+}
+
+// ------------------------------------------------------ backward: delta --
+// delta[bh][q] = sum_d dO[q][d] * O[q][d] (fp32).  One wavefront per row.
+template <typename T>
+__global__ void __launch_bounds__(256)
+attn_bwd_delta(BwdArgs a, int D) {
+  const int lane = threadIdx.x & 63;
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int64_t n_rows = (int64_t)a.B * a.H * a.Tq;
+  if (row >= n_rows) return;
+  const int q = (int)(row % a.Tq);
+  const int64_t bh = row / a.Tq;
+  const int b = (int)(bh / a.H), h = (int)(bh % a.H);
+  const T* o = (const T*)a.o + b * a.so_b + h * a.so_h + (int64_t)q * a.so_s;
+  const T* d = (const T*)a.dout + b * a.sdo_b + h * a.sdo_h + (int64_t)q * a.sdo_s;
+  float s = 0.f;
+  for (int i = lane; i < D; i += 64) s += to_f32(o[i]) * to_f32(d[i]);
+  s = wave_sum(s);
+  if (lane == 0) a.delta[row] = s;
+}
+
+// ------------------------------------------------- MFMA backward: dK, dV --
+constexpr int kDkvBN = 128;  // kv rows per workgroup (32 per wavefront)
+constexpr int kDkvBM = 64;   // query rows per step
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256)
+attn_bwd_dkdv_mfma(BwdArgs a) {
+  typedef Mfma<T> M;
+  typedef typename M::V V;
+  constexpr int KS = D / 16;
+  constexpr int DP = D < 32 ? 32 : D;
+  constexpr int MT = DP / 32;
+  constexpr int QLD = D + 8;
+  constexpr int TLD = kDkvBM + 8;
+  __shared__ __attribute__((aligned(16))) T Q_s[kDkvBM * QLD];
+  __shared__ __attribute__((aligned(16))) T dO_s[kDkvBM * QLD];
+  __shared__ __attribute__((aligned(16))) T Qt_s[DP * TLD];
+  __shared__ __attribute__((aligned(16))) T dOt_s[DP * TLD];
+  __shared__ float lse_s[kDkvBM], delta_s[kDkvBM];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int bhk = w / a.n_tiles;
+  const int kt = a.n_tiles - 1 - (w % a.n_tiles);  // heaviest (fewest visible queries) last
+  const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
+  const int group = a.H / a.Hkv;
+  const int kv0 = kt * kDkvBN;
+  const int kvw = kv0 + wave * 32 + l32;  // this lane's kv row (MFMA column)
+  const bool kvvalid = kvw < a.Tkv;
+  const T* kp = (const T*)a.k + b * a.sk_b + hk * a.sk_h;
+  const T* vp = (const T*)a.v + b * a.sv_b + hk * a.sv_h;
+  const float sl2 = a.scale * kLog2e;
+
+  if (D < DP) {
+    zero_pad_rows<T, D, DP, TLD>(Qt_s);
+    zero_pad_rows<T, D, DP, TLD>(dOt_s);
+  }
+
+  V kf[KS], vf[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    kf[s] = kvvalid ? ld8(kp + (int64_t)kvw * a.sk_s + 16 * s + 8 * g) : zero8<T>();
+    vf[s] = kvvalid ? ld8(vp + (int64_t)kvw * a.sv_s + 16 * s + 8 * g) : zero8<T>();
+  }
+  f32x16 dv[MT], dk[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    dv[mt] = zero16();
+    dk[mt] = zero16();
+  }
+
+  const int q_begin = a.causal ? (kv0 / kDkvBM) * kDkvBM : 0;
+  for (int hq = hk * group; hq < (hk + 1) * group; ++hq) {
+    const T* qp = (const T*)a.q + b * a.sq_b + hq * a.sq_h;
+    const T* dop = (const T*)a.dout + b * a.sdo_b + hq * a.sdo_h;
+    const float* lsep = a.lse + ((int64_t)b * a.H + hq) * a.Tq;
+    const float* delp = a.delta + ((int64_t)b * a.H + hq) * a.Tq;
+    for (int q0 = q_begin; q0 < a.Tq; q0 += kDkvBM) {
+      __syncthreads();
+      const int valid = min(kDkvBM, a.Tq - q0);
+      stage_tile<T, kDkvBM, D, QLD, TLD, true, true>(qp + (int64_t)q0 * a.sq_s, a.sq_s, valid,
+                                                     Q_s, Qt_s);
+      stage_tile<T, kDkvBM, D, QLD, TLD, true, true>(dop + (int64_t)q0 * a.sdo_s, a.sdo_s,
+                                                     valid, dO_s, dOt_s);
+      if (threadIdx.x < kDkvBM) {
+        const int qq = q0 + threadIdx.x;
+        lse_s[threadIdx.x] = qq < a.Tq ? lsep[qq] * kLog2e : INFINITY;
+        delta_s[threadIdx.x] = qq < a.Tq ? delp[qq] : 0.f;
+      }
+      __syncthreads();
+      if (a.causal && q0 + kDkvBM - 1 < kv0 + wave * 32) continue;  // wave fully masked
+
+#pragma unroll
+      for (int mq = 0; mq < kDkvBM / 32; ++mq) {
+        f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+        for (int st = 0; st < KS; ++st) {
+          const V qa = ld8(Q_s + (32 * mq + l32) * QLD + 16 * st + 8 * g);
+          s = M::mma(qa, kf[st], s);
+          const V da = ld8(dO_s + (32 * mq + l32) * QLD + 16 * st + 8 * g);
+          dp = M::mma(da, vf[st], dp);
+        }
+        // s[r] = S[q0 + 32mq + 8(r/4) + 4g + r%4][kvw]
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qi = 32 * mq + 8 * (r >> 2) + 4 * g + (r & 3);
+          float p = exp2f(s[r] * sl2 - lse_s[qi]);
+          if (!kvvalid || (a.causal && kvw > q0 + qi)) p = 0.f;
+          s[r] = p;
+          dp[r] = p * (dp[r] - delta_s[qi]);
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          V pb, db;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) {
+            pb[j] = (T)s[8 * t + j];
+            db[j] = (T)dp[8 * t + j];
+          }
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt) {
+            const T* dr = dOt_s + (32 * mt + l32) * TLD + 32 * mq + 16 * t + 4 * g;
+            dv[mt] = M::mma(ld4x2<T>(dr, dr + 8), pb, dv[mt]);
+            const T* qr = Qt_s + (32 * mt + l32) * TLD + 32 * mq + 16 * t + 4 * g;
+            dk[mt] = M::mma(ld4x2<T>(qr, qr + 8), db, dk[mt]);
+          }
+        }
+      }
+    }
+  }
+
+  if (kvvalid) {
+    T* dkr = (T*)a.dk + b * a.sdk_b + hk * a.sdk_h + (int64_t)kvw * a.sdk_s;
+    T* dvr = (T*)a.dv + b * a.sdv_b + hk * a.sdv_h + (int64_t)kvw * a.sdv_s;
+    const float sc = a.scale;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d0 = 32 * mt + 8 * rr + 4 * g;
+        if (d0 < D) {
+          store4<T>(dkr + d0, dk[mt][4 * rr] * sc, dk[mt][4 * rr + 1] * sc,
+                    dk[mt][4 * rr + 2] * sc, dk[mt][4 * rr + 3] * sc);
+          store4<T>(dvr + d0, dv[mt][4 * rr], dv[mt][4 * rr + 1], dv[mt][4 * rr + 2],
+                    dv[mt][4 * rr + 3]);
+        }
+      }
+    }
+  }
+}
+
+// ----------------------------------------------------- MFMA backward: dQ --
+constexpr int kDqBM = 128;  // query rows per workgroup (32 per wavefront)
+constexpr int kDqBN = 64;   // kv rows per step
+
+template <typename T, int D>
+__global__ void __launch_bounds__(256)
+attn_bwd_dq_mfma(BwdArgs a) {
+  typedef Mfma<T> M;
+  typedef typename M::V V;
+  constexpr int KS = D / 16;
+  constexpr int DP = D < 32 ? 32 : D;
+  constexpr int MT = DP / 32;
+  constexpr int KLD = D + 8;
+  constexpr int TLD = kDqBN + 8;
+  __shared__ __attribute__((aligned(16))) T K_s[kDqBN * KLD];
+  __shared__ __attribute__((aligned(16))) T V_s[kDqBN * KLD];
+  __shared__ __attribute__((aligned(16))) T Kt_s[DP * TLD];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = w / a.n_tiles;
+  const int qt = a.n_tiles - 1 - (w % a.n_tiles);
+  const int b = bh / a.H, h = bh % a.H;
+  const int hk = h / (a.H / a.Hkv);
+  const T* qp = (const T*)a.q + b * a.sq_b + h * a.sq_h;
+  const T* dop = (const T*)a.dout + b * a.sdo_b + h * a.sdo_h;
+  const T* kp = (const T*)a.k + b * a.sk_b + hk * a.sk_h;
+  const T* vp = (const T*)a.v + b * a.sv_b + hk * a.sv_h;
+  const int q0 = qt * kDqBM;
+  const int qw0 = q0 + wave * 32;
+  const int qrow = qw0 + l32;
+  const bool qvalid = qrow < a.Tq;
+  const float sl2 = a.scale * kLog2e;
+
+  if (D < DP) zero_pad_rows<T, D, DP, TLD>(Kt_s);
+
+  V qf[KS], df[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    qf[s] = qvalid ? ld8(qp + (int64_t)qrow * a.sq_s + 16 * s + 8 * g) : zero8<T>();
+    df[s] = qvalid ? ld8(dop + (int64_t)qrow * a.sdo_s + 16 * s + 8 * g) : zero8<T>();
+  }
+  const float lse2 = qvalid ? a.lse[(int64_t)bh * a.Tq + qrow] * kLog2e : INFINITY;
+  const float dl = qvalid ? a.delta[(int64_t)bh * a.Tq + qrow] : 0.f;
+
+  f32x16 dq[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) dq[mt] = zero16();
+
+  const int kv_end = a.causal ? min(a.Tkv, q0 + kDqBM) : a.Tkv;
+  for (int kv0 = 0; kv0 < kv_end; kv0 += kDqBN) {
+    __syncthreads();
+    const int valid = min(kDqBN, a.Tkv - kv0);
+    stage_tile<T, kDqBN, D, KLD, TLD, true, true>(kp + (int64_t)kv0 * a.sk_s, a.sk_s, valid,
+                                                  K_s, Kt_s);
+    stage_tile<T, kDqBN, D, KLD, TLD, true, false>(vp + (int64_t)kv0 * a.sv_s, a.sv_s, valid,
+                                                   V_s, nullptr);
+    __syncthreads();
+    if (a.causal && kv0 > qw0 + 31) continue;  // wave fully masked
+
+    f32x16 ds[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int st = 0; st < KS; ++st) {
+        s = M::mma(ld8(K_s + (32 * u + l32) * KLD + 16 * st + 8 * g), qf[st], s);
+        dp = M::mma(ld8(V_s + (32 * u + l32) * KLD + 16 * st + 8 * g), df[st], dp);
+      }
+      // s[r] = S^T[kv0 + 32u + 8(r/4) + 4g + r%4][qrow]
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int kv = kv0 + 32 * u + 8 * (r >> 2) + 4 * g + (r & 3);
+        float p = exp2f(s[r] * sl2 - lse2);
+        if (kv >= a.Tkv || (a.causal && kv > qrow)) p = 0.f;
+        ds[u][r] = p * (dp[r] - dl);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < kDqBN / 16; ++t) {
+      V db;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) db[j] = (T)ds[t >> 1][8 * (t & 1) + j];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const T* kr = Kt_s + (32 * mt + l32) * TLD + 16 * t + 4 * g;
+        dq[mt] = M::mma(ld4x2<T>(kr, kr + 8), db, dq[mt]);
+      }
+    }
+  }
+
+  if (qvalid) {
+    T* dqr = (T*)a.dq + b * a.sdq_b + h * a.sdq_h + (int64_t)qrow * a.sdq_s;
+    const float sc = a.scale;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d0 = 32 * mt + 8 * rr + 4 * g;
+        if (d0 < D)
+          store4<T>(dqr + d0, dq[mt][4 * rr] * sc, dq[mt][4 * rr + 1] * sc,
+                    dq[mt][4 * rr + 2] * sc, dq[mt][4 * rr + 3] * sc);
+      }
+    }
+  }
+}
+
+// --------------------------------------------------------------- SIMT path --
+// One wavefront per row; lane i owns head-dim entries i, i+64, ...
+constexpr int kSimtMaxPerLane = 16;  // head_dim <= 1024
+
+template <typename T, int PL>
+__global__ void __launch_bounds__(64)
+attn_fwd_simt(FwdArgs a, int D) {
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int qrow = (int)(row % a.Tq);
+  const int64_t bh = row / a.Tq;
+  const int b = (int)(bh / a.H), h = (int)(bh % a.H);
+  const int hk = h / (a.H / a.Hkv);
+  const T* qp = (const T*)a.q + b * a.sq_b + h * a.sq_h + (int64_t)qrow * a.sq_s;
+  const T* kp = (const T*)a.k + b * a.sk_b + hk * a.sk_h;
+  const T* vp = (const T*)a.v + b * a.sv_b + hk * a.sv_h;
+  float qv[PL], acc[PL];
+#pragma unroll
+  for (int j = 0; j < PL; ++j) {
+    const int d = lane + 64 * j;
+    qv[j] = d < D ? to_f32(qp[d]) : 0.f;
+    acc[j] = 0.f;
+  }
+  float m = -INFINITY, l = 0.f;
+  const int kv_end = a.causal ? min(a.Tkv, qrow + 1) : a.Tkv;
+  for (int kv = 0; kv < kv_end; ++kv) {
+    const T* kr = kp + (int64_t)kv * a.sk_s;
+    float part = 0.f;
+#pragma unroll
+    for (int j = 0; j < PL; ++j) {
+      const int d = lane + 64 * j;
+      if (d < D) part += qv[j] * to_f32(kr[d]);
+    }
+    const float s = wave_sum(part) * a.scale;
+    const float m_new = fmaxf(m, s);
+    const float alpha = expf(m - m_new);
+    const float p = expf(s - m_new);
+    l = l * alpha + p;
+    m = m_new;
+    const T* vr = vp + (int64_t)kv * a.sv_s;
+#pragma unroll
+    for (int j = 0; j < PL; ++j) {
+      const int d = lane + 64 * j;
+      acc[j] = acc[j] * alpha + (d < D ? p * to_f32(vr[d]) : 0.f);
+    }
+  }
+  const float inv = l > 0.f ? 1.0f / l : 0.f;
+  T* orow = (T*)a.o + b * a.so_b + h * a.so_h + (int64_t)qrow * a.so_s;
+#pragma unroll
+  for (int j = 0; j < PL; ++j) {
+    const int d = lane + 64 * j;
+    if (d < D) orow[d] = from_f32<T>(acc[j] * inv);
+  }
+  if (lane == 0) a.lse[row] = m + logf(l);
+}
+
+template <typename T, int PL>
+__global__ void __launch_bounds__(64)
+attn_bwd_dq_simt(BwdArgs a, int D) {
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;
+  const int qrow = (int)(row % a.Tq);
+  const int64_t bh = row / a.Tq;
+  const int b = (int)(bh / a.H), h = (int)(bh % a.H);
+  const int hk = h / (a.H / a.Hkv);
+  const T* qp = (const T*)a.q + b * a.sq_b + h * a.sq_h + (int64_t)qrow * a.sq_s;
+  const T* dp_ = (const T*)a.dout + b * a.sdo_b + h * a.sdo_h + (int64_t)qrow * a.sdo_s;
+  const T* kp = (const T*)a.k + b * a.sk_b + hk * a.sk_h;
+  const T* vp = (const T*)a.v + b * a.sv_b + hk * a.sv_h;
+  const float lse = a.lse[row], dl = a.delta[row];
+  float qv[PL], dov[PL], acc[PL];
+#pragma unroll
+  for (int j = 0; j < PL; ++j) {
+    const int d = lane + 64 * j;
+    qv[j] = d < D ? to_f32(qp[d]) : 0.f;
+    dov[j] = d < D ? to_f32(dp_[d]) : 0.f;
+    acc[j] = 0.f;
+  }
+  const int kv_end = a.causal ? min(a.Tkv, qrow + 1) : a.Tkv;
+  for (int kv = 0; kv < kv_end; ++kv) {
+    const T* kr = kp + (int64_t)kv * a.sk_s;
+    const T* vr = vp + (int64_t)kv * a.sv_s;
+    float ps = 0.f, pd = 0.f;
+#pragma unroll
+    for (int j = 0; j < PL; ++j) {
+      const int d = lane + 64 * j;
+      if (d < D) {
+        ps += qv[j] * to_f32(kr[d]);
+        pd += dov[j] * to_f32(vr[d]);
+      }
+    }
+    const float p = expf(wave_sum(ps) * a.scale - lse);
+    const float ds = p * (wave_sum(pd) - dl);
+#pragma unroll
+    for (int j = 0; j < PL; ++j) {
+      const int d = lane + 64 * j;
+      if (d < D) acc[j] += ds * to_f32(kr[d]);
+    }
+  }
+  T* out = (T*)a.dq + b * a.sdq_b + h * a.sdq_h + (int64_t)qrow * a.sdq_s;
+#pragma unroll
+  for (int j = 0; j < PL; ++j) {
+    const int d = lane + 64 * j;
+    if (d < D) out[d] = from_f32<T>(acc[j] * a.scale);
+  }
+}
+
+template <typename T, int PL>
+__global__ void __launch_bounds__(64)
+attn_bwd_dkdv_simt(BwdArgs a, int D) {
+  const int lane = threadIdx.x;
+  const int64_t row = blockIdx.x;  // over B * Hkv * Tkv
+  const int kv = (int)(row % a.Tkv);
+  const int64_t bhk = row / a.Tkv;
+  const int b = (int)(bhk / a.Hkv), hk = (int)(bhk % a.Hkv);
+  const int group = a.H / a.Hkv;
+  const T* kr = (const T*)a.k + b * a.sk_b + hk * a.sk_h + (int64_t)kv * a.sk_s;
+  const T* vr = (const T*)a.v + b * a.sv_b + hk * a.sv_h + (int64_t)kv * a.sv_s;
+  float kv_k[PL], kv_v[PL], dk[PL], dv[PL];
+#pragma unroll
+  for (int j = 0; j < PL; ++j) {
+    const int d = lane + 64 * j;
+    kv_k[j] = d < D ? to_f32(kr[d]) : 0.f;
+    kv_v[j] = d < D ? to_f32(vr[d]) : 0.f;
+    dk[j] = dv[j] = 0.f;
+  }
+  for (int hq = hk * group; hq < (hk + 1) * group; ++hq) {
+    const T* qp = (const T*)a.q + b * a.sq_b + hq * a.sq_h;
+    const T* dop = (const T*)a.dout + b * a.sdo_b + hq * a.sdo_h;
+    const int64_t rbase = ((int64_t)b * a.H + hq) * a.Tq;
+    for (int q = a.causal ? kv : 0; q < a.Tq; ++q) {
+      const T* qr = qp + (int64_t)q * a.sq_s;
+      const T* dr = dop + (int64_t)q * a.sdo_s;
+      float ps = 0.f, pd = 0.f;
+#pragma unroll
+      for (int j = 0; j < PL; ++j) {
+        const int d = lane + 64 * j;
+        if (d < D) {
+          ps += to_f32(qr[d]) * kv_k[j];
+          pd += to_f32(dr[d]) * kv_v[j];
+        }
+      }
+      const float p = expf(wave_sum(ps) * a.scale - a.lse[rbase + q]);
+      const float ds = p * (wave_sum(pd) - a.delta[rbase + q]);
+#pragma unroll
+      for (int j = 0; j < PL; ++j) {
+        const int d = lane + 64 * j;
+        if (d < D) {
+          dv[j] += p * to_f32(dr[d]);
+          dk[j] += ds * to_f32(qr[d]);
+        }
+      }
+    }
+  }
+  T* dko = (T*)a.dk + b * a.sdk_b + hk * a.sdk_h + (int64_t)kv * a.sdk_s;
+  T* dvo = (T*)a.dv + b * a.sdv_b + hk * a.sdv_h + (int64_t)kv * a.sdv_s;
+#pragma unroll
+  for (int j = 0; j < PL; ++j) {
+    const int d = lane + 64 * j;
+    if (d < D) {
+      dko[d] = from_f32<T>(dk[j] * a.scale);
+      dvo[d] = from_f32<T>(dv[j]);
+    }
+  }
+}
+
+// ------------------------------------------------------------- host side --
+bool mfma_head_dim(int64_t d) { return d == 16 || d == 32 || d == 64 || d == 128; }
+
+int simt_per_lane(int64_t d) {
+  int pl = 1;
+  while (pl * 64 < d) pl *= 2;
+  return pl;
+}
+
+#define TRI_SIMT_SWITCH(pl, LAUNCH)                                   \
+  switch (pl) {                                                       \
+    case 1: LAUNCH(1); break;  case 2: LAUNCH(2); break;              \
+    case 4: LAUNCH(4); break;  case 8: LAUNCH(8); break;              \
+    case 16: LAUNCH(16); break;                                       \
+    default: return fail(TRI_EINVAL, "attention: head_dim too large"); \
+  }
+
+#define TRI_HEAD_DIM_SWITCH(d, LAUNCH)                                \
+  switch (d) {                                                        \
+    case 16: LAUNCH(16); break;  case 32: LAUNCH(32); break;          \
+    case 64: LAUNCH(64); break;  case 128: LAUNCH(128); break;        \
+    default: return fail(TRI_EINVAL, "attention: no MFMA kernel for head_dim %d", (int)d); \
+  }
+
+template <typename T>
+int fwd_mfma(const FwdArgs& a, int64_t D, hipStream_t st) {
+  FwdArgs x = a;
+  x.n_tiles = (int)cdiv(a.Tq, kFwdBM);
+  const int64_t blocks = (int64_t)x.n_tiles * a.B * a.H;
+#define LAUNCH(DD) attn_fwd_mfma<T, DD><<<(unsigned)blocks, 256, 0, st>>>(x)
+  TRI_HEAD_DIM_SWITCH(D, LAUNCH)
+#undef LAUNCH
+  return check_launch("attention forward (mfma)");
+}
+
+template <typename T>
+int fwd_simt(const FwdArgs& a, int64_t D, hipStream_t st) {
+  const int64_t rows = (int64_t)a.B * a.H * a.Tq;
+#define LAUNCH(PL) attn_fwd_simt<T, PL><<<(unsigned)rows, 64, 0, st>>>(a, (int)D)
+  TRI_SIMT_SWITCH(simt_per_lane(D), LAUNCH)
+#undef LAUNCH
+  return check_launch("attention forward (simt)");
+}
+
+template <typename T>
+int bwd_mfma(const BwdArgs& a, int64_t D, hipStream_t st) {
+  BwdArgs x = a;
+  x.n_tiles = (int)cdiv(a.Tkv, kDkvBN);
+  const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;
+#define LAUNCH(DD) attn_bwd_dkdv_mfma<T, DD><<<(unsigned)kv_blocks, 256, 0, st>>>(x)
+  TRI_HEAD_DIM_SWITCH(D, LAUNCH)
+#undef LAUNCH
+  if (int e = check_launch("attention backward (dk/dv, mfma)")) return e;
+  x.n_tiles = (int)cdiv(a.Tq, kDqBM);
+  const int64_t q_blocks = (int64_t)x.n_tiles * a.B * a.H;
+#define LAUNCH(DD) attn_bwd_dq_mfma<T, DD><<<(unsigned)q_blocks, 256, 0, st>>>(x)
+  TRI_HEAD_DIM_SWITCH(D, LAUNCH)
+#undef LAUNCH
+  return check_launch("attention backward (dq, mfma)");
+}
+
+template <typename T>
+int bwd_impl(const BwdArgs& a, int64_t D, bool mfma, hipStream_t st) {
+  const int64_t rows = (int64_t)a.B * a.H * a.Tq;
+  attn_bwd_delta<T><<<(unsigned)cdiv(rows, 4), 256, 0, st>>>(a, (int)D);
+  if (int e = check_launch("attention backward (delta)")) return e;
+  if constexpr (!std::is_same<T, float>::value) {
+    if (mfma) return bwd_mfma<T>(a, D, st);
+  }
+  const int64_t kv_rows = (int64_t)a.B * a.Hkv * a.Tkv;
+  const int pl = simt_per_lane(D);
+#define LAUNCH(PL) attn_bwd_dq_simt<T, PL><<<(unsigned)rows, 64, 0, st>>>(a, (int)D)
+  TRI_SIMT_SWITCH(pl, LAUNCH)
+#undef LAUNCH
+  if (int e = check_launch("attention backward (dq, simt)")) return e;
+#define LAUNCH(PL) attn_bwd_dkdv_simt<T, PL><<<(unsigned)kv_rows, 64, 0, st>>>(a, (int)D)
+  TRI_SIMT_SWITCH(pl, LAUNCH)
+#undef LAUNCH
+  return check_launch("attention backward (dk/dv, simt)");
+}
+
+// Row strides must keep 16-byte alignment of every row for the MFMA path.
+bool rows_aligned(const void* p, int64_t sb, int64_t sh, int64_t ss) {
+  return aligned16(p) && sb % 8 == 0 && sh % 8 == 0 && ss % 8 == 0;
+}
+
+int check_dims(int64_t B, int64_t H, int64_t Hkv, int64_t Tq, int64_t Tkv, int64_t D) {
+  if (B < 0 || H <= 0 || Hkv <= 0 || H % Hkv != 0 || Tq < 0 || Tkv < 0 || D <= 0)
+    return fail(TRI_EINVAL, "attention: bad shape B=%lld H=%lld Hkv=%lld Tq=%lld Tkv=%lld D=%lld",
+                (long long)B, (long long)H, (long long)Hkv, (long long)Tq, (long long)Tkv,
+                (long long)D);
+  if (D > 64 * kSimtMaxPerLane)
+    return fail(TRI_EINVAL, "attention: head_dim %lld exceeds %d", (long long)D,
+                64 * kSimtMaxPerLane);
+  if (B * H * Tq >= ((int64_t)1 << 31) || B * Hkv * Tkv >= ((int64_t)1 << 31) ||
+      Tq >= ((int64_t)1 << 30) || Tkv >= ((int64_t)1 << 30))
+    return fail(TRI_EINVAL, "attention: problem too large");
+  return TRI_OK;
+}
+
+}  // namespace
+}  // namespace tri
+
+using namespace tri;
+
+extern "C" int tritium_attention_fwd(const void* q, const void* k, const void* v, void* o,
+                                     float* lse, int64_t B, int64_t H, int64_t Hkv, int64_t Tq,
+                                     int64_t Tkv, int64_t D, const int64_t* strides, int causal,
+                                     int dtype, void* stream) {
+  if (int e = check_dims(B, H, Hkv, Tq, Tkv, D)) return e;
+  if (B == 0 || Tq == 0) return TRI_OK;
+  FwdArgs a;
+  a.q = q; a.k = k; a.v = v; a.o = o; a.lse = lse;
+  a.sq_b = strides[0]; a.sq_h = strides[1]; a.sq_s = strides[2];
+  a.sk_b = strides[3]; a.sk_h = strides[4]; a.sk_s = strides[5];
+  a.sv_b = strides[6]; a.sv_h = strides[7]; a.sv_s = strides[8];
+  a.so_b = strides[9]; a.so_h = strides[10]; a.so_s = strides[11];
+  a.B = (int)B; a.H = (int)H; a.Hkv = (int)Hkv; a.Tq = (int)Tq; a.Tkv = (int)Tkv;
+  a.causal = causal != 0;
+  a.n_tiles = 0;
+  a.scale = (float)(1.0 / sqrt((double)D));
+  hipStream_t st = (hipStream_t)stream;
+  const bool mfma = dtype != kF32 && mfma_head_dim(D) &&
+                    rows_aligned(q, a.sq_b, a.sq_h, a.sq_s) &&
+                    rows_aligned(k, a.sk_b, a.sk_h, a.sk_s) &&
+                    rows_aligned(v, a.sv_b, a.sv_h, a.sv_s) && aligned16(o) &&
+                    a.so_s % 4 == 0 && a.so_b % 4 == 0 && a.so_h % 4 == 0;
+  if (mfma) {
+    if (dtype == kBF16) return fwd_mfma<bf16_t>(a, D, st);
+    return fwd_mfma<f16_t>(a, D, st);
+  }
+  TRI_DISPATCH_FLOAT(dtype, T, return fwd_simt<T>(a, D, st));
+  return TRI_OK;
+}
+
+extern "C" int tritium_attention_bwd(const void* dout, const void* q, const void* k,
+                                     const void* v, const void* o, const float* lse, void* dq,
+                                     void* dk, void* dv, float* delta, int64_t B, int64_t H,
+                                     int64_t Hkv, int64_t Tq, int64_t Tkv, int64_t D,
+                                     const int64_t* strides, int causal, int dtype,
+                                     void* stream) {
+  if (int e = check_dims(B, H, Hkv, Tq, Tkv, D)) return e;
+  if (B == 0 || Tq == 0 || Tkv == 0) return TRI_OK;
+  BwdArgs a;
+  a.q = q; a.k = k; a.v = v; a.o = o; a.dout = dout; a.lse = lse; a.delta = delta;
+  a.dq = dq; a.dk = dk; a.dv = dv;
+  a.sq_b = strides[0]; a.sq_h = strides[1]; a.sq_s = strides[2];
+  a.sk_b = strides[3]; a.sk_h = strides[4]; a.sk_s = strides[5];
+  a.sv_b = strides[6]; a.sv_h = strides[7]; a.sv_s = strides[8];
+  a.so_b = strides[9]; a.so_h = strides[10]; a.so_s = strides[11];
+  a.sdo_b = strides[12]; a.sdo_h = strides[13]; a.sdo_s = strides[14];
+  a.sdq_b = strides[15]; a.sdq_h = strides[16]; a.sdq_s = strides[17];
+  a.sdk_b = strides[18]; a.sdk_h = strides[19]; a.sdk_s = strides[20];
+  a.sdv_b = strides[21]; a.sdv_h = strides[22]; a.sdv_s = strides[23];
+  a.B = (int)B; a.H = (int)H; a.Hkv = (int)Hkv; a.Tq = (int)Tq; a.Tkv = (int)Tkv;
+  a.causal = causal != 0;
+  a.n_tiles = 0;
+  a.scale = (float)(1.0 / sqrt((double)D));
+  const bool out_ok = [&] {
+    const int64_t* s = strides + 15;
+    for (int i = 0; i < 9; ++i)
+      if (s[i] % 4 != 0) return false;
+    return aligned16(dq) && aligned16(dk) && aligned16(dv);
+  }();
+  const bool mfma = dtype != kF32 && mfma_head_dim(D) &&
+                    rows_aligned(q, a.sq_b, a.sq_h, a.sq_s) &&
+                    rows_aligned(k, a.sk_b, a.sk_h, a.sk_s) &&
+                    rows_aligned(v, a.sv_b, a.sv_h, a.sv_s) &&
+                    rows_aligned(dout, a.sdo_b, a.sdo_h, a.sdo_s) && out_ok;
+  hipStream_t st = (hipStream_t)stream;
+  TRI_DISPATCH_FLOAT(dtype, T, return bwd_impl<T>(a, D, mfma, st));
+  return TRI_OK;
+}

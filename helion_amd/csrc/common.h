@@ -1,0 +1,93 @@
+// Shared device helpers and C-ABI error plumbing for libtritium_hip.so.
+//
+// Everything here is written for gfx950 (CDNA4): 64-lane wavefronts,
+// 16-byte global vector accesses, hardware bf16 conversion.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+namespace tri {
+
+// dtype codes shared with the Python boundary (helion_amd/_lib.py).
+enum DType : int { kF32 = 0, kF16 = 1, kBF16 = 2 };
+
+typedef __bf16 bf16_t;
+typedef _Float16 f16_t;
+
+constexpr int kWave = 64;
+
+// N elements of T moved as one aligned access (16 bytes for N*sizeof(T)==16).
+template <typename T, int N>
+struct __attribute__((aligned(sizeof(T) * N))) Pack {
+  T v[N];
+};
+
+__device__ __forceinline__ float to_f32(float x) { return x; }
+__device__ __forceinline__ float to_f32(f16_t x) { return (float)x; }
+__device__ __forceinline__ float to_f32(bf16_t x) { return (float)x; }
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float x) {
+  return (T)x;  // round-to-nearest-even (v_cvt_pk_bf16_f32 / v_cvt_f16_f32)
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void load_f32(const T* __restrict__ p, float (&out)[N]) {
+  Pack<T, N> pk = *reinterpret_cast<const Pack<T, N>*>(p);
+#pragma unroll
+  for (int i = 0; i < N; ++i) out[i] = to_f32(pk.v[i]);
+}
+
+template <typename T, int N>
+__device__ __forceinline__ void store_f32(T* __restrict__ p, const float (&in)[N]) {
+  Pack<T, N> pk;
+#pragma unroll
+  for (int i = 0; i < N; ++i) pk.v[i] = from_f32<T>(in[i]);
+  *reinterpret_cast<Pack<T, N>*>(p) = pk;
+}
+
+// Butterfly sum over the 64 lanes of a wavefront; every lane gets the total.
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
+  return v;
+}
+
+__host__ __device__ constexpr inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline int dtype_size(int dtype) { return dtype == kF32 ? 4 : 2; }
+
+// ---- error plumbing (defined in capi.hip) ---------------------------------
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+// Returns 0, or records the pending launch error of the calling thread.
+int check_launch(const char* what);
+
+}  // namespace tri
+
+// Error codes returned by every extern "C" entry point.
+#define TRI_OK 0
+#define TRI_EINVAL 1   // argument rejected by the library
+#define TRI_ELAUNCH 2  // HIP runtime reported an error
+
+// Dispatch a runtime dtype code to a storage type `T` inside `body`.
+#define TRI_DISPATCH_FLOAT(dtype, T, ...)                                \
+  do {                                                                   \
+    switch (dtype) {                                                     \
+      case ::tri::kF32: { typedef float T; __VA_ARGS__; } break;         \
+      case ::tri::kF16: { typedef ::tri::f16_t T; __VA_ARGS__; } break;  \
+      case ::tri::kBF16: { typedef ::tri::bf16_t T; __VA_ARGS__; } break; \
+      default: return ::tri::fail(TRI_EINVAL, "unsupported dtype code %d", (int)(dtype)); \
+    }                                                                    \
+  } while (0)

@@ -1,0 +1,156 @@
+// SwiGLU forward and backward for gfx950.
+//
+// Reference arithmetic: alkinun/helion tritium/ops/swiglu.py:32-35 (forward)
+// and 51-58 (backward), all in fp32 with the result stored in the input dtype.
+//
+// Pure streaming kernels: each lane moves U 16-byte vectors per operand, the
+// U loads of a lane are issued before any math so a wavefront keeps
+// U * (#operands) * 1 KiB in flight; a block covers one contiguous
+// 256 * U * VEC element span, so every access is fully coalesced.
+#include "common.h"
+#include "../../include/tritium_hip.h"
+
+namespace tri {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int kUnroll = 4;
+
+__device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + __expf(-x)); }
+
+template <typename T, int VEC, int U>
+__global__ void __launch_bounds__(kBlock)
+swiglu_fwd_kernel(const T* __restrict__ x, const T* __restrict__ g, T* __restrict__ out,
+                  int64_t n) {
+  const int64_t nvec = n / VEC;
+  const int64_t first = (int64_t)blockIdx.x * kBlock * U + threadIdx.x;
+  float xv[U][VEC], gv[U][VEC];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t iv = first + (int64_t)u * kBlock;
+    if (iv < nvec) {
+      load_f32<T, VEC>(x + iv * VEC, xv[u]);
+      load_f32<T, VEC>(g + iv * VEC, gv[u]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t iv = first + (int64_t)u * kBlock;
+    if (iv < nvec) {
+      float o[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) o[i] = xv[u][i] * sigmoid_f32(xv[u][i]) * gv[u][i];
+      store_f32<T, VEC>(out + iv * VEC, o);
+    }
+  }
+  if (VEC > 1 && blockIdx.x == gridDim.x - 1) {
+    for (int64_t e = nvec * VEC + threadIdx.x; e < n; e += kBlock) {
+      const float a = to_f32(x[e]);
+      out[e] = from_f32<T>(a * sigmoid_f32(a) * to_f32(g[e]));
+    }
+  }
+}
+
+template <typename T, int VEC, int U>
+__global__ void __launch_bounds__(kBlock)
+swiglu_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ g,
+                  T* __restrict__ dx, T* __restrict__ dg, int64_t n) {
+  const int64_t nvec = n / VEC;
+  const int64_t first = (int64_t)blockIdx.x * kBlock * U + threadIdx.x;
+  float dv[U][VEC], xv[U][VEC], gv[U][VEC];
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t iv = first + (int64_t)u * kBlock;
+    if (iv < nvec) {
+      load_f32<T, VEC>(dy + iv * VEC, dv[u]);
+      load_f32<T, VEC>(x + iv * VEC, xv[u]);
+      load_f32<T, VEC>(g + iv * VEC, gv[u]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < U; ++u) {
+    const int64_t iv = first + (int64_t)u * kBlock;
+    if (iv < nvec) {
+      float ox[VEC], og[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const float s = sigmoid_f32(xv[u][i]);
+        const float silu = xv[u][i] * s;
+        const float dsilu = s * (1.0f + xv[u][i] * (1.0f - s));
+        ox[i] = dv[u][i] * gv[u][i] * dsilu;
+        og[i] = dv[u][i] * silu;
+      }
+      store_f32<T, VEC>(dx + iv * VEC, ox);
+      store_f32<T, VEC>(dg + iv * VEC, og);
+    }
+  }
+  if (VEC > 1 && blockIdx.x == gridDim.x - 1) {
+    for (int64_t e = nvec * VEC + threadIdx.x; e < n; e += kBlock) {
+      const float a = to_f32(x[e]), d = to_f32(dy[e]), gg = to_f32(g[e]);
+      const float s = sigmoid_f32(a);
+      dx[e] = from_f32<T>(d * gg * (s * (1.0f + a * (1.0f - s))));
+      dg[e] = from_f32<T>(d * (a * s));
+    }
+  }
+}
+
+template <int VEC>
+unsigned grid_for(int64_t n) {
+  const int64_t nvec = n / VEC;
+  return (unsigned)std::max<int64_t>(1, cdiv(nvec, (int64_t)kBlock * kUnroll));
+}
+
+template <typename T>
+int fwd_impl(const void* x, const void* g, void* out, int64_t n, hipStream_t s) {
+  constexpr int VEC = 16 / sizeof(T);
+  if (aligned16(x) && aligned16(g) && aligned16(out)) {
+    swiglu_fwd_kernel<T, VEC, kUnroll><<<grid_for<VEC>(n), kBlock, 0, s>>>(
+        (const T*)x, (const T*)g, (T*)out, n);
+  } else {
+    swiglu_fwd_kernel<T, 1, kUnroll><<<grid_for<1>(n), kBlock, 0, s>>>(
+        (const T*)x, (const T*)g, (T*)out, n);
+  }
+  return check_launch("swiglu forward");
+}
+
+template <typename T>
+int bwd_impl(const void* dy, const void* x, const void* g, void* dx, void* dg, int64_t n,
+             hipStream_t s) {
+  constexpr int VEC = 16 / sizeof(T);
+  if (aligned16(dy) && aligned16(x) && aligned16(g) && aligned16(dx) && aligned16(dg)) {
+    swiglu_bwd_kernel<T, VEC, kUnroll><<<grid_for<VEC>(n), kBlock, 0, s>>>(
+        (const T*)dy, (const T*)x, (const T*)g, (T*)dx, (T*)dg, n);
+  } else {
+    swiglu_bwd_kernel<T, 1, kUnroll><<<grid_for<1>(n), kBlock, 0, s>>>(
+        (const T*)dy, (const T*)x, (const T*)g, (T*)dx, (T*)dg, n);
+  }
+  return check_launch("swiglu backward");
+}
+
+int check_n(int64_t n) {
+  if (n < 0 || n / ((int64_t)kBlock * kUnroll) >= ((int64_t)1 << 31))
+    return fail(TRI_EINVAL, "swiglu: unsupported element count %lld", (long long)n);
+  return TRI_OK;
+}
+
+}  // namespace
+}  // namespace tri
+
+using namespace tri;
+
+extern "C" int tritium_swiglu_fwd(const void* x, const void* gate, void* out, int64_t n,
+                                  int dtype, void* stream) {
+  if (int e = check_n(n)) return e;
+  if (n == 0) return TRI_OK;
+  TRI_DISPATCH_FLOAT(dtype, T, return fwd_impl<T>(x, gate, out, n, (hipStream_t)stream));
+  return TRI_OK;
+}
+
+extern "C" int tritium_swiglu_bwd(const void* dy, const void* x, const void* gate, void* dx,
+                                  void* dgate, int64_t n, int dtype, void* stream) {
+  if (int e = check_n(n)) return e;
+  if (n == 0) return TRI_OK;
+  TRI_DISPATCH_FLOAT(dtype, T,
+                     return bwd_impl<T>(dy, x, gate, dx, dgate, n, (hipStream_t)stream));
+  return TRI_OK;
+}

@@ -1,0 +1,140 @@
+/*
+ * tritium_hip.h -- C ABI of libtritium_hip.so, the gfx950 (MI355X) kernel
+ * library behind the Python `helion_amd` package (a drop-in for the
+ * reference's `tritium.ops` layer, alkinun/helion tritium/ops/).
+ *
+ * Conventions for every entry point:
+ *   - all tensor arguments are raw device pointers to densely packed,
+ *     row-major data unless a stride argument says otherwise;
+ *   - `dtype` codes: 0 = float32, 1 = float16, 2 = bfloat16;
+ *   - `stream` is a hipStream_t (torch.cuda.current_stream().cuda_stream);
+ *     every call only enqueues work on it and never synchronises;
+ *   - the library never allocates device memory: outputs and workspaces come
+ *     from the caller (torch's caching allocator on the Python side);
+ *   - return value 0 = success, 1 = argument rejected, 2 = HIP launch error;
+ *     tritium_last_error() then returns a message (thread-local).
+ */
+#ifndef TRITIUM_HIP_H_
+#define TRITIUM_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#define TRITIUM_HIP_ABI_VERSION 1
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* ---- library -------------------------------------------------------------
+ * Replaces tritium/_compat.py:1-34 (the Triton build shim applied at import):
+ * the loader checks these before any kernel call. */
+const char* tritium_last_error(void);
+int tritium_abi_version(void);
+int tritium_runtime_version(void);
+
+/* ---- RMSNorm ---------------------------------------------------------------
+ * Forward of tritium.rmsnorm / tritium.residual_rmsnorm
+ * (tritium/ops/rmsnorm.py:29-51 `_rmsnorm_forward_kernel`, 54-83
+ * `_residual_rmsnorm_forward_kernel`, host side 325-349 and 749-778).
+ * x, residual, y, residual_out: [n_rows, hidden] in `dtype`; weight: [hidden]
+ * in `dtype`; rstd: [n_rows] float32.  residual and residual_out are both
+ * NULL (plain RMSNorm) or both set (y = rmsnorm(x + residual),
+ * residual_out = x + residual). */
+int tritium_rmsnorm_fwd(const void* x, const void* residual, const void* weight, void* y,
+                        void* residual_out, float* rstd, int64_t n_rows, int64_t hidden,
+                        float eps, int dtype, void* stream);
+
+/* Workspace bytes tritium_rmsnorm_bwd may use for these sizes. */
+size_t tritium_rmsnorm_bwd_workspace_size(int64_t n_rows, int64_t hidden);
+
+/* Backward of RMSNorm (tritium/ops/rmsnorm.py:105-280 kernels, host
+ * `_rmsnorm_backward_with_rstd` 519-574, standalone `rmsnorm_backward`
+ * 577-613 and the residual backward 700-734).
+ * rstd == NULL recomputes it from x (standalone rmsnorm_backward);
+ * dresidual != NULL is added to dx (residual backward, fused add);
+ * dweight == NULL skips dweight, else it receives [hidden] in `dtype`,
+ * reduced deterministically through `workspace`. */
+int tritium_rmsnorm_bwd(const void* dy, const void* x, const void* weight, const float* rstd,
+                        const void* dresidual, void* dx, void* dweight, void* workspace,
+                        size_t workspace_bytes, int64_t n_rows, int64_t hidden, float eps,
+                        int dtype, void* stream);
+
+/* ---- RoPE ------------------------------------------------------------------
+ * tritium.rope / tritium.rope_ and the RoPE backward (tritium/ops/rope.py:24-90
+ * `_rope_kernel`, host 201-291, autograd 294-360).
+ * q, k, q_out, k_out: [n_tokens, n_heads, head_dim] in `dtype` (q_out may equal
+ * q and k_out may equal k: in-place); cos/sin tables: [max_position,
+ * head_dim/2] in `table_dtype`; position_kind 0 = none (position = token),
+ * 1 = int32 ids, 2 = int64 ids; inverse != 0 applies the inverse rotation
+ * (the backward).  A position outside [0, max_position) yields NaN outputs
+ * for that token. */
+int tritium_rope(const void* q, const void* k, const void* cos_table, const void* sin_table,
+                 const void* position_ids, int position_kind, void* q_out, void* k_out,
+                 int64_t n_tokens, int64_t n_heads, int64_t head_dim, int64_t max_position,
+                 int64_t position_offset, int interleaved, int inverse, int dtype,
+                 int table_dtype, void* stream);
+
+/* ---- SwiGLU ----------------------------------------------------------------
+ * tritium.swiglu forward (tritium/ops/swiglu.py:21-35 `_swiglu_forward_kernel`,
+ * host 61-73): out = silu(x) * gate over n elements. */
+int tritium_swiglu_fwd(const void* x, const void* gate, void* out, int64_t n, int dtype,
+                       void* stream);
+
+/* tritium.swiglu_backward (tritium/ops/swiglu.py:38-58 `_swiglu_backward_kernel`,
+ * host 76-100). */
+int tritium_swiglu_bwd(const void* dy, const void* x, const void* gate, void* dx, void* dgate,
+                       int64_t n, int dtype, void* stream);
+
+/* ---- AdamW -----------------------------------------------------------------
+ * tritium.adamw_step (tritium/ops/adamw.py:20-54 `_adamw_step_kernel`, host
+ * 113-151): in-place update of one parameter tensor (param/grad in `dtype`,
+ * exp_avg/exp_avg_sq float32).  Bias corrections 1 - beta**step come from the
+ * caller (adamw.py:133-134). */
+int tritium_adamw_step(void* param, const void* grad, float* exp_avg, float* exp_avg_sq,
+                       int64_t n, float lr, float beta1, float beta2, float eps,
+                       float weight_decay, double bias_correction1, double bias_correction2,
+                       int dtype, void* stream);
+
+/* Elements one block of the multi-tensor kernel updates. */
+int64_t tritium_adamw_chunk_elements(void);
+
+/* Multi-tensor AdamW in ONE launch (replaces the per-parameter loop of
+ * helion.AdamW.step, helion/optim.py:50-70, each iteration of which calls
+ * adamw.py:113-151).  `table` is a DEVICE array of n_tensors * 7 int64:
+ * [param, grad, exp_avg, exp_avg_sq, numel, flags, first_chunk] where
+ * flags = dtype | (16-byte-aligned << 8) and first_chunk is the exclusive
+ * prefix sum of ceil(numel / tritium_adamw_chunk_elements()). */
+int tritium_adamw_step_multi(const int64_t* table, int n_tensors, int64_t total_chunks,
+                             float lr, float beta1, float beta2, float eps, float weight_decay,
+                             double bias_correction1, double bias_correction2, void* stream);
+
+/* ---- attention -------------------------------------------------------------
+ * Forward of tritium.attention (tritium/ops/attention.py:31-141
+ * `_attention_forward_kernel`, 144-217 decode kernel, host 284-396).
+ * q: [B, H, Tq, D], k/v: [B, Hkv, Tkv, D], o: like q, all in `dtype` with a
+ * unit head_dim stride and element strides strides[0..11] =
+ * {q_b, q_h, q_s, k_b, k_h, k_s, v_b, v_h, v_s, o_b, o_h, o_s} (host array).
+ * lse: [B, H, Tq] float32, natural-log logsumexp of the scaled scores.
+ * causal != 0 applies the top-left mask q_pos >= kv_pos; scale = D^-0.5.
+ * bf16/fp16 with D in {16, 32, 64, 128} run on MFMA, anything else on the
+ * SIMT path (D <= 1024). */
+int tritium_attention_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
+                          int64_t B, int64_t H, int64_t Hkv, int64_t Tq, int64_t Tkv, int64_t D,
+                          const int64_t* strides, int causal, int dtype, void* stream);
+
+/* Backward of tritium.attention (tritium/ops/attention.py:399-629 kernels,
+ * host `_attention_backward_impl` 632-702).  strides[0..23] = q, k, v, o,
+ * dout, dq, dk, dv (batch, head, seq each); dq/dk/dv are written in `dtype`
+ * with their own strides (no atomics); delta: [B*H*Tq] float32 workspace. */
+int tritium_attention_bwd(const void* dout, const void* q, const void* k, const void* v,
+                          const void* o, const float* lse, void* dq, void* dk, void* dv,
+                          float* delta, int64_t B, int64_t H, int64_t Hkv, int64_t Tq,
+                          int64_t Tkv, int64_t D, const int64_t* strides, int causal, int dtype,
+                          void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRITIUM_HIP_H_ */

@@ -1,0 +1,119 @@
+"""Attention HIP kernels (MFMA bf16/fp16, SIMT fp32) vs the float64 oracle,
+mirroring the reference's tests/tritium/test_attention.py (head dims, GQA,
+non-causal, KV-cache decode, autograd) plus the module's strided layout, ragged
+lengths, q_len != kv_len and head_dim 128.  Tolerance: bf16/fp16 max-abs 2e-2
+(+2e-2 relative, as tests/_utils.py:14-17), fp32 1e-5."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import helion_amd as tritium
+import oracle
+from _helpers import DTYPES, assert_close, np32, randn
+
+pytestmark = pytest.mark.gpu
+
+ATOL = {torch.float32: 1e-5, torch.float16: 2e-2, torch.bfloat16: 2e-2}
+
+
+def _check(dtype, b, h, hkv, tq, tkv, d, causal, seed=0, grads=True, layout="bhtd"):
+    def make(n, t, s):
+        if layout == "bthd":  # what helion.Attention passes: view(b, s, n, d).transpose(1, 2)
+            return randn((b, t, n, d), dtype, s).transpose(1, 2)
+        return randn((b, n, t, d), dtype, s)
+
+    q, k, v = make(h, tq, seed), make(hkv, tkv, seed + 1), make(hkv, tkv, seed + 2)
+    do = randn((b, h, tq, d), dtype, seed + 3)
+    qs, ks, vs = (t.detach().requires_grad_(grads) for t in (q, k, v))
+    o = tritium.attention(qs, ks, vs, is_causal=causal)
+    eo, lse = oracle.attention.forward(np32(q), np32(k), np32(v), causal)
+    tol = ATOL[dtype]
+    assert_close(o, eo, tol, tol, "o")
+    if not grads:
+        return
+    o.backward(do)
+    edq, edk, edv = oracle.attention.backward(np32(do), np32(q), np32(k), np32(v), lse, causal)
+    assert_close(qs.grad, edq, tol, tol, "dq")
+    assert_close(ks.grad, edk, tol, tol, "dk")
+    assert_close(vs.grad, edv, tol, tol, "dv")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("head_dim", [16, 32, 64, 128])
+@pytest.mark.parametrize(("batch", "n_heads", "seq"), [(1, 4, 64), (2, 8, 128)])
+def test_attention_forward_backward(dtype, head_dim, batch, n_heads, seq):
+    _check(dtype, batch, n_heads, n_heads, seq, seq, head_dim, True)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_attention_grouped_query(dtype):
+    _check(dtype, 2, 8, 2, 128, 128, 64, True, seed=4)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_ragged_and_unequal_lengths(dtype, causal):
+    _check(dtype, 1, 2, 2, 77, 77, 64, causal, seed=7)
+    _check(dtype, 1, 2, 1, 50, 200, 128, causal, seed=8)
+    _check(dtype, 1, 2, 2, 200, 50, 32, causal, seed=9)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_attention_non_causal(dtype):
+    _check(dtype, 1, 4, 4, 64, 64, 32, False, seed=10)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+def test_attention_module_layout_strided(dtype):
+    # the reference's strided-dq bug (attention.py:625-629 vs 645) must not recur
+    _check(dtype, 2, 4, 4, 96, 96, 64, True, seed=11, layout="bthd")
+    _check(dtype, 2, 4, 2, 130, 130, 128, True, seed=12, layout="bthd")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_attention_kv_cache_single_query(dtype):
+    b, h, kv_len, d = 2, 4, 64, 32
+    cache_k = randn((b, h, 80, d), dtype, 1)
+    cache_v = randn((b, h, 80, d), dtype, 2)
+    k, v = cache_k[:, :, :kv_len], cache_v[:, :, :kv_len]  # strided cache slices
+    q = k[:, :, -1:, :].contiguous()
+    o = tritium.attention(q, k, v, is_causal=False)
+    eo, _ = oracle.attention.forward(np32(q), np32(k), np32(v), False)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    assert_close(o, eo, tol, tol)
+
+
+def test_attention_large_head_bf16_t1024():
+    _check(torch.bfloat16, 1, 2, 2, 1024, 1024, 128, True, seed=13)
+
+
+def test_attention_invariants():
+    # T = 1 -> o = v; causal row 0 -> o[0] = v[0]; uniform v rows -> o = v
+    q = randn((1, 2, 1, 64), torch.bfloat16, 1)
+    k = randn((1, 2, 1, 64), torch.bfloat16, 2)
+    v = randn((1, 2, 1, 64), torch.bfloat16, 3)
+    assert torch.equal(tritium.attention(q, k, v), v)
+    q = randn((1, 2, 130, 64), torch.bfloat16, 4)
+    k = randn((1, 2, 130, 64), torch.bfloat16, 5)
+    v = randn((1, 2, 1, 64), torch.bfloat16, 6).expand(1, 2, 130, 64).contiguous()
+    o = tritium.attention(q, k, v)
+    assert_close(o, np32(v), 1e-2, 1e-2)
+    v2 = randn((1, 2, 130, 64), torch.bfloat16, 7)
+    o2 = tritium.attention(q, k, v2)
+    assert torch.equal(o2[:, :, 0], v2[:, :, 0])
+
+
+def test_attention_deterministic():
+    q = randn((1, 4, 256, 64), torch.bfloat16, 1).requires_grad_(True)
+    k = randn((1, 4, 256, 64), torch.bfloat16, 2).requires_grad_(True)
+    v = randn((1, 4, 256, 64), torch.bfloat16, 3).requires_grad_(True)
+    grads = []
+    for _ in range(2):
+        q.grad = k.grad = v.grad = None
+        tritium.attention(q, k, v).sum().backward()
+        grads.append((q.grad.clone(), k.grad.clone(), v.grad.clone()))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)

@@ -1,0 +1,163 @@
+"""RoPE, SwiGLU and AdamW HIP kernels vs the CPU oracle (parity), mirroring the
+reference's tests/tritium/test_{rope,swiglu,adamw}.py at north-star tolerances."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import helion_amd as tritium
+import oracle
+from _helpers import DTYPES, NAME, TOL, assert_close, np32, randn
+
+pytestmark = pytest.mark.gpu
+
+
+# ------------------------------------------------------------------- RoPE --
+def _tables(max_pos, head_dim, dtype=torch.float32):
+    c, s = oracle.rope.make_cos_sin(max_pos, head_dim)
+    return torch.from_numpy(c).to(dtype).cuda(), torch.from_numpy(s).to(dtype).cuda()
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("head_dim", [2, 6, 32, 64, 128])
+@pytest.mark.parametrize("layout", ["2d", "3d"])
+@pytest.mark.parametrize("interleaved", [False, True])
+def test_rope_forward(dtype, head_dim, layout, interleaved):
+    n_tokens, n_heads = 37, 3
+    shape = (n_tokens, head_dim) if layout == "2d" else (n_tokens, n_heads, head_dim)
+    q = randn(shape, dtype, 1)
+    k = randn(shape, dtype, 2)
+    cos, sin = _tables(64, head_dim)
+    qo, ko = tritium.rope(q, k, cos, sin, interleaved=interleaved)
+    eq, ek = oracle.rope.forward(np32(q), np32(k), np32(cos), np32(sin),
+                                 interleaved=interleaved, dtype=NAME[dtype])
+    rtol, atol = TOL[dtype]
+    assert_close(qo, eq, rtol, atol, "q")
+    assert_close(ko, ek, rtol, atol, "k")
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("pos_dtype", [torch.int32, torch.int64])
+@pytest.mark.parametrize("table_dtype", [torch.float32, torch.bfloat16])
+def test_rope_position_ids_offset_and_backward(dtype, pos_dtype, table_dtype):
+    b, s, h, d = 3, 50, 4, 128
+    q = randn((b * s, h, d), dtype, 3).requires_grad_(True)
+    k = randn((b * s, h, d), dtype, 4).requires_grad_(True)
+    cos, sin = _tables(64, d, table_dtype)
+    pos = torch.arange(s, device="cuda", dtype=pos_dtype).repeat(b)
+    qo, ko = tritium.rope(q, k, cos, sin, position_ids=pos, position_offset=7)
+    dqo, dko = randn((b * s, h, d), dtype, 5), randn((b * s, h, d), dtype, 6)
+    torch.autograd.backward((qo, ko), (dqo, dko))
+    npos = np32(pos).astype(np.int64)
+    kw = dict(position_ids=npos, position_offset=7, dtype=NAME[dtype])
+    eq, ek = oracle.rope.forward(np32(q), np32(k), np32(cos), np32(sin), **kw)
+    edq, edk = oracle.rope.backward(np32(dqo), np32(dko), np32(cos), np32(sin), **kw)
+    rtol, atol = TOL[dtype]
+    assert_close(qo, eq, rtol, atol, "q")
+    assert_close(ko, ek, rtol, atol, "k")
+    assert_close(q.grad, edq, rtol, atol, "dq")
+    assert_close(k.grad, edk, rtol, atol, "dk")
+
+
+def test_rope_inplace_matches_out_of_place():
+    q = randn((128, 32, 128), torch.bfloat16, 8)
+    k = randn((128, 32, 128), torch.bfloat16, 9)
+    cos, sin = _tables(128, 128)
+    qo, ko = tritium.rope(q, k, cos, sin)
+    tritium.rope_(q, k, cos, sin)
+    assert torch.equal(q, qo) and torch.equal(k, ko)
+
+
+def test_rope_out_of_range_position_is_nan_not_a_fault():
+    q = randn((4, 2, 16), torch.float32, 1)
+    cos, sin = _tables(8, 16)
+    pos = torch.tensor([0, 1, 100, 3], device="cuda")
+    qo, _ = tritium.rope(q, q, cos, sin, position_ids=pos)
+    assert torch.isnan(qo[2]).all() and not torch.isnan(qo[[0, 1, 3]]).any()
+    with pytest.raises(ValueError, match="positions"):
+        tritium.rope(q, q, cos, sin, position_offset=6)
+
+
+# ----------------------------------------------------------------- SwiGLU --
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n", [1, 7, 16, 1024, 8193, 1 << 20])
+def test_swiglu_forward_backward(dtype, n):
+    x = randn((n,), dtype, 1).requires_grad_(True)
+    g = randn((n,), dtype, 2).requires_grad_(True)
+    dy = randn((n,), dtype, 3)
+    out = tritium.swiglu(x, g)
+    out.backward(dy)
+    eo = oracle.swiglu.forward(np32(x), np32(g), NAME[dtype])
+    edx, edg = oracle.swiglu.backward(np32(dy), np32(x), np32(g), NAME[dtype])
+    rtol, atol = TOL[dtype]
+    assert_close(out, eo, rtol, atol, "out")
+    assert_close(x.grad, edx, rtol, atol, "dx")
+    assert_close(g.grad, edg, rtol, atol, "dgate")
+
+
+def test_swiglu_unaligned_views():
+    base = randn((4099,), torch.bfloat16, 4)
+    x, g = base[1:4097], base[2:4098]
+    out = tritium.swiglu(x, g)
+    assert_close(out, oracle.swiglu.forward(np32(x), np32(g), "bf16"), 3e-2, 3e-2)
+    dx, dg = tritium.swiglu_backward(x, x, g)
+    edx, edg = oracle.swiglu.backward(np32(x), np32(x), np32(g), "bf16")
+    assert_close(dx, edx, 3e-2, 3e-2)
+    assert_close(dg, edg, 3e-2, 3e-2)
+
+
+# ------------------------------------------------------------------ AdamW --
+@pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize("n", [1, 128, 4096, 10007])
+def test_adamw_step(dtype, n):
+    p = randn((n,), dtype, 1)
+    g = randn((n,), dtype, 2)
+    m = torch.zeros(n, device="cuda")
+    v = torch.zeros(n, device="cuda")
+    hp = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+    ep, em, ev = np32(p), np32(m), np32(v)
+    for step in (1, 2, 3):
+        tritium.adamw_step(p, g, m, v, step=step, **hp)
+        ep, em, ev = oracle.adamw.step(ep, np32(g), em, ev, step=step, dtype=NAME[dtype], **hp)
+    rtol, atol = TOL[dtype]
+    assert_close(p, ep, rtol, atol, "param")
+    assert_close(m, em, 1e-5, 1e-7, "exp_avg")
+    assert_close(v, ev, 1e-5, 1e-9, "exp_avg_sq")
+
+
+def test_adamw_multi_matches_single_and_oracle():
+    shapes = [(3,), (50257, 8), (768,), (5, 7), (4096,), (1,), (0,), (3072, 3)]
+    dtypes = [torch.float32, torch.float32, torch.bfloat16, torch.float16,
+              torch.float32, torch.float32, torch.float32, torch.float32]
+    params = [randn(s, d, i) for i, (s, d) in enumerate(zip(shapes, dtypes))]
+    grads = [randn(s, d, 100 + i) * 1e-2 for i, (s, d) in enumerate(zip(shapes, dtypes))]
+    ms = [torch.zeros(s, device="cuda") for s in shapes]
+    vs = [torch.zeros(s, device="cuda") for s in shapes]
+    ref_p = [p.clone() for p in params]
+    ref_m = [m.clone() for m in ms]
+    ref_v = [v.clone() for v in vs]
+    hp = dict(lr=6e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+    for step in (1, 2):
+        tritium.adamw_step_multi(params, grads, ms, vs, step=step, **hp)
+        for p, g, m, v in zip(ref_p, grads, ref_m, ref_v):
+            tritium.adamw_step(p, g, m, v, step=step, **hp)
+    for a, b in zip(params + ms + vs, ref_p + ref_m + ref_v):
+        assert torch.equal(a, b)
+    ep, em, ev = oracle.adamw.step(np32(params[1]), np32(grads[1]),
+                                   np32(ms[1]), np32(vs[1]), step=3, **hp)
+    tritium.adamw_step_multi(params, grads, ms, vs, step=3, **hp)
+    assert_close(params[1], ep, 1e-5, 1e-5)
+
+
+def test_adamw_step1_closed_form():
+    # from zero moments, step 1: p1 = p*(1 - lr*wd) - lr * g / (|g| + eps)
+    n = 4096
+    p = randn((n,), torch.float32, 1)
+    g = randn((n,), torch.float32, 2)
+    m, v = torch.zeros(n, device="cuda"), torch.zeros(n, device="cuda")
+    lr, wd, eps = 1e-3, 0.1, 1e-8
+    expect = np32(p) * (1 - lr * wd) - lr * np32(g) / (np.abs(np32(g)) + eps)
+    tritium.adamw_step(p, g, m, v, lr=lr, beta1=0.9, beta2=0.95, eps=eps, weight_decay=wd, step=1)
+    assert_close(p, expect, 1e-5, 1e-6)
