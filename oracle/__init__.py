@@ -22,7 +22,7 @@ docstring of every module; the CPU test-suite (``tests/test_oracle_*.py``)
 runs those checks.
 """
 
-from . import adamw, attention, linear_ce, numerics, rmsnorm, rope, swiglu
+from . import adamw, attention, linear_ce, numerics, rmsnorm, rope, swiglu, torch_ref
 
 __all__ = [
     "adamw",
@@ -32,4 +32,5 @@ __all__ = [
     "rmsnorm",
     "rope",
     "swiglu",
+    "torch_ref",
 ]
