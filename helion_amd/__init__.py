@@ -17,6 +17,7 @@ import torch  # noqa: F401  (must be loaded before libtritium_hip.so)
 
 from .adamw import adamw_step, adamw_step_multi
 from .attention import attention
+from .linear_ce import linear_cross_entropy, linear_cross_entropy_backward
 from .rmsnorm import residual_rmsnorm, rmsnorm, rmsnorm_backward
 from .rope import rope, rope_
 from .swiglu import swiglu, swiglu_backward
@@ -28,6 +29,8 @@ __all__ = [
     "adamw_step",
     "adamw_step_multi",
     "attention",
+    "linear_cross_entropy",
+    "linear_cross_entropy_backward",
     "residual_rmsnorm",
     "rmsnorm",
     "rmsnorm_backward",

@@ -67,6 +67,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P,
          _I32, _I32, _P],
     ),
+    "tritium_linear_ce_fwd_workspace_size": (_SZ, [_I64, _I64]),
+    "tritium_linear_ce_fwd": (
+        _I32,
+        [_P, _P, _P, _I32, _I64, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I32, _P],
+    ),
+    "tritium_linear_ce_bwd_workspace_size": (_SZ, [_I64, _I64, _I64, _I32, _I32, _I32, _I64]),
+    "tritium_linear_ce_bwd": (
+        _I32,
+        [_P, _P, _P, _P, _I32, _I64, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I32, _P],
+    ),
     "tritium_adamw_step_multi": (
         _I32,
         [_P, _I32, _I64, _F32, _F32, _F32, _F32, _F32, _F64, _F64, _P],

@@ -1,0 +1,623 @@
+// Fused linear + cross-entropy forward and backward for gfx950.
+//
+// Reference arithmetic: alkinun/helion tritium/ops/cross_entropy.py:219-293
+// (forward: logits = hidden @ weight^T with fp32 accumulation, per-row
+// lse = max + ln(sum exp(logit - max)), nll = lse - logit[target], mean) and
+// 103-131 + 937-957 (backward: G = (softmax - onehot) * grad_out / count,
+// dhidden = G @ weight, dweight = G^T @ hidden).  ignore_index follows
+// torch's F.cross_entropy: ignored rows add nothing and the mean divides by
+// the number of non-ignored rows.
+//
+// Forward -- the logits never reach HBM:
+//   lce_fwd_kernel     S^T = W H^T tile by tile (gemm_nt.h core, vocab along
+//                      the tile's rows, tokens along its columns); epilogue in
+//                      registers: per (vocab block, token) max and sum of
+//                      exp(logit - max), and the target logit (written by the
+//                      one lane whose row is the target);
+//   lce_fwd_rows       per token: combine the vocab-block partials online into
+//                      lse, nll; per-block partial sums of nll and counts;
+//   lce_fwd_finalize   one block: loss = sum(nll) / count in a fixed order.
+// Backward, per vocab chunk of Vc rows (bounded G memory):
+//   lce_g_kernel       recompute S^T for the chunk, epilogue
+//                      G = (exp(S - lse) - onehot) * grad_out / count (0 for
+//                      ignored rows), written as G^T [Vc, N] and G [N, Vc];
+//   dH (+)= G W_c      NT GEMM with B = W^T (made once per backward);
+//   dW_c = G^T H       NT GEMM with B = H^T, the full token reduction inside
+//                      one GEMM, stored once in the weight dtype.
+// All reductions are in a fixed order: results are bitwise reproducible.
+#include <math.h>
+
+#include <type_traits>
+
+#include "common.h"
+#include "gemm_nt.h"
+#include "../../include/tritium_hip.h"
+
+namespace tri {
+namespace {
+
+using gemm::Acc;
+using gemm::kBM;
+using gemm::kBN;
+using gemm::kMT;
+using gemm::kNT;
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kRowsBlock = 256;        // threads of lce_fwd_rows
+constexpr int kRowsSplit = 8;          // threads per token in lce_fwd_rows
+constexpr int64_t kGBudget = (int64_t)1 << 30;  // bytes for G and G^T of one chunk
+
+template <typename TT>
+__device__ __forceinline__ int64_t load_target(const TT* t, int64_t n) {
+  return (int64_t)t[n];
+}
+
+// ------------------------------------------------------------- forward ----
+struct FwdArgs {
+  const void* hidden;  // [N, D]
+  const void* weight;  // [V, D]
+  const void* target;  // [N] int32 / int64
+  float* pmax;         // [tiles_v, N]
+  float* psum;         // [tiles_v, N]
+  float* tlogit;       // [N]
+  int64_t N, D, V, ld;
+  int tiles_v, tiles_n;
+};
+
+template <typename T, typename TT>
+__global__ void __launch_bounds__(gemm::kThreads)
+lce_fwd_kernel(FwdArgs a) {
+  __shared__ gemm::Smem<T> sm;
+  __shared__ float red[2][kBN];
+  int tm, tn;
+  gemm::tile_of(blockIdx.x, gridDim.x, a.tiles_v, a.tiles_n, tm, tn);
+  gemm::Problem p{a.weight, a.hidden, a.ld, a.ld, a.V, a.N, a.D};
+  Acc acc;
+  gemm::mainloop<T>(p, tm, tn, sm, acc);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t v0 = (int64_t)tm * kBM, n0 = (int64_t)tn * kBN;
+  const TT* target = (const TT*)a.target;
+
+  float mx[kNT];
+#pragma unroll
+  for (int j = 0; j < kNT; ++j) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < kMT; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (v0 + gemm::acc_row(wm, i, r, g) < a.V) m = fmaxf(m, acc.t[i][j][r]);
+    m = fmaxf(m, __shfl_xor(m, 32, 64));
+    if (g == 0) red[wm][gemm::acc_col(wn, j, l32)] = m;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kNT; ++j) {
+    const int col = gemm::acc_col(wn, j, l32);
+    mx[j] = fmaxf(red[0][col], red[1][col]);
+  }
+  __syncthreads();
+#pragma unroll
+  for (int j = 0; j < kNT; ++j) {
+    const int col = gemm::acc_col(wn, j, l32);
+    const int64_t n = n0 + col;
+    const float ms = mx[j] * kLog2e;
+    float s = 0.f;
+#pragma unroll
+    for (int i = 0; i < kMT; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r)
+        if (v0 + gemm::acc_row(wm, i, r, g) < a.V) s += exp2f(acc.t[i][j][r] * kLog2e - ms);
+    s += __shfl_xor(s, 32, 64);
+    if (g == 0) red[wm][col] = s;
+    // the target logit: written by the single lane that holds its row
+    if (n < a.N) {
+      const int64_t t = load_target(target, n);
+      const int64_t dt = t - v0 - wm * 128;
+      if (t < a.V && dt >= 0 && dt < 128) {
+#pragma unroll
+        for (int i = 0; i < kMT; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (gemm::acc_row(0, i, r, g) == dt) a.tlogit[n] = acc.t[i][j][r];
+      }
+    }
+  }
+  __syncthreads();
+  if (wm == 0 && g == 0) {
+#pragma unroll
+    for (int j = 0; j < kNT; ++j) {
+      const int col = gemm::acc_col(wn, j, l32);
+      const int64_t n = n0 + col;
+      if (n < a.N) {
+        a.pmax[(int64_t)tm * a.N + n] = mx[j];
+        a.psum[(int64_t)tm * a.N + n] = red[0][col] + red[1][col];
+      }
+    }
+  }
+}
+
+__global__ void __launch_bounds__(256)
+fill_f32(float* __restrict__ p, int64_t n, float value) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = value;
+}
+
+// Combine (max, sum) pairs: sum is relative to its max.
+__device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2) {
+  const float mn = fmaxf(m, m2);
+  if (mn == -INFINITY) return;
+  s = s * exp2f((m - mn) * kLog2e) + s2 * exp2f((m2 - mn) * kLog2e);
+  m = mn;
+}
+
+// kRowsSplit threads per token; the partial vocab blocks b = k, k+8, ... of
+// one thread are merged online, then the 8 threads merge in a fixed order.
+template <typename TT>
+__global__ void __launch_bounds__(kRowsBlock)
+lce_fwd_rows(const float* __restrict__ pmax, const float* __restrict__ psum,
+             const float* __restrict__ tlogit, const TT* __restrict__ target,
+             int64_t ignore_index, float* __restrict__ lse, double* __restrict__ block_nll,
+             int* __restrict__ block_cnt, int64_t N, int tiles_v) {
+  __shared__ float sm_m[kRowsBlock], sm_s[kRowsBlock];
+  __shared__ double sm_nll[kRowsBlock / kRowsSplit];
+  __shared__ int sm_cnt[kRowsBlock / kRowsSplit];
+  const int tok = threadIdx.x / kRowsSplit, part = threadIdx.x % kRowsSplit;
+  const int64_t n = (int64_t)blockIdx.x * (kRowsBlock / kRowsSplit) + tok;
+  float m = -INFINITY, s = 0.f;
+  if (n < N) {
+    for (int b = part; b < tiles_v; b += kRowsSplit)
+      lse_merge(m, s, pmax[(int64_t)b * N + n], psum[(int64_t)b * N + n]);
+  }
+  sm_m[threadIdx.x] = m;
+  sm_s[threadIdx.x] = s;
+  __syncthreads();
+  if (part == 0) {
+    double nll = 0.0;
+    int cnt = 0;
+    if (n < N) {
+      for (int k = 1; k < kRowsSplit; ++k) lse_merge(m, s, sm_m[threadIdx.x + k], sm_s[threadIdx.x + k]);
+      const float l = m + logf(s);
+      lse[n] = l;
+      const int64_t t = load_target(target, n);
+      if (t != ignore_index) {
+        nll = (double)(l - tlogit[n]);
+        cnt = 1;
+      }
+    }
+    sm_nll[tok] = nll;
+    sm_cnt[tok] = cnt;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    double acc = 0.0;
+    int cnt = 0;
+    for (int k = 0; k < kRowsBlock / kRowsSplit; ++k) {
+      acc += sm_nll[k];
+      cnt += sm_cnt[k];
+    }
+    block_nll[blockIdx.x] = acc;
+    block_cnt[blockIdx.x] = cnt;
+  }
+}
+
+__global__ void __launch_bounds__(256)
+lce_fwd_finalize(const double* __restrict__ block_nll, const int* __restrict__ block_cnt,
+                 int n_blocks, float* __restrict__ loss, float* __restrict__ n_valid) {
+  __shared__ double sn[256];
+  __shared__ long long sc[256];
+  double acc = 0.0;
+  long long cnt = 0;
+  for (int b = threadIdx.x; b < n_blocks; b += 256) {
+    acc += block_nll[b];
+    cnt += block_cnt[b];
+  }
+  sn[threadIdx.x] = acc;
+  sc[threadIdx.x] = cnt;
+  __syncthreads();
+  for (int w = 128; w > 0; w >>= 1) {
+    if (threadIdx.x < w) {
+      sn[threadIdx.x] += sn[threadIdx.x + w];
+      sc[threadIdx.x] += sc[threadIdx.x + w];
+    }
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) {
+    // mean over non-ignored rows; no valid row gives 0/0 = NaN (torch semantics)
+    loss[0] = (float)(sn[0] / (double)sc[0]);
+    if (n_valid != nullptr) n_valid[0] = (float)sc[0];
+  }
+}
+
+// ------------------------------------------------------------ backward ----
+template <typename TT>
+__global__ void __launch_bounds__(1024)
+lce_count_valid(const TT* __restrict__ target, int64_t N, int64_t ignore_index,
+                float* __restrict__ n_valid) {
+  __shared__ int red[1024];
+  int c = 0;
+  for (int64_t n = threadIdx.x; n < N; n += 1024) c += (load_target(target, n) != ignore_index);
+  red[threadIdx.x] = c;
+  __syncthreads();
+  for (int w = 512; w > 0; w >>= 1) {
+    if (threadIdx.x < w) red[threadIdx.x] += red[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) n_valid[0] = (float)red[0];
+}
+
+struct GArgs {
+  const void* hidden;   // [N, D]
+  const void* weight;   // rows [vc0, vc0 + Vc) of [V, D]
+  const void* target;   // [N]
+  const float* lse;     // [N]
+  const float* grad_out;
+  const float* n_valid;
+  void* gt;             // [Vc, ld_gt]   (may be null)
+  void* gm;             // [N, ld_g]     (may be null)
+  int64_t N, D, Vc, ld, ld_gt, ld_g, vc0, ignore_index;
+  int tiles_v, tiles_n;
+};
+
+template <typename T, typename TT>
+__global__ void __launch_bounds__(gemm::kThreads)
+lce_g_kernel(GArgs a) {
+  __shared__ gemm::Smem<T> sm;
+  int tm, tn;
+  gemm::tile_of(blockIdx.x, gridDim.x, a.tiles_v, a.tiles_n, tm, tn);
+  gemm::Problem p{a.weight, a.hidden, a.ld, a.ld, a.Vc, a.N, a.D};
+  Acc acc;
+  gemm::mainloop<T>(p, tm, tn, sm, acc);
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t v0 = (int64_t)tm * kBM, n0 = (int64_t)tn * kBN;
+  const float coef_all = a.grad_out[0] / a.n_valid[0];
+  T* gt = (T*)a.gt;
+  T* gm = (T*)a.gm;
+#pragma unroll
+  for (int j = 0; j < kNT; ++j) {
+    const int64_t n = n0 + gemm::acc_col(wn, j, l32);
+    if (n >= a.N) continue;
+    const float l2 = a.lse[n] * kLog2e;
+    const int64_t t = load_target((const TT*)a.target, n);
+    const float coef = (t == a.ignore_index) ? 0.f : coef_all;
+    const int64_t tl = t - a.vc0;  // target row inside this chunk
+#pragma unroll
+    for (int i = 0; i < kMT; ++i) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        float gv[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * rr + e;
+          const int64_t v = v0 + gemm::acc_row(wm, i, r, g);
+          const float pr = exp2f(acc.t[i][j][r] * kLog2e - l2);
+          gv[e] = (pr - (v == tl ? 1.f : 0.f)) * coef;
+        }
+        const int64_t vb = v0 + gemm::acc_row(wm, i, 4 * rr, g);  // 4 consecutive rows
+        if (gt != nullptr) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (vb + e < a.Vc) gt[(vb + e) * a.ld_gt + n] = from_f32<T>(gv[e]);
+        }
+        if (gm != nullptr) {
+          T* dst = gm + n * a.ld_g + vb;
+          if (vb + 4 <= a.Vc) {
+            store_f32<T, 4>(dst, gv);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (vb + e < a.Vc) dst[e] = from_f32<T>(gv[e]);
+          }
+        }
+      }
+    }
+  }
+}
+
+// Plain GEMM: out[m, n] = (acc_in[m, n] if acc_in) + (A B^T)[m, n].
+template <typename T, typename OT>
+__global__ void __launch_bounds__(gemm::kThreads)
+gemm_store_kernel(gemm::Problem p, const float* acc_in, OT* out, int64_t ldc, int tiles_m,
+                  int tiles_n) {
+  __shared__ gemm::Smem<T> sm;
+  int tm, tn;
+  gemm::tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  Acc acc;
+  gemm::mainloop<T>(p, tm, tn, sm, acc);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int64_t m0 = (int64_t)tm * kBM, n0 = (int64_t)tn * kBN;
+#pragma unroll
+  for (int j = 0; j < kNT; ++j) {
+    const int64_t n = n0 + gemm::acc_col(wn, j, l32);
+    if (n >= p.N) continue;
+#pragma unroll
+    for (int i = 0; i < kMT; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = m0 + gemm::acc_row(wm, i, r, g);
+        if (m < p.M) {
+          float v = acc.t[i][j][r];
+          if (acc_in != nullptr) v += acc_in[m * ldc + n];
+          out[m * ldc + n] = from_f32<OT>(v);
+        }
+      }
+  }
+}
+
+// out[c, r] = in[r, c] for an R x C matrix (64 x 64 tiles through LDS).
+template <typename E>
+__global__ void __launch_bounds__(256)
+transpose_kernel(const E* __restrict__ in, int64_t ld_in, E* __restrict__ out, int64_t ld_out,
+                 int64_t R, int64_t C) {
+  __shared__ E tile[64][65];
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
+  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int64_t r = r0 + ty + 4 * k, c = c0 + tx;
+    if (r < R && c < C) tile[ty + 4 * k][tx] = in[r * ld_in + c];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int64_t c = c0 + ty + 4 * k, r = r0 + tx;
+    if (r < R && c < C) out[c * ld_out + r] = tile[tx][ty + 4 * k];
+  }
+}
+
+// ----------------------------------------------------------- host side ----
+int64_t round_up(int64_t x, int64_t m) { return cdiv(x, m) * m; }
+
+struct FwdLayout {
+  int tiles_v, tiles_n, rows_blocks;
+  size_t pmax, psum, tlogit, bnll, bcnt, total;
+};
+
+FwdLayout fwd_layout(int64_t N, int64_t V) {
+  FwdLayout L;
+  L.tiles_v = (int)cdiv(V, kBM);
+  L.tiles_n = (int)cdiv(N, kBN);
+  L.rows_blocks = (int)cdiv(N, kRowsBlock / kRowsSplit);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += (size_t)round_up((int64_t)bytes, 256);
+    return at;
+  };
+  L.pmax = take((size_t)L.tiles_v * N * 4);
+  L.psum = take((size_t)L.tiles_v * N * 4);
+  L.tlogit = take((size_t)N * 4);
+  L.bnll = take((size_t)L.rows_blocks * 8);
+  L.bcnt = take((size_t)L.rows_blocks * 4);
+  L.total = off;
+  return L;
+}
+
+struct BwdLayout {
+  int64_t chunk, n_chunks, ld_wt, ld_ht, ld_g;
+  size_t n_valid, wt, ht, gm, gt, dh_acc, total;
+};
+
+BwdLayout bwd_layout(int64_t N, int64_t D, int64_t V, int esz, bool need_dh, bool need_dw,
+                     int64_t chunk_rows) {
+  BwdLayout L;
+  const int64_t vpad = round_up(V, kBM);
+  int64_t chunk = chunk_rows > 0 ? round_up(chunk_rows, kBM)
+                                 : (kGBudget / std::max<int64_t>(1, 2 * N * esz)) / kBM * kBM;
+  chunk = std::max<int64_t>(kBM, std::min<int64_t>(chunk, vpad));
+  L.chunk = chunk;
+  L.n_chunks = cdiv(V, chunk);
+  L.ld_wt = round_up(V, 8);
+  L.ld_ht = round_up(N, 8);
+  L.ld_g = round_up(chunk, 8);
+  size_t off = 0;
+  auto take = [&](size_t bytes) {
+    const size_t at = off;
+    off += (size_t)round_up((int64_t)bytes, 256);
+    return at;
+  };
+  L.n_valid = take(4);
+  L.wt = need_dh ? take((size_t)D * L.ld_wt * esz) : 0;
+  L.ht = need_dw ? take((size_t)D * L.ld_ht * esz) : 0;
+  L.gm = need_dh ? take((size_t)N * L.ld_g * esz) : 0;
+  L.gt = need_dw ? take((size_t)chunk * L.ld_ht * esz) : 0;
+  L.dh_acc = (need_dh && L.n_chunks > 1) ? take((size_t)N * D * 4) : 0;
+  L.total = off;
+  return L;
+}
+
+int check_sizes(int64_t N, int64_t D, int64_t V, int dtype) {
+  if (N < 0 || D <= 0 || V <= 0)
+    return fail(TRI_EINVAL, "linear_ce: bad shape N=%lld D=%lld V=%lld", (long long)N,
+                (long long)D, (long long)V);
+  const int ve = dtype == kF32 ? 4 : 8;
+  if (D % ve != 0)
+    return fail(TRI_EINVAL, "linear_ce: hidden_size %lld must be a multiple of %d", (long long)D, ve);
+  if (cdiv(V, kBM) * cdiv(N, kBN) >= ((int64_t)1 << 31) || N >= ((int64_t)1 << 31))
+    return fail(TRI_EINVAL, "linear_ce: problem too large");
+  return TRI_OK;
+}
+
+template <typename T>
+int gemm_store(const gemm::Problem& p, const float* acc_in, void* out, bool out_f32, int64_t ldc,
+               hipStream_t st) {
+  const int tiles_m = (int)cdiv(p.M, kBM), tiles_n = (int)cdiv(p.N, kBN);
+  const unsigned blocks = (unsigned)((int64_t)tiles_m * tiles_n);
+  if (out_f32)
+    gemm_store_kernel<T, float><<<blocks, gemm::kThreads, 0, st>>>(p, acc_in, (float*)out, ldc,
+                                                                   tiles_m, tiles_n);
+  else
+    gemm_store_kernel<T, T><<<blocks, gemm::kThreads, 0, st>>>(p, acc_in, (T*)out, ldc, tiles_m,
+                                                               tiles_n);
+  return check_launch("linear_ce gemm");
+}
+
+template <typename E>
+int transpose(const void* in, int64_t ld_in, void* out, int64_t ld_out, int64_t R, int64_t C,
+              hipStream_t st) {
+  const dim3 grid((unsigned)cdiv(C, 64), (unsigned)cdiv(R, 64));
+  transpose_kernel<E><<<grid, 256, 0, st>>>((const E*)in, ld_in, (E*)out, ld_out, R, C);
+  return check_launch("linear_ce transpose");
+}
+
+template <typename T, typename TT>
+int fwd_impl(const void* hidden, const void* weight, const void* target, int64_t ignore_index,
+             float* loss, float* lse, float* n_valid, void* ws, size_t ws_bytes, int64_t N,
+             int64_t D, int64_t V, hipStream_t st) {
+  const FwdLayout L = fwd_layout(N, V);
+  if (ws_bytes < L.total) return fail(TRI_EINVAL, "linear_ce forward: workspace too small");
+  char* w = (char*)ws;
+  FwdArgs a;
+  a.hidden = hidden; a.weight = weight; a.target = target;
+  a.pmax = (float*)(w + L.pmax);
+  a.psum = (float*)(w + L.psum);
+  a.tlogit = (float*)(w + L.tlogit);
+  a.N = N; a.D = D; a.V = V; a.ld = D;
+  a.tiles_v = L.tiles_v; a.tiles_n = L.tiles_n;
+  // a target outside [0, V) that is not ignore_index leaves NaN here (-> NaN loss);
+  // a fill kernel rather than a memset node, so the call can be graph-captured
+  fill_f32<<<(unsigned)cdiv(N, 256), 256, 0, st>>>(a.tlogit, N, __builtin_nanf(""));
+  if (int e = check_launch("linear_ce forward fill")) return e;
+  lce_fwd_kernel<T, TT><<<(unsigned)((int64_t)L.tiles_v * L.tiles_n), gemm::kThreads, 0, st>>>(a);
+  if (int e = check_launch("linear_ce forward gemm")) return e;
+  lce_fwd_rows<TT><<<(unsigned)L.rows_blocks, kRowsBlock, 0, st>>>(
+      a.pmax, a.psum, a.tlogit, (const TT*)target, ignore_index, lse, (double*)(w + L.bnll),
+      (int*)(w + L.bcnt), N, L.tiles_v);
+  if (int e = check_launch("linear_ce forward rows")) return e;
+  lce_fwd_finalize<<<1, 256, 0, st>>>((const double*)(w + L.bnll), (const int*)(w + L.bcnt),
+                                      L.rows_blocks, loss, n_valid);
+  return check_launch("linear_ce forward finalize");
+}
+
+template <typename T, typename TT>
+int bwd_impl(const float* grad_out, const void* hidden, const void* weight, const void* target,
+             int64_t ignore_index, const float* lse, void* dhidden, void* dweight, void* ws,
+             size_t ws_bytes, int64_t N, int64_t D, int64_t V, int64_t chunk_rows,
+             hipStream_t st) {
+  const bool need_dh = dhidden != nullptr, need_dw = dweight != nullptr;
+  if (!need_dh && !need_dw) return TRI_OK;
+  const BwdLayout L = bwd_layout(N, D, V, (int)sizeof(T), need_dh, need_dw, chunk_rows);
+  if (ws_bytes < L.total) return fail(TRI_EINVAL, "linear_ce backward: workspace too small");
+  char* w = (char*)ws;
+  float* n_valid = (float*)(w + L.n_valid);
+  lce_count_valid<TT><<<1, 1024, 0, st>>>((const TT*)target, N, ignore_index, n_valid);
+  if (int e = check_launch("linear_ce count")) return e;
+  typedef typename std::conditional<sizeof(T) == 4, uint32_t, uint16_t>::type E;
+  T* wt = need_dh ? (T*)(w + L.wt) : nullptr;
+  T* ht = need_dw ? (T*)(w + L.ht) : nullptr;
+  T* gm = need_dh ? (T*)(w + L.gm) : nullptr;
+  T* gt = need_dw ? (T*)(w + L.gt) : nullptr;
+  float* dh_acc = L.dh_acc ? (float*)(w + L.dh_acc) : nullptr;
+  if (need_dh) {
+    if (int e = transpose<E>(weight, D, wt, L.ld_wt, V, D, st)) return e;
+  }
+  if (need_dw) {
+    if (int e = transpose<E>(hidden, D, ht, L.ld_ht, N, D, st)) return e;
+  }
+  for (int64_t c = 0; c < L.n_chunks; ++c) {
+    const int64_t vc0 = c * L.chunk;
+    const int64_t vc = std::min<int64_t>(L.chunk, V - vc0);
+    GArgs ga;
+    ga.hidden = hidden;
+    ga.weight = (const T*)weight + vc0 * D;
+    ga.target = target;
+    ga.lse = lse;
+    ga.grad_out = grad_out;
+    ga.n_valid = n_valid;
+    ga.gt = gt;
+    ga.gm = gm;
+    ga.N = N; ga.D = D; ga.Vc = vc; ga.ld = D;
+    ga.ld_gt = L.ld_ht; ga.ld_g = L.ld_g; ga.vc0 = vc0; ga.ignore_index = ignore_index;
+    ga.tiles_v = (int)cdiv(vc, kBM);
+    ga.tiles_n = (int)cdiv(N, kBN);
+    lce_g_kernel<T, TT><<<(unsigned)((int64_t)ga.tiles_v * ga.tiles_n), gemm::kThreads, 0, st>>>(ga);
+    if (int e = check_launch("linear_ce gradient tile")) return e;
+    if (need_dh) {
+      // dH[N, D] (+)= G[N, vc] * W[vc0:vc0+vc, :]  ==  A = G, B = W^T[:, vc0:]
+      gemm::Problem p{gm, wt + vc0, L.ld_g, L.ld_wt, N, D, vc};
+      const bool last = c + 1 == L.n_chunks;
+      const float* in = c > 0 ? dh_acc : nullptr;
+      if (int e = last ? gemm_store<T>(p, in, dhidden, false, D, st)
+                       : gemm_store<T>(p, in, dh_acc, true, D, st))
+        return e;
+    }
+    if (need_dw) {
+      // dW[vc0:vc0+vc, :] = G^T[vc, N] * H[N, D]  ==  A = G^T, B = H^T
+      gemm::Problem p{gt, ht, L.ld_ht, L.ld_ht, vc, D, N};
+      if (int e = gemm_store<T>(p, nullptr, (T*)dweight + vc0 * D, false, D, st)) return e;
+    }
+  }
+  return TRI_OK;
+}
+
+#define TRI_DISPATCH_TARGET(kind, TT, ...)                                         \
+  do {                                                                             \
+    if ((kind) == 1) { typedef int32_t TT; __VA_ARGS__; }                          \
+    else if ((kind) == 2) { typedef int64_t TT; __VA_ARGS__; }                     \
+    else return fail(TRI_EINVAL, "linear_ce: bad target kind %d", (int)(kind));    \
+  } while (0)
+
+}  // namespace
+}  // namespace tri
+
+using namespace tri;
+
+extern "C" size_t tritium_linear_ce_fwd_workspace_size(int64_t n_rows, int64_t vocab) {
+  if (n_rows <= 0 || vocab <= 0) return 0;
+  return fwd_layout(n_rows, vocab).total;
+}
+
+extern "C" int tritium_linear_ce_fwd(const void* hidden, const void* weight, const void* target,
+                                     int target_kind, int64_t ignore_index, float* loss,
+                                     float* lse, float* n_valid, void* workspace,
+                                     size_t workspace_bytes, int64_t n_rows, int64_t hidden_size,
+                                     int64_t vocab, int dtype, void* stream) {
+  if (int e = check_sizes(n_rows, hidden_size, vocab, dtype)) return e;
+  if (n_rows == 0) return TRI_OK;
+  if (!aligned16(hidden) || !aligned16(weight))
+    return fail(TRI_EINVAL, "linear_ce: hidden and weight must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  TRI_DISPATCH_TARGET(target_kind, TT,
+    TRI_DISPATCH_FLOAT(dtype, T,
+      return fwd_impl<T, TT>(hidden, weight, target, ignore_index, loss, lse, n_valid, workspace,
+                             workspace_bytes, n_rows, hidden_size, vocab, st)));
+  return TRI_OK;
+}
+
+extern "C" size_t tritium_linear_ce_bwd_workspace_size(int64_t n_rows, int64_t hidden_size,
+                                                       int64_t vocab, int dtype,
+                                                       int need_dhidden, int need_dweight,
+                                                       int64_t chunk_rows) {
+  if (n_rows <= 0 || vocab <= 0 || hidden_size <= 0) return 0;
+  return bwd_layout(n_rows, hidden_size, vocab, dtype == kF32 ? 4 : 2, need_dhidden != 0,
+                    need_dweight != 0, chunk_rows)
+      .total;
+}
+
+extern "C" int tritium_linear_ce_bwd(const float* grad_out, const void* hidden, const void* weight,
+                                     const void* target, int target_kind, int64_t ignore_index,
+                                     const float* lse, void* dhidden, void* dweight,
+                                     void* workspace, size_t workspace_bytes, int64_t n_rows,
+                                     int64_t hidden_size, int64_t vocab, int64_t chunk_rows,
+                                     int dtype, void* stream) {
+  if (int e = check_sizes(n_rows, hidden_size, vocab, dtype)) return e;
+  if (n_rows == 0) return TRI_OK;
+  if (!aligned16(hidden) || !aligned16(weight) || (dhidden && !aligned16(dhidden)) ||
+      (dweight && !aligned16(dweight)) || !aligned16(workspace))
+    return fail(TRI_EINVAL, "linear_ce: buffers must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  TRI_DISPATCH_TARGET(target_kind, TT,
+    TRI_DISPATCH_FLOAT(dtype, T,
+      return bwd_impl<T, TT>(grad_out, hidden, weight, target, ignore_index, lse, dhidden,
+                             dweight, workspace, workspace_bytes, n_rows, hidden_size, vocab,
+                             chunk_rows, st)));
+  return TRI_OK;
+}

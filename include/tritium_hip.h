@@ -133,6 +133,37 @@ int tritium_attention_bwd(const void* dout, const void* q, const void* k, const 
                           int64_t Tkv, int64_t D, const int64_t* strides, int causal, int dtype,
                           void* stream);
 
+/* ---- fused linear + cross-entropy ---------------------------------------------
+ * Forward of tritium.linear_cross_entropy (tritium/ops/cross_entropy.py:134-293
+ * kernels, host `_linear_cross_entropy_forward` 563-640, autograd 663-705),
+ * plus torch's ignore_index (absent from the reference).
+ * hidden: [n_rows, hidden_size], weight: [vocab, hidden_size] in `dtype`,
+ * 16-byte aligned, hidden_size a multiple of 8 (16-bit) or 4 (fp32);
+ * target: [n_rows] int32 (target_kind 1) or int64 (2).  Writes loss[0] = mean
+ * over rows whose target != ignore_index of lse - logit[target] (NaN when no
+ * row counts), lse: [n_rows] float32 (natural log), n_valid[0] (may be NULL) =
+ * that row count as float.  The logits are never written to memory. */
+size_t tritium_linear_ce_fwd_workspace_size(int64_t n_rows, int64_t vocab);
+int tritium_linear_ce_fwd(const void* hidden, const void* weight, const void* target,
+                          int target_kind, int64_t ignore_index, float* loss, float* lse,
+                          float* n_valid, void* workspace, size_t workspace_bytes,
+                          int64_t n_rows, int64_t hidden_size, int64_t vocab, int dtype,
+                          void* stream);
+
+/* Backward: tritium.linear_cross_entropy_backward (tritium/ops/cross_entropy.py:863-959).
+ * grad_out: device float32 scalar; lse from the forward.  dhidden: [n_rows,
+ * hidden_size], dweight: [vocab, hidden_size], both in `dtype`; either may be
+ * NULL (not computed).  The vocabulary is processed in chunks of chunk_rows
+ * rows (0 = automatic, about 1 GiB of gradient tiles). */
+size_t tritium_linear_ce_bwd_workspace_size(int64_t n_rows, int64_t hidden_size, int64_t vocab,
+                                            int dtype, int need_dhidden, int need_dweight,
+                                            int64_t chunk_rows);
+int tritium_linear_ce_bwd(const float* grad_out, const void* hidden, const void* weight,
+                          const void* target, int target_kind, int64_t ignore_index,
+                          const float* lse, void* dhidden, void* dweight, void* workspace,
+                          size_t workspace_bytes, int64_t n_rows, int64_t hidden_size,
+                          int64_t vocab, int64_t chunk_rows, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
