@@ -50,9 +50,9 @@ def sources() -> list[str]:
     )
 
 
-def _compile(src: str) -> tuple[str, str]:
-    obj = os.path.join(OBJ_DIR, os.path.basename(src)[: -len(".hip")] + ".o")
-    cmd = [HIPCC, *COMPILE_FLAGS, "-c", src, "-o", obj]
+def _compile(src: str, obj_dir: str = OBJ_DIR, defines: tuple[str, ...] = ()) -> tuple[str, str]:
+    obj = os.path.join(obj_dir, os.path.basename(src)[: -len(".hip")] + ".o")
+    cmd = [HIPCC, *COMPILE_FLAGS, *(f"-D{d}" for d in defines), "-c", src, "-o", obj]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     noise = "'-packed-fp32-ops' is not a recognized feature"
     log = "\n".join(
@@ -63,32 +63,39 @@ def _compile(src: str) -> tuple[str, str]:
     return obj, log
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> str:
-    """Compile every csrc/*.hip and link the shared library; return its path."""
-    os.makedirs(OBJ_DIR, exist_ok=True)
+def build(jobs: int | None = None, verbose: bool = False, out: str = LIB_PATH,
+          defines: tuple[str, ...] = ()) -> str:
+    """Compile every csrc/*.hip and link the shared library; return its path.
+
+    ``out`` and ``defines`` (``-D`` macros) build variant libraries, e.g. a
+    different GEMM tile configuration, next to the default one."""
+    obj_dir = OBJ_DIR if out == LIB_PATH else out + ".objs"
+    os.makedirs(obj_dir, exist_ok=True)
     srcs = sources()
     jobs = jobs or min(len(srcs), max(1, min(16, os.cpu_count() or 1)))
     with cf.ThreadPoolExecutor(max_workers=jobs) as pool:
-        results = list(pool.map(_compile, srcs))
+        results = list(pool.map(lambda s: _compile(s, obj_dir, tuple(defines)), srcs))
     for obj, log in results:
         if log.strip() and verbose:
             print(f"[{os.path.basename(obj)}]\n{log}", file=sys.stderr)
-    tmp = LIB_PATH + ".tmp"
+    tmp = out + ".tmp"
     cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp,
            *[obj for obj, _ in results]]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{proc.stdout}{proc.stderr}")
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
 
 
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("-v", "--verbose", action="store_true")
+    ap.add_argument("--out", default=LIB_PATH, help="library path (default: in-tree)")
+    ap.add_argument("-D", dest="defines", action="append", default=[], help="preprocessor macro")
     args = ap.parse_args(argv)
-    print(build(args.jobs, args.verbose))
+    print(build(args.jobs, args.verbose, args.out, tuple(args.defines)))
     return 0
 
 

@@ -23,7 +23,11 @@ import threading
 import torch
 
 LIB_NAME = "libtritium_hip.so"
-LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+# TRITIUM_HIP_LIB selects another build of the same library (e.g. a variant
+# tile configuration built with `python -m helion_amd._build --out ... -D ...`).
+LIB_PATH = os.environ.get("TRITIUM_HIP_LIB") or os.path.join(
+    os.path.dirname(os.path.abspath(__file__)), LIB_NAME
+)
 ABI_VERSION = 1
 
 DTYPE_CODES = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
@@ -67,7 +71,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P,
          _I32, _I32, _P],
     ),
-    "tritium_linear_ce_fwd_workspace_size": (_SZ, [_I64, _I64]),
+    "tritium_linear_ce_fwd_workspace_size": (_SZ, [_I64, _I64, _I32]),
     "tritium_linear_ce_fwd": (
         _I32,
         [_P, _P, _P, _I32, _I64, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I32, _P],

@@ -1,21 +1,28 @@
 // Block-tiled GEMM core C = A * B^T for gfx950 with pluggable epilogues.
 //
 // Both operands are "K-contiguous": A is [M, K] and B is [N, K], row-major
-// with leading dimensions lda / ldb (elements, multiples of 16 bytes), so
-// every MFMA fragment is one 16-byte LDS read.  One workgroup = 4 wavefronts
-// computes a kBM x kBN tile of C; wavefront w owns rows (w>>1)*128 .. +128 and
-// columns (w&1)*64 .. +64, i.e. 4 x 2 tiles of 32 x 32.
+// with leading dimensions lda / ldb (elements; rows 16-byte aligned), so every
+// MFMA fragment is one 16-byte LDS read.  A workgroup of WM x WN wavefronts
+// computes a BM x BN tile of C; wavefront (wm, wn) owns the (BM/WM) x (BN/WN)
+// sub-tile at (wm*BM/WM, wn*BN/WN), i.e. MT x NT tiles of 32 x 32.
 //
-// Accumulator layout (identical for the MFMA and the SIMT core, so epilogues
-// are shared): acc[i][j][r] holds
-//     C[m0 + wm*128 + 32*i + 8*(r/4) + 4*(lane/32) + r%4][n0 + wn*64 + 32*j + lane%32]
-// which is the C layout of v_mfma_f32_32x32x16_{bf16,f16}.
+// Accumulator layout (identical for the MFMA and the fp32 SIMT core, so the
+// epilogues are shared): acc.t[i][j][r] holds
+//     C[m0 + acc_row(wm, i, r, g)][n0 + acc_col(wn, j, lane % 32)],  g = lane / 32,
+// the C layout of v_mfma_f32_32x32x16_{bf16,f16}.
 //
-// Pipeline: K is walked in tiles of 128 bytes per row (64 16-bit or 32 fp32
-// elements), double-buffered in LDS (rows padded by 16 bytes against bank
-// conflicts).  Global loads of tile k+1 are issued into registers before the
-// MFMAs of tile k and written to the other LDS buffer afterwards, one barrier
-// per K tile.  Out-of-range rows and the K tail read as zero.
+// Pipeline: K is walked in tiles of RB bytes per row (64 or 128: 32 or 64
+// 16-bit elements) through STAGES LDS buffers.  Tiles are fetched with
+// global_load_lds_dwordx4 (straight into LDS, no staging registers): lane i
+// of an instruction fills bytes [16 i, 16 i + 16) of a 1 KiB run, which covers
+// 1024 / RB rows; each lane picks which 16-byte granule it fetches so that the rows
+// land XOR-swizzled (granule c of row r at slot c ^ swz_key(r)), and the MFMA
+// fragment reads of consecutive rows hit distinct 16-byte bank groups.
+// One barrier per K tile: at step kt the wave waits for tile kt, syncs, issues
+// tile kt + STAGES - 1 into the buffer read at step kt - 1, then computes.
+// Rows past M (N) re-read the last valid row (their results are never
+// stored); a partial last K tile is zero-filled through registers and done
+// first, so the pipelined loop has no bounds checks.
 #pragma once
 
 #include "common.h"
@@ -26,177 +33,72 @@ namespace gemm {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) void lds_void;
 
-constexpr int kBM = 256;
-constexpr int kBN = 128;
-constexpr int kThreads = 256;
-constexpr int kMT = 4;  // 32-row MFMA tiles per wavefront
-constexpr int kNT = 2;  // 32-column MFMA tiles per wavefront
-constexpr int kRowBytes = 128;
-constexpr int kPadBytes = 16;
+constexpr int kXcds = 8;
 
-template <typename T> constexpr int bk() { return kRowBytes / (int)sizeof(T); }
-template <typename T> constexpr int ldl() { return (kRowBytes + kPadBytes) / (int)sizeof(T); }
+// BM x BN tile, WM x WN wavefronts, STAGES LDS buffers of K tiles whose rows
+// are RB bytes (64 or 128: 32 or 64 16-bit elements).
+template <int BM_, int BN_, int WM_, int WN_, int STAGES_, int RB_ = 128>
+struct Cfg {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_, STAGES = STAGES_, RB = RB_;
+  static constexpr int THREADS = WM * WN * 64;
+  static constexpr int WTM = BM / WM, WTN = BN / WN;
+  static constexpr int MT = WTM / 32, NT = WTN / 32;
+  static constexpr int GRAN = RB / 16;            // 16-byte granules per row
+  static constexpr int DMA_ROWS = 1024 / RB;      // rows per global_load_lds (1 KiB)
+  static constexpr int STAGE_BYTES = (BM + BN) * RB;
+  static constexpr int SMEM_BYTES = STAGES * STAGE_BYTES;
+  static constexpr int DMA_PER_WAVE = (BM + BN) / DMA_ROWS / (WM * WN);
+  static_assert(RB == 64 || RB == 128, "row bytes");
+  static_assert((BM + BN) % (DMA_ROWS * WM * WN) == 0, "rows must split evenly over the wavefronts");
+  static_assert(BM % DMA_ROWS == 0 && WTM % 32 == 0 && WTN % 32 == 0, "32x32 MFMA tiles");
+  static_assert(STAGES >= 2, "at least double buffering");
+};
+
+template <class C>
+struct Acc {
+  f32x16 t[C::MT][C::NT];
+};
+
+template <class C, typename T> constexpr int bk() { return C::RB / (int)sizeof(T); }
 template <typename T> constexpr int vec() { return 16 / (int)sizeof(T); }
 
-template <typename T>
-struct Smem {
-  T a[2][kBM * ldl<T>()];
-  T b[2][kBN * ldl<T>()];
-};
+// XOR pattern of tile row r: a b128 read of the same granule of 8 consecutive
+// rows (one 128-byte LDS cycle) or of 16 consecutive rows (one 256-byte
+// cycle) touches every 16-byte bank group once.
+template <class C>
+__device__ __forceinline__ int swz_key(int r) {
+  if constexpr (C::RB == 128) return (r & 7) ^ ((r >> 3) & 1);
+  else return ((r >> 2) ^ (r >> 1)) & 3;
+}
+// Byte offset of 16-byte granule c of tile row r.
+template <class C>
+__device__ __forceinline__ int swz(int r, int c) { return r * C::RB + ((c ^ swz_key<C>(r)) << 4); }
 
-struct Acc {
-  f32x16 t[kMT][kNT];
-};
-
-// Registers holding one K tile of one operand between its global load and
-// its LDS store: ROWS rows x 8 sixteen-byte vectors, spread over 256 lanes.
-template <int ROWS>
-struct Staging {
-  uint4 v[ROWS * 8 / kThreads];
-};
-
-template <typename T, int ROWS>
-__device__ __forceinline__ void load_tile(Staging<ROWS>& st, const T* __restrict__ base,
-                                          int64_t ld, int64_t row0, int64_t n_rows, int64_t k0,
-                                          int64_t K) {
-  constexpr int VE = vec<T>();
-#pragma unroll
-  for (int i = 0; i < ROWS * 8 / kThreads; ++i) {
-    const int idx = i * kThreads + threadIdx.x;
-    const int64_t row = row0 + (idx >> 3);
-    const int64_t k = k0 + (int64_t)(idx & 7) * VE;
-    uint4 v = make_uint4(0, 0, 0, 0);
-    if (row < n_rows) {
-      const T* p = base + row * ld + k;
-      if (k + VE <= K) {
-        v = *reinterpret_cast<const uint4*>(p);
-      } else if (k < K) {
-        Pack<T, VE> pk;
-#pragma unroll
-        for (int e = 0; e < VE; ++e) pk.v[e] = (k + e < K) ? p[e] : (T)0.f;
-        v = __builtin_bit_cast(uint4, pk);
-      }
-    }
-    st.v[i] = v;
-  }
+template <class C>
+__device__ __forceinline__ int acc_row(int wm, int i, int r, int g) {
+  return wm * C::WTM + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+}
+template <class C>
+__device__ __forceinline__ int acc_col(int wn, int j, int l32) {
+  return wn * C::WTN + 32 * j + l32;
 }
 
-template <typename T, int ROWS>
-__device__ __forceinline__ void store_tile(const Staging<ROWS>& st, T* lds) {
-  constexpr int VE = vec<T>();
-#pragma unroll
-  for (int i = 0; i < ROWS * 8 / kThreads; ++i) {
-    const int idx = i * kThreads + threadIdx.x;
-    *reinterpret_cast<uint4*>(lds + (idx >> 3) * ldl<T>() + (idx & 7) * VE) = st.v[i];
-  }
+// s_waitcnt with vmcnt = n and the other counters unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
+
+__device__ __forceinline__ int64_t imin(int64_t a, int64_t b) { return a < b ? a : b; }
 
 __device__ __forceinline__ f32x16 zero16() {
   f32x16 z;
 #pragma unroll
   for (int i = 0; i < 16; ++i) z[i] = 0.f;
   return z;
-}
-
-// ---- per-K-tile compute: MFMA for 16-bit types, FMA for fp32 --------------
-template <typename T> struct Core;
-
-__device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ f32x16 mma(f16x8 a, f16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-}
-
-template <typename T, typename V>
-__device__ __forceinline__ void mfma_tile(Acc& acc, const T* As, const T* Bs, int wm, int wn) {
-  const int lane = threadIdx.x & 63;
-  const int l32 = lane & 31, g = lane >> 5;
-  constexpr int LD = ldl<T>();
-#pragma unroll
-  for (int s = 0; s < bk<T>() / 16; ++s) {
-    V a[kMT], b[kNT];
-#pragma unroll
-    for (int i = 0; i < kMT; ++i)
-      a[i] = *reinterpret_cast<const V*>(As + (wm * 128 + 32 * i + l32) * LD + 16 * s + 8 * g);
-#pragma unroll
-    for (int j = 0; j < kNT; ++j)
-      b[j] = *reinterpret_cast<const V*>(Bs + (wn * 64 + 32 * j + l32) * LD + 16 * s + 8 * g);
-#pragma unroll
-    for (int i = 0; i < kMT; ++i)
-#pragma unroll
-      for (int j = 0; j < kNT; ++j) acc.t[i][j] = mma(a[i], b[j], acc.t[i][j]);
-  }
-}
-
-template <> struct Core<bf16_t> {
-  static __device__ __forceinline__ void tile(Acc& acc, const bf16_t* As, const bf16_t* Bs,
-                                              int wm, int wn) {
-    mfma_tile<bf16_t, bf16x8>(acc, As, Bs, wm, wn);
-  }
-};
-template <> struct Core<f16_t> {
-  static __device__ __forceinline__ void tile(Acc& acc, const f16_t* As, const f16_t* Bs,
-                                              int wm, int wn) {
-    mfma_tile<f16_t, f16x8>(acc, As, Bs, wm, wn);
-  }
-};
-
-// fp32: exact FMA arithmetic in the same accumulator layout.  Per 4-wide K
-// step a lane reads one float4 per accumulated row group and per column.
-template <> struct Core<float> {
-  static __device__ __forceinline__ void tile(Acc& acc, const float* As, const float* Bs,
-                                              int wm, int wn) {
-    const int lane = threadIdx.x & 63;
-    const int l32 = lane & 31, g = lane >> 5;
-    constexpr int LD = ldl<float>();
-#pragma unroll 1
-    for (int k = 0; k < bk<float>(); k += 4) {
-      float4 b[kNT];
-#pragma unroll
-      for (int j = 0; j < kNT; ++j)
-        b[j] = *reinterpret_cast<const float4*>(Bs + (wn * 64 + 32 * j + l32) * LD + k);
-#pragma unroll
-      for (int i = 0; i < kMT; ++i) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = wm * 128 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
-          const float4 a = *reinterpret_cast<const float4*>(As + m * LD + k);
-#pragma unroll
-          for (int j = 0; j < kNT; ++j) {
-            float c = acc.t[i][j][r];
-            c = fmaf(a.x, b[j].x, c);
-            c = fmaf(a.y, b[j].y, c);
-            c = fmaf(a.z, b[j].z, c);
-            c = fmaf(a.w, b[j].w, c);
-            acc.t[i][j][r] = c;
-          }
-        }
-      }
-    }
-  }
-};
-
-// Tile coordinates of work item `w` of a tiles_m x tiles_n grid: groups of
-// kGroupM row tiles are walked column by column so that the blocks resident
-// on one XCD share A and B tiles in its L2.
-constexpr int kGroupM = 4;
-constexpr int kXcds = 8;
-
-__device__ __forceinline__ void tile_of(int64_t bid, int64_t n_blocks, int tiles_m, int tiles_n,
-                                        int& tm, int& tn) {
-  // XCD-aware: block ids are dealt round-robin to the 8 XCDs; give each XCD a
-  // contiguous range of work items.
-  int64_t w = bid;
-  if (n_blocks % kXcds == 0) w = (bid % kXcds) * (n_blocks / kXcds) + bid / kXcds;
-  const int64_t per_group = (int64_t)kGroupM * tiles_n;
-  const int64_t group = w / per_group;
-  const int first_m = (int)(group * kGroupM);
-  const int gsize = min(tiles_m - first_m, kGroupM);
-  const int64_t in_group = w % per_group;
-  tm = first_m + (int)(in_group % gsize);
-  tn = (int)(in_group / gsize);
 }
 
 struct Problem {
@@ -206,50 +108,285 @@ struct Problem {
   int64_t M, N, K;
 };
 
-// Main loop: accumulate the (tm, tn) tile of A * B^T over all of K.
-template <typename T>
-__device__ __forceinline__ void mainloop(const Problem& p, int tm, int tn, Smem<T>& sm,
-                                         Acc& acc) {
-  const int wave = threadIdx.x >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
-  const T* A = (const T*)p.a;
-  const T* B = (const T*)p.b;
-  const int64_t m0 = (int64_t)tm * kBM, n0 = (int64_t)tn * kBN;
-  constexpr int BK = bk<T>();
-#pragma unroll
-  for (int i = 0; i < kMT; ++i)
-#pragma unroll
-    for (int j = 0; j < kNT; ++j) acc.t[i][j] = zero16();
+// One global_load_lds_dwordx4: lane i's 16 bytes at `g` land at LDS byte
+// lds + 16 i.  Issued through inline assembly on purpose: the compiler models
+// a pending LDS DMA by turning every later LDS-read wait into lgkmcnt(0),
+// which would serialise the fragment reads of step s + 1 with the MFMAs of
+// step s.  Its completion is awaited explicitly (wait_vmcnt before the
+// barrier that publishes the tile); VMEM operations the compiler does not
+// see can only make its own in-order vmcnt waits stricter.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
+               : "memory", "m0");
+}
 
-  const int64_t nk = cdiv(p.K, BK);
-  Staging<kBM> sa;
-  Staging<kBN> sb;
-  load_tile<T, kBM>(sa, A, p.lda, m0, p.M, 0, p.K);
-  load_tile<T, kBN>(sb, B, p.ldb, n0, p.N, 0, p.K);
-  store_tile<T, kBM>(sa, sm.a[0]);
-  store_tile<T, kBN>(sb, sm.b[0]);
-  __syncthreads();
-  for (int64_t kt = 0; kt < nk; ++kt) {
-    const int cur = (int)(kt & 1);
-    const bool more = kt + 1 < nk;
-    if (more) {
-      load_tile<T, kBM>(sa, A, p.lda, m0, p.M, (kt + 1) * BK, p.K);
-      load_tile<T, kBN>(sb, B, p.ldb, n0, p.N, (kt + 1) * BK, p.K);
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_void*)p;
+}
+
+// Issue the DMA of K tile k0 of both operands into one LDS stage.
+template <class C, typename T>
+__device__ __forceinline__ void dma_tile(char* stage, const Problem& p, int64_t m0, int64_t n0,
+                                         int64_t k0) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rr = lane / C::GRAN;  // row inside the instruction's run of DMA_ROWS rows
+  constexpr int VE = vec<T>();
+#pragma unroll
+  for (int q = 0; q < C::DMA_PER_WAVE; ++q) {
+    const int grp = wave * C::DMA_PER_WAVE + q;  // wave-uniform run of rows
+    const int trow = grp * C::DMA_ROWS + rr;     // tile row (A rows, then B rows)
+    // the granule that lands in slot lane % GRAN of that row
+    const int c = (lane % C::GRAN) ^ swz_key<C>(trow);
+    const T* src;
+    if (grp * C::DMA_ROWS < C::BM) {
+      const int64_t row = imin(m0 + trow, p.M - 1);
+      src = (const T*)p.a + row * p.lda + k0 + c * VE;
+    } else {
+      const int64_t row = imin(n0 + trow - C::BM, p.N - 1);
+      src = (const T*)p.b + row * p.ldb + k0 + c * VE;
     }
-    Core<T>::tile(acc, sm.a[cur], sm.b[cur], wm, wn);
-    if (more) {
-      store_tile<T, kBM>(sa, sm.a[cur ^ 1]);
-      store_tile<T, kBN>(sb, sm.b[cur ^ 1]);
-    }
-    __syncthreads();
+    dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(stage + grp * C::DMA_ROWS * C::RB)));
   }
 }
 
-// Row of C held by accumulator element (i, r) of this lane, relative to the tile.
-__device__ __forceinline__ int acc_row(int wm, int i, int r, int g) {
-  return wm * 128 + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
+// The partial last K tile [k0, K) through registers, zero-filled past K.
+template <class C, typename T>
+__device__ __forceinline__ void reg_tile(char* stage, const Problem& p, int64_t m0, int64_t n0,
+                                         int64_t k0) {
+  constexpr int VE = vec<T>();
+  for (int idx = threadIdx.x; idx < (C::BM + C::BN) * C::GRAN; idx += C::THREADS) {
+    const int row = idx / C::GRAN, c = idx % C::GRAN;
+    const T* src;
+    if (row < C::BM) {
+      src = (const T*)p.a + imin(m0 + row, p.M - 1) * p.lda;
+    } else {
+      src = (const T*)p.b + imin(n0 + row - C::BM, p.N - 1) * p.ldb;
+    }
+    const int64_t k = k0 + c * VE;
+    Pack<T, VE> pk;
+#pragma unroll
+    for (int e = 0; e < VE; ++e) pk.v[e] = (k + e < p.K) ? src[k + e] : (T)0.f;
+    *reinterpret_cast<Pack<T, VE>*>(stage + swz<C>(row, c)) = pk;
+  }
 }
-__device__ __forceinline__ int acc_col(int wn, int j, int l32) { return wn * 64 + 32 * j + l32; }
+
+// Register-staged copy of one K tile: global loads into VGPRs (issued early),
+// LDS stores later (after the MFMAs of the current tile).
+template <class C>
+struct Stage {
+  static constexpr int N = (C::BM + C::BN) * C::GRAN / C::THREADS;
+  uint4 v[N];
+};
+
+template <class C, typename T>
+__device__ __forceinline__ void stage_load(Stage<C>& st, const Problem& p, int64_t m0, int64_t n0,
+                                           int64_t k0) {
+  constexpr int VE = vec<T>();
+#pragma unroll
+  for (int q = 0; q < Stage<C>::N; ++q) {
+    const int idx = q * C::THREADS + threadIdx.x;
+    const int row = idx / C::GRAN, c = idx % C::GRAN;  // row-uniform per 8 or 4 lanes
+    const T* src;
+    if (row < C::BM) {
+      src = (const T*)p.a + imin(m0 + row, p.M - 1) * p.lda;
+    } else {
+      src = (const T*)p.b + imin(n0 + row - C::BM, p.N - 1) * p.ldb;
+    }
+    st.v[q] = *reinterpret_cast<const uint4*>(src + k0 + c * VE);
+  }
+}
+
+template <class C>
+__device__ __forceinline__ void stage_store(const Stage<C>& st, char* stage) {
+#pragma unroll
+  for (int q = 0; q < Stage<C>::N; ++q) {
+    const int idx = q * C::THREADS + threadIdx.x;
+    *reinterpret_cast<uint4*>(stage + swz<C>(idx / C::GRAN, idx % C::GRAN)) = st.v[q];
+  }
+}
+
+// ---- per-K-tile compute: MFMA for 16-bit types, FMA for fp32 --------------
+__device__ __forceinline__ f32x16 mma(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mma(f16x8 a, f16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+template <typename T> struct FragOf;
+template <> struct FragOf<bf16_t> { typedef bf16x8 V; };
+template <> struct FragOf<f16_t> { typedef f16x8 V; };
+
+// Compiler fence: no instruction is scheduled across it.
+__device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
+
+template <class C, typename T>
+__device__ __forceinline__ void compute_tile(const char* stage, Acc<C>& acc, int wm, int wn) {
+  const char* As = stage;
+  const char* Bs = stage + C::BM * C::RB;
+  const int lane = threadIdx.x & 63;
+  const int l32 = lane & 31, g = lane >> 5;
+  if constexpr (sizeof(T) == 2) {
+    // Explicit order, fenced against the scheduler: the fragment reads of
+    // 16-deep step s + 1 are issued before the MFMAs of step s, so each LDS
+    // round trip hides behind a step of MFMAs (left alone, the compiler
+    // reuses one fragment buffer and waits on every read).
+    typedef typename FragOf<T>::V V;
+    constexpr int KS = C::RB / 32;  // 16-deep MFMA steps per K tile
+    V a[2][C::MT], b[2][C::NT];
+    auto load = [&](int s, int buf) {
+#pragma unroll
+      for (int i = 0; i < C::MT; ++i)
+        a[buf][i] = *reinterpret_cast<const V*>(As + swz<C>(wm * C::WTM + 32 * i + l32, 2 * s + g));
+#pragma unroll
+      for (int j = 0; j < C::NT; ++j)
+        b[buf][j] = *reinterpret_cast<const V*>(Bs + swz<C>(wn * C::WTN + 32 * j + l32, 2 * s + g));
+    };
+    load(0, 0);
+    fence();
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      if (s + 1 < KS) load(s + 1, (s + 1) & 1);
+      fence();
+#pragma unroll
+      for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+        for (int j = 0; j < C::NT; ++j)
+          acc.t[i][j] = mma(a[s & 1][i], b[s & 1][j], acc.t[i][j]);
+      fence();
+    }
+  } else {
+    // fp32: exact FMAs; one float4 (one granule) per row and per column per step
+#pragma unroll 1
+    for (int c = 0; c < C::GRAN; ++c) {
+      float4 b[C::NT];
+#pragma unroll
+      for (int j = 0; j < C::NT; ++j)
+        b[j] = *reinterpret_cast<const float4*>(Bs + swz<C>(wn * C::WTN + 32 * j + l32, c));
+#pragma unroll
+      for (int i = 0; i < C::MT; ++i) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const float4 a = *reinterpret_cast<const float4*>(As + swz<C>(acc_row<C>(wm, i, r, g), c));
+#pragma unroll
+          for (int j = 0; j < C::NT; ++j) {
+            float v = acc.t[i][j][r];
+            v = fmaf(a.x, b[j].x, v);
+            v = fmaf(a.y, b[j].y, v);
+            v = fmaf(a.z, b[j].z, v);
+            v = fmaf(a.w, b[j].w, v);
+            acc.t[i][j][r] = v;
+          }
+        }
+      }
+    }
+  }
+}
+
+// Tile coordinates of block `bid` of a tiles_m x tiles_n grid.  Block ids are
+// dealt round-robin to the 8 XCDs; each XCD gets a contiguous range of work
+// items, walked in groups of GROUP_M row tiles column by column so that the
+// blocks resident on one XCD share A and B tiles in its L2.
+template <int GROUP_M = 4>
+__device__ __forceinline__ void tile_of(int64_t bid, int64_t n_blocks, int tiles_m, int tiles_n,
+                                        int& tm, int& tn) {
+  int64_t w = bid;
+  if (n_blocks % kXcds == 0) w = (bid % kXcds) * (n_blocks / kXcds) + bid / kXcds;
+  const int64_t per_group = (int64_t)GROUP_M * tiles_n;
+  const int64_t group = w / per_group;
+  const int first_m = (int)(group * GROUP_M);
+  const int gsize = min(tiles_m - first_m, GROUP_M);
+  const int64_t in_group = w % per_group;
+  tm = first_m + (int)(in_group % gsize);
+  tn = (int)(in_group / gsize);
+}
+
+#ifndef TRI_GEMM_DMA
+#define TRI_GEMM_DMA 1
+#endif
+
+// Accumulate the (tm, tn) tile of A * B^T over all of K.  `smem` holds
+// C::SMEM_BYTES of LDS (1 KiB aligned).
+template <class C, typename T>
+__device__ __forceinline__ void mainloop(const Problem& p, int tm, int tn, char* smem,
+                                         Acc<C>& acc) {
+  const int wave = threadIdx.x >> 6;
+  const int wm = wave / C::WN, wn = wave % C::WN;
+  const int64_t m0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
+  constexpr int BK = bk<C, T>();
+#pragma unroll
+  for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+    for (int j = 0; j < C::NT; ++j) acc.t[i][j] = zero16();
+
+  const int64_t nfull = p.K / BK;
+  if (p.K % BK != 0) {
+    reg_tile<C, T>(smem, p, m0, n0, nfull * BK);
+    __syncthreads();
+    compute_tile<C, T>(smem, acc, wm, wn);
+    __syncthreads();
+  }
+  if constexpr (C::STAGES == 2 && !TRI_GEMM_DMA) {
+    // register-staged double buffer: at step kt the global loads of tile
+    // kt + 1 are in flight while tile kt is multiplied, then land in the
+    // buffer read at step kt - 1
+    Stage<C> st;
+    if (nfull > 0) {
+      stage_load<C, T>(st, p, m0, n0, 0);
+      stage_store<C>(st, smem);
+    }
+    for (int64_t kt = 0; kt + 1 < nfull; ++kt) {
+      __syncthreads();
+      stage_load<C, T>(st, p, m0, n0, (kt + 1) * BK);
+      compute_tile<C, T>(smem + (int)(kt & 1) * C::STAGE_BYTES, acc, wm, wn);
+      stage_store<C>(st, smem + (int)((kt + 1) & 1) * C::STAGE_BYTES);
+    }
+    if (nfull > 0) {
+      __syncthreads();
+      compute_tile<C, T>(smem + (int)((nfull - 1) & 1) * C::STAGE_BYTES, acc, wm, wn);
+    }
+  } else if constexpr (C::STAGES == 2) {
+    // branch-free steady state: wait for tile kt, sync, prefetch tile kt + 1
+    // into the buffer read at step kt - 1, compute tile kt
+    if (nfull > 0) dma_tile<C, T>(smem, p, m0, n0, 0);
+    for (int64_t kt = 0; kt + 1 < nfull; ++kt) {
+      wait_vmcnt<0>();
+      __syncthreads();
+      dma_tile<C, T>(smem + (int)((kt + 1) & 1) * C::STAGE_BYTES, p, m0, n0, (kt + 1) * BK);
+      compute_tile<C, T>(smem + (int)(kt & 1) * C::STAGE_BYTES, acc, wm, wn);
+    }
+    if (nfull > 0) {
+      wait_vmcnt<0>();
+      __syncthreads();
+      compute_tile<C, T>(smem + (int)((nfull - 1) & 1) * C::STAGE_BYTES, acc, wm, wn);
+    }
+  } else {
+#pragma unroll
+    for (int s = 0; s < C::STAGES - 1; ++s)
+      if (s < nfull) dma_tile<C, T>(smem + s * C::STAGE_BYTES, p, m0, n0, (int64_t)s * BK);
+    for (int64_t kt = 0; kt < nfull; ++kt) {
+      if (kt + C::STAGES - 2 < nfull)
+        wait_vmcnt<(C::STAGES - 2) * C::DMA_PER_WAVE>();
+      else
+        wait_vmcnt<0>();
+      __syncthreads();
+      const int64_t next = kt + C::STAGES - 1;
+      if (next < nfull)
+        dma_tile<C, T>(smem + (int)(next % C::STAGES) * C::STAGE_BYTES, p, m0, n0, next * BK);
+      compute_tile<C, T>(smem + (int)(kt % C::STAGES) * C::STAGE_BYTES, acc, wm, wn);
+    }
+  }
+  __syncthreads();
+}
+
+// Configurations: 16-bit types run 256 x 256 tiles on 8 wavefronts (2 per
+// SIMD, 128 x 64 each), double-buffered 128-byte K rows; fp32 (exact SIMT
+// arithmetic) runs 128 x 128 tiles on 4 wavefronts.
+#ifndef TRI_GEMM16_CFG
+#define TRI_GEMM16_CFG 256, 256, 2, 4, 2, 128
+#endif
+template <typename T> struct CfgOf { typedef Cfg<TRI_GEMM16_CFG> type; };
+template <> struct CfgOf<float> { typedef Cfg<128, 128, 2, 2, 2> type; };
 
 }  // namespace gemm
 }  // namespace tri

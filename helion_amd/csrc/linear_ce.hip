@@ -37,10 +37,10 @@ namespace tri {
 namespace {
 
 using gemm::Acc;
-using gemm::kBM;
-using gemm::kBN;
-using gemm::kMT;
-using gemm::kNT;
+using gemm::acc_col;
+using gemm::acc_row;
+template <typename T> using CfgT = typename gemm::CfgOf<T>::type;
+constexpr int kMaxBM = 256;  // largest row tile of any configuration
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kRowsBlock = 256;        // threads of lce_fwd_rows
@@ -65,76 +65,83 @@ struct FwdArgs {
 };
 
 template <typename T, typename TT>
-__global__ void __launch_bounds__(gemm::kThreads)
+__global__ void __launch_bounds__(CfgT<T>::THREADS)
 lce_fwd_kernel(FwdArgs a) {
-  __shared__ gemm::Smem<T> sm;
-  __shared__ float red[2][kBN];
+  typedef CfgT<T> C;
+  __shared__ __attribute__((aligned(1024))) char smem[C::SMEM_BYTES];
+  __shared__ float red[C::WM][C::BN];
   int tm, tn;
   gemm::tile_of(blockIdx.x, gridDim.x, a.tiles_v, a.tiles_n, tm, tn);
   gemm::Problem p{a.weight, a.hidden, a.ld, a.ld, a.V, a.N, a.D};
-  Acc acc;
-  gemm::mainloop<T>(p, tm, tn, sm, acc);
+  Acc<C> acc;
+  gemm::mainloop<C, T>(p, tm, tn, smem, acc);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31, g = lane >> 5;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int64_t v0 = (int64_t)tm * kBM, n0 = (int64_t)tn * kBN;
+  const int wm = wave / C::WN, wn = wave % C::WN;
+  const int64_t v0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
   const TT* target = (const TT*)a.target;
 
-  float mx[kNT];
+  float mx[C::NT];
 #pragma unroll
-  for (int j = 0; j < kNT; ++j) {
+  for (int j = 0; j < C::NT; ++j) {
     float m = -INFINITY;
 #pragma unroll
-    for (int i = 0; i < kMT; ++i)
+    for (int i = 0; i < C::MT; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        if (v0 + gemm::acc_row(wm, i, r, g) < a.V) m = fmaxf(m, acc.t[i][j][r]);
+        if (v0 + acc_row<C>(wm, i, r, g) < a.V) m = fmaxf(m, acc.t[i][j][r]);
     m = fmaxf(m, __shfl_xor(m, 32, 64));
-    if (g == 0) red[wm][gemm::acc_col(wn, j, l32)] = m;
+    if (g == 0) red[wm][acc_col<C>(wn, j, l32)] = m;
   }
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < kNT; ++j) {
-    const int col = gemm::acc_col(wn, j, l32);
-    mx[j] = fmaxf(red[0][col], red[1][col]);
+  for (int j = 0; j < C::NT; ++j) {
+    const int col = acc_col<C>(wn, j, l32);
+    float m = red[0][col];
+#pragma unroll
+    for (int k = 1; k < C::WM; ++k) m = fmaxf(m, red[k][col]);
+    mx[j] = m;
   }
   __syncthreads();
 #pragma unroll
-  for (int j = 0; j < kNT; ++j) {
-    const int col = gemm::acc_col(wn, j, l32);
+  for (int j = 0; j < C::NT; ++j) {
+    const int col = acc_col<C>(wn, j, l32);
     const int64_t n = n0 + col;
     const float ms = mx[j] * kLog2e;
     float s = 0.f;
 #pragma unroll
-    for (int i = 0; i < kMT; ++i)
+    for (int i = 0; i < C::MT; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        if (v0 + gemm::acc_row(wm, i, r, g) < a.V) s += exp2f(acc.t[i][j][r] * kLog2e - ms);
+        if (v0 + acc_row<C>(wm, i, r, g) < a.V) s += exp2f(acc.t[i][j][r] * kLog2e - ms);
     s += __shfl_xor(s, 32, 64);
     if (g == 0) red[wm][col] = s;
     // the target logit: written by the single lane that holds its row
     if (n < a.N) {
       const int64_t t = load_target(target, n);
-      const int64_t dt = t - v0 - wm * 128;
-      if (t < a.V && dt >= 0 && dt < 128) {
+      const int64_t dt = t - v0 - wm * C::WTM;
+      if (t < a.V && dt >= 0 && dt < C::WTM) {
 #pragma unroll
-        for (int i = 0; i < kMT; ++i)
+        for (int i = 0; i < C::MT; ++i)
 #pragma unroll
           for (int r = 0; r < 16; ++r)
-            if (gemm::acc_row(0, i, r, g) == dt) a.tlogit[n] = acc.t[i][j][r];
+            if (acc_row<C>(0, i, r, g) == dt) a.tlogit[n] = acc.t[i][j][r];
       }
     }
   }
   __syncthreads();
   if (wm == 0 && g == 0) {
 #pragma unroll
-    for (int j = 0; j < kNT; ++j) {
-      const int col = gemm::acc_col(wn, j, l32);
+    for (int j = 0; j < C::NT; ++j) {
+      const int col = acc_col<C>(wn, j, l32);
       const int64_t n = n0 + col;
       if (n < a.N) {
+        float s = red[0][col];
+#pragma unroll
+        for (int k = 1; k < C::WM; ++k) s += red[k][col];
         a.pmax[(int64_t)tm * a.N + n] = mx[j];
-        a.psum[(int64_t)tm * a.N + n] = red[0][col] + red[1][col];
+        a.psum[(int64_t)tm * a.N + n] = s;
       }
     }
   }
@@ -263,43 +270,42 @@ struct GArgs {
 };
 
 template <typename T, typename TT>
-__global__ void __launch_bounds__(gemm::kThreads)
+__global__ void __launch_bounds__(CfgT<T>::THREADS)
 lce_g_kernel(GArgs a) {
-  __shared__ gemm::Smem<T> sm;
+  typedef CfgT<T> C;
+  __shared__ __attribute__((aligned(1024))) char smem[C::SMEM_BYTES];
   int tm, tn;
   gemm::tile_of(blockIdx.x, gridDim.x, a.tiles_v, a.tiles_n, tm, tn);
   gemm::Problem p{a.weight, a.hidden, a.ld, a.ld, a.Vc, a.N, a.D};
-  Acc acc;
-  gemm::mainloop<T>(p, tm, tn, sm, acc);
+  Acc<C> acc;
+  gemm::mainloop<C, T>(p, tm, tn, smem, acc);
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31, g = lane >> 5;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int64_t v0 = (int64_t)tm * kBM, n0 = (int64_t)tn * kBN;
+  const int wm = wave / C::WN, wn = wave % C::WN;
+  const int64_t v0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
   const float coef_all = a.grad_out[0] / a.n_valid[0];
   T* gt = (T*)a.gt;
   T* gm = (T*)a.gm;
 #pragma unroll
-  for (int j = 0; j < kNT; ++j) {
-    const int64_t n = n0 + gemm::acc_col(wn, j, l32);
+  for (int j = 0; j < C::NT; ++j) {
+    const int64_t n = n0 + acc_col<C>(wn, j, l32);
     if (n >= a.N) continue;
     const float l2 = a.lse[n] * kLog2e;
     const int64_t t = load_target((const TT*)a.target, n);
     const float coef = (t == a.ignore_index) ? 0.f : coef_all;
     const int64_t tl = t - a.vc0;  // target row inside this chunk
 #pragma unroll
-    for (int i = 0; i < kMT; ++i) {
+    for (int i = 0; i < C::MT; ++i) {
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
+        const int64_t vb = v0 + acc_row<C>(wm, i, 4 * rr, g);  // 4 consecutive rows
         float gv[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int r = 4 * rr + e;
-          const int64_t v = v0 + gemm::acc_row(wm, i, r, g);
-          const float pr = exp2f(acc.t[i][j][r] * kLog2e - l2);
-          gv[e] = (pr - (v == tl ? 1.f : 0.f)) * coef;
+          const float pr = exp2f(acc.t[i][j][4 * rr + e] * kLog2e - l2);
+          gv[e] = (pr - (vb + e == tl ? 1.f : 0.f)) * coef;
         }
-        const int64_t vb = v0 + gemm::acc_row(wm, i, 4 * rr, g);  // 4 consecutive rows
         if (gt != nullptr) {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
@@ -322,27 +328,28 @@ lce_g_kernel(GArgs a) {
 
 // Plain GEMM: out[m, n] = (acc_in[m, n] if acc_in) + (A B^T)[m, n].
 template <typename T, typename OT>
-__global__ void __launch_bounds__(gemm::kThreads)
+__global__ void __launch_bounds__(CfgT<T>::THREADS)
 gemm_store_kernel(gemm::Problem p, const float* acc_in, OT* out, int64_t ldc, int tiles_m,
                   int tiles_n) {
-  __shared__ gemm::Smem<T> sm;
+  typedef CfgT<T> C;
+  __shared__ __attribute__((aligned(1024))) char smem[C::SMEM_BYTES];
   int tm, tn;
   gemm::tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
-  Acc acc;
-  gemm::mainloop<T>(p, tm, tn, sm, acc);
+  Acc<C> acc;
+  gemm::mainloop<C, T>(p, tm, tn, smem, acc);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31, g = lane >> 5;
-  const int wm = wave >> 1, wn = wave & 1;
-  const int64_t m0 = (int64_t)tm * kBM, n0 = (int64_t)tn * kBN;
+  const int wm = wave / C::WN, wn = wave % C::WN;
+  const int64_t m0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
 #pragma unroll
-  for (int j = 0; j < kNT; ++j) {
-    const int64_t n = n0 + gemm::acc_col(wn, j, l32);
+  for (int j = 0; j < C::NT; ++j) {
+    const int64_t n = n0 + acc_col<C>(wn, j, l32);
     if (n >= p.N) continue;
 #pragma unroll
-    for (int i = 0; i < kMT; ++i)
+    for (int i = 0; i < C::MT; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t m = m0 + gemm::acc_row(wm, i, r, g);
+        const int64_t m = m0 + acc_row<C>(wm, i, r, g);
         if (m < p.M) {
           float v = acc.t[i][j][r];
           if (acc_in != nullptr) v += acc_in[m * ldc + n];
@@ -381,10 +388,10 @@ struct FwdLayout {
   size_t pmax, psum, tlogit, bnll, bcnt, total;
 };
 
-FwdLayout fwd_layout(int64_t N, int64_t V) {
+FwdLayout fwd_layout(int64_t N, int64_t V, int bm, int bn) {
   FwdLayout L;
-  L.tiles_v = (int)cdiv(V, kBM);
-  L.tiles_n = (int)cdiv(N, kBN);
+  L.tiles_v = (int)cdiv(V, bm);
+  L.tiles_n = (int)cdiv(N, bn);
   L.rows_blocks = (int)cdiv(N, kRowsBlock / kRowsSplit);
   size_t off = 0;
   auto take = [&](size_t bytes) {
@@ -409,10 +416,10 @@ struct BwdLayout {
 BwdLayout bwd_layout(int64_t N, int64_t D, int64_t V, int esz, bool need_dh, bool need_dw,
                      int64_t chunk_rows) {
   BwdLayout L;
-  const int64_t vpad = round_up(V, kBM);
-  int64_t chunk = chunk_rows > 0 ? round_up(chunk_rows, kBM)
-                                 : (kGBudget / std::max<int64_t>(1, 2 * N * esz)) / kBM * kBM;
-  chunk = std::max<int64_t>(kBM, std::min<int64_t>(chunk, vpad));
+  const int64_t vpad = round_up(V, kMaxBM);
+  int64_t chunk = chunk_rows > 0 ? round_up(chunk_rows, kMaxBM)
+                                 : (kGBudget / std::max<int64_t>(1, 2 * N * esz)) / kMaxBM * kMaxBM;
+  chunk = std::max<int64_t>(kMaxBM, std::min<int64_t>(chunk, vpad));
   L.chunk = chunk;
   L.n_chunks = cdiv(V, chunk);
   L.ld_wt = round_up(V, 8);
@@ -441,7 +448,8 @@ int check_sizes(int64_t N, int64_t D, int64_t V, int dtype) {
   const int ve = dtype == kF32 ? 4 : 8;
   if (D % ve != 0)
     return fail(TRI_EINVAL, "linear_ce: hidden_size %lld must be a multiple of %d", (long long)D, ve);
-  if (cdiv(V, kBM) * cdiv(N, kBN) >= ((int64_t)1 << 31) || N >= ((int64_t)1 << 31))
+  if (cdiv(V, 128) * cdiv(N, 128) >= ((int64_t)1 << 31) || N >= ((int64_t)1 << 31) ||
+      cdiv(V, 64) > 65535 || cdiv(N, 64) > 65535)
     return fail(TRI_EINVAL, "linear_ce: problem too large");
   return TRI_OK;
 }
@@ -449,14 +457,15 @@ int check_sizes(int64_t N, int64_t D, int64_t V, int dtype) {
 template <typename T>
 int gemm_store(const gemm::Problem& p, const float* acc_in, void* out, bool out_f32, int64_t ldc,
                hipStream_t st) {
-  const int tiles_m = (int)cdiv(p.M, kBM), tiles_n = (int)cdiv(p.N, kBN);
+  typedef CfgT<T> C;
+  const int tiles_m = (int)cdiv(p.M, C::BM), tiles_n = (int)cdiv(p.N, C::BN);
   const unsigned blocks = (unsigned)((int64_t)tiles_m * tiles_n);
   if (out_f32)
-    gemm_store_kernel<T, float><<<blocks, gemm::kThreads, 0, st>>>(p, acc_in, (float*)out, ldc,
-                                                                   tiles_m, tiles_n);
+    gemm_store_kernel<T, float><<<blocks, C::THREADS, 0, st>>>(p, acc_in, (float*)out, ldc,
+                                                               tiles_m, tiles_n);
   else
-    gemm_store_kernel<T, T><<<blocks, gemm::kThreads, 0, st>>>(p, acc_in, (T*)out, ldc, tiles_m,
-                                                               tiles_n);
+    gemm_store_kernel<T, T><<<blocks, C::THREADS, 0, st>>>(p, acc_in, (T*)out, ldc, tiles_m,
+                                                           tiles_n);
   return check_launch("linear_ce gemm");
 }
 
@@ -472,7 +481,8 @@ template <typename T, typename TT>
 int fwd_impl(const void* hidden, const void* weight, const void* target, int64_t ignore_index,
              float* loss, float* lse, float* n_valid, void* ws, size_t ws_bytes, int64_t N,
              int64_t D, int64_t V, hipStream_t st) {
-  const FwdLayout L = fwd_layout(N, V);
+  typedef CfgT<T> C;
+  const FwdLayout L = fwd_layout(N, V, C::BM, C::BN);
   if (ws_bytes < L.total) return fail(TRI_EINVAL, "linear_ce forward: workspace too small");
   char* w = (char*)ws;
   FwdArgs a;
@@ -486,7 +496,7 @@ int fwd_impl(const void* hidden, const void* weight, const void* target, int64_t
   // a fill kernel rather than a memset node, so the call can be graph-captured
   fill_f32<<<(unsigned)cdiv(N, 256), 256, 0, st>>>(a.tlogit, N, __builtin_nanf(""));
   if (int e = check_launch("linear_ce forward fill")) return e;
-  lce_fwd_kernel<T, TT><<<(unsigned)((int64_t)L.tiles_v * L.tiles_n), gemm::kThreads, 0, st>>>(a);
+  lce_fwd_kernel<T, TT><<<(unsigned)((int64_t)L.tiles_v * L.tiles_n), C::THREADS, 0, st>>>(a);
   if (int e = check_launch("linear_ce forward gemm")) return e;
   lce_fwd_rows<TT><<<(unsigned)L.rows_blocks, kRowsBlock, 0, st>>>(
       a.pmax, a.psum, a.tlogit, (const TT*)target, ignore_index, lse, (double*)(w + L.bnll),
@@ -536,9 +546,9 @@ int bwd_impl(const float* grad_out, const void* hidden, const void* weight, cons
     ga.gm = gm;
     ga.N = N; ga.D = D; ga.Vc = vc; ga.ld = D;
     ga.ld_gt = L.ld_ht; ga.ld_g = L.ld_g; ga.vc0 = vc0; ga.ignore_index = ignore_index;
-    ga.tiles_v = (int)cdiv(vc, kBM);
-    ga.tiles_n = (int)cdiv(N, kBN);
-    lce_g_kernel<T, TT><<<(unsigned)((int64_t)ga.tiles_v * ga.tiles_n), gemm::kThreads, 0, st>>>(ga);
+    ga.tiles_v = (int)cdiv(vc, CfgT<T>::BM);
+    ga.tiles_n = (int)cdiv(N, CfgT<T>::BN);
+    lce_g_kernel<T, TT><<<(unsigned)((int64_t)ga.tiles_v * ga.tiles_n), CfgT<T>::THREADS, 0, st>>>(ga);
     if (int e = check_launch("linear_ce gradient tile")) return e;
     if (need_dh) {
       // dH[N, D] (+)= G[N, vc] * W[vc0:vc0+vc, :]  ==  A = G, B = W^T[:, vc0:]
@@ -570,9 +580,10 @@ int bwd_impl(const float* grad_out, const void* hidden, const void* weight, cons
 
 using namespace tri;
 
-extern "C" size_t tritium_linear_ce_fwd_workspace_size(int64_t n_rows, int64_t vocab) {
+extern "C" size_t tritium_linear_ce_fwd_workspace_size(int64_t n_rows, int64_t vocab, int dtype) {
   if (n_rows <= 0 || vocab <= 0) return 0;
-  return fwd_layout(n_rows, vocab).total;
+  if (dtype == kF32) return fwd_layout(n_rows, vocab, CfgT<float>::BM, CfgT<float>::BN).total;
+  return fwd_layout(n_rows, vocab, CfgT<bf16_t>::BM, CfgT<bf16_t>::BN).total;
 }
 
 extern "C" int tritium_linear_ce_fwd(const void* hidden, const void* weight, const void* target,

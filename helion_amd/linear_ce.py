@@ -115,7 +115,9 @@ def _linear_cross_entropy_forward(hidden, weight, target, ignore_index: int = IG
         return loss, lse
     h2 = _kernel_operand(hidden.reshape(n_rows, hidden_size))
     w2 = _kernel_operand(weight)
-    ws_bytes = _lib.lib().tritium_linear_ce_fwd_workspace_size(n_rows, vocab_size)
+    ws_bytes = _lib.lib().tritium_linear_ce_fwd_workspace_size(
+        n_rows, vocab_size, _lib.dtype_code(hidden.dtype)
+    )
     ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
     _lib.call(
         "tritium_linear_ce_fwd",

@@ -143,7 +143,7 @@ int tritium_attention_bwd(const void* dout, const void* q, const void* k, const 
  * over rows whose target != ignore_index of lse - logit[target] (NaN when no
  * row counts), lse: [n_rows] float32 (natural log), n_valid[0] (may be NULL) =
  * that row count as float.  The logits are never written to memory. */
-size_t tritium_linear_ce_fwd_workspace_size(int64_t n_rows, int64_t vocab);
+size_t tritium_linear_ce_fwd_workspace_size(int64_t n_rows, int64_t vocab, int dtype);
 int tritium_linear_ce_fwd(const void* hidden, const void* weight, const void* target,
                           int target_kind, int64_t ignore_index, float* loss, float* lse,
                           float* n_valid, void* workspace, size_t workspace_bytes,
