@@ -11,6 +11,7 @@ from __future__ import annotations
 import numpy as np
 
 DTYPES = ("f32", "f16", "bf16")
+# "f64" keeps float64 values unrounded: a truth value for finite-difference checks.
 
 
 def bf16_round(x: np.ndarray) -> np.ndarray:
@@ -27,6 +28,8 @@ def bf16_round(x: np.ndarray) -> np.ndarray:
 
 def quantize(x: np.ndarray, dtype: str) -> np.ndarray:
     """Return float32 ``x`` rounded to the storage dtype ``dtype``."""
+    if dtype == "f64":
+        return np.array(x, dtype=np.float64)
     x = np.asarray(x, dtype=np.float32)
     if dtype == "f32":
         return x.copy()
