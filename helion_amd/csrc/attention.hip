@@ -112,41 +112,79 @@ struct BwdArgs {
   float scale;
 };
 
-// Copy a ROWS x D tile of T (row stride `ld` elements in global memory,
-// rows >= valid_rows read as zero) into LDS twice: row-major (`rm`, row
-// stride RLD) and transposed (`tr`, row stride TLD, one row per d).  Each
-// thread moves 4 rows x 8 columns: four 16-byte global loads, four 16-byte
-// row-major LDS writes, eight 8-byte transposed LDS writes.
-template <typename T, int ROWS, int D, int RLD, int TLD, bool RM, bool TR>
-__device__ __forceinline__ void stage_tile(const T* __restrict__ g, int64_t ld, int valid_rows,
-                                           T* rm, T* tr) {
-  constexpr int CH = D / 8;
-  constexpr int ITEMS = (ROWS / 4) * CH;
-  for (int it = threadIdx.x; it < ITEMS; it += 256) {
-    const int r4 = it / CH, cc = it % CH;
-    Pack<T, 8> rows[4];
+// Transposed LDS tiles are [d][64] with no padding: the 8-byte unit u (4
+// elements) of row d sits at slot u ^ tr_key(d).  A 32-lane 8-byte read of
+// 32 consecutive rows at one u, and a write of rows 8 apart, both touch
+// every bank pair once (tr_key is a bijection on any 16 even or odd rows).
+__device__ __forceinline__ int tr_key(int d) { return ((d >> 1) ^ (d >> 3)) & 15; }
+__device__ __forceinline__ int tr_off(int d, int u) { return d * 64 + ((u ^ tr_key(d)) << 2); }
+
+// A ROWS x D tile of T (row stride `ld` elements in global memory, rows >=
+// valid_rows read as zero), copied in two halves so that the global loads
+// of the next tile are in flight while the current one is multiplied:
+// fetch() issues the loads into registers (each thread 4 rows x 8 columns,
+// four 16-byte loads), put_rm() writes the tile row-major (row stride RLD)
+// and put_tr() transposed (a tr_off() tile, 8-byte writes).
+template <typename T, int ROWS, int D>
+struct TileRegs {
+  static constexpr int CH = D / 8;
+  static constexpr int ITEMS = (ROWS / 4) * CH;
+  static constexpr int PER_THREAD = (ITEMS + 255) / 256;
+  Pack<T, 8> v[PER_THREAD][4];
+
+  __device__ __forceinline__ void fetch(const T* __restrict__ g, int64_t ld, int valid_rows) {
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = r4 * 4 + i;
-      if (r < valid_rows) {
-        rows[i] = *reinterpret_cast<const Pack<T, 8>*>(g + (int64_t)r * ld + cc * 8);
-      } else {
+    for (int q = 0; q < PER_THREAD; ++q) {
+      const int it = q * 256 + threadIdx.x;
+      const int r4 = it / CH, cc = it % CH;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) rows[i].v[j] = (T)0.f;
-      }
-      if (RM) *reinterpret_cast<Pack<T, 8>*>(rm + r * RLD + cc * 8) = rows[i];
-    }
-    if (TR) {
+      for (int i = 0; i < 4; ++i) {
+        const int r = r4 * 4 + i;
+        if (it < ITEMS && r < valid_rows) {
+          v[q][i] = *reinterpret_cast<const Pack<T, 8>*>(g + (int64_t)r * ld + cc * 8);
+        } else {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        Pack<T, 4> col;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) col.v[i] = rows[i].v[j];
-        *reinterpret_cast<Pack<T, 4>*>(tr + (cc * 8 + j) * TLD + r4 * 4) = col;
+          for (int j = 0; j < 8; ++j) v[q][i].v[j] = (T)0.f;
+        }
       }
     }
   }
-}
+
+  template <int RLD>
+  __device__ __forceinline__ void put_rm(T* rm) const {
+#pragma unroll
+    for (int q = 0; q < PER_THREAD; ++q) {
+      const int it = q * 256 + threadIdx.x;
+      if (it >= ITEMS) continue;
+      const int r4 = it / CH, cc = it % CH;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        *reinterpret_cast<Pack<T, 8>*>(rm + (r4 * 4 + i) * RLD + cc * 8) = v[q][i];
+    }
+  }
+
+  // Transposed copy into a tr_off() tile (ROWS must be 64).  A lane writes
+  // its 8 rows in an order keyed on r4's parity, so the two halves of a
+  // 32-lane write cycle land in opposite bank halves.
+  __device__ __forceinline__ void put_tr(T* tr) const {
+    static_assert(ROWS == 64, "transposed tiles are 64 wide");
+#pragma unroll
+    for (int q = 0; q < PER_THREAD; ++q) {
+      const int it = q * 256 + threadIdx.x;
+      if (it >= ITEMS) continue;
+      const int r4 = it / CH, cc = it % CH;
+      const bool odd = (r4 & 1) != 0;
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {
+        // row j = k ^ odd, selected between two compile-time register indices
+        Pack<T, 4> col;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) col.v[i] = odd ? v[q][i].v[k ^ 1] : v[q][i].v[k];
+        *reinterpret_cast<Pack<T, 4>*>(tr + tr_off(cc * 8 + (k ^ (int)odd), r4)) = col;
+      }
+    }
+  }
+};
 
 // Zero rows [D, DP) of a transposed LDS tile (head_dim < 32 pads to 32).
 template <typename T, int D, int DP, int TLD>
@@ -175,9 +213,9 @@ attn_fwd_mfma(FwdArgs a) {
   constexpr int DP = D < 32 ? 32 : D;
   constexpr int MT = DP / 32;
   constexpr int KLD = D + 8;
-  constexpr int VLD = kFwdBN + 8;
-  __shared__ __attribute__((aligned(16))) T K_s[kFwdBN * KLD];
-  __shared__ __attribute__((aligned(16))) T Vt_s[DP * VLD];
+  constexpr int VLD = kFwdBN;  // transposed V: tr_off() layout
+  __shared__ __attribute__((aligned(16))) T K_sb[2][kFwdBN * KLD];
+  __shared__ __attribute__((aligned(16))) T Vt_sb[2][DP * VLD];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31, g = lane >> 5;
@@ -197,7 +235,8 @@ attn_fwd_mfma(FwdArgs a) {
   const float sl2 = a.scale * kLog2e;
 
   if (D < DP) {
-    zero_pad_rows<T, D, DP, VLD>(Vt_s);
+    zero_pad_rows<T, D, DP, VLD>(Vt_sb[0]);
+    zero_pad_rows<T, D, DP, VLD>(Vt_sb[1]);
   }
 
   V qf[KS];
@@ -211,14 +250,23 @@ attn_fwd_mfma(FwdArgs a) {
   float m = -INFINITY, l = 0.f;
 
   const int kv_end = a.causal ? min(a.Tkv, q0 + kFwdBM) : a.Tkv;
-  for (int kv0 = 0; kv0 < kv_end; kv0 += kFwdBN) {
+  // double-buffered: the loads of K/V tile i+1 are in flight during tile i
+  TileRegs<T, kFwdBN, D> kr, vr;
+  if (kv_end > 0) {
+    kr.fetch(kp, a.sk_s, min(kFwdBN, a.Tkv));
+    vr.fetch(vp, a.sv_s, min(kFwdBN, a.Tkv));
+  }
+  for (int kv0 = 0, it = 0; kv0 < kv_end; kv0 += kFwdBN, ++it) {
+    T* K_s = K_sb[it & 1];
+    T* Vt_s = Vt_sb[it & 1];
+    kr.template put_rm<KLD>(K_s);
+    vr.put_tr(Vt_s);
     __syncthreads();
-    const int valid = min(kFwdBN, a.Tkv - kv0);
-    stage_tile<T, kFwdBN, D, KLD, VLD, true, false>(kp + (int64_t)kv0 * a.sk_s, a.sk_s, valid,
-                                                    K_s, nullptr);
-    stage_tile<T, kFwdBN, D, KLD, VLD, false, true>(vp + (int64_t)kv0 * a.sv_s, a.sv_s, valid,
-                                                    nullptr, Vt_s);
-    __syncthreads();
+    if (kv0 + kFwdBN < kv_end) {
+      const int nxt = kv0 + kFwdBN;
+      kr.fetch(kp + (int64_t)nxt * a.sk_s, a.sk_s, min(kFwdBN, a.Tkv - nxt));
+      vr.fetch(vp + (int64_t)nxt * a.sv_s, a.sv_s, min(kFwdBN, a.Tkv - nxt));
+    }
 
     f32x16 s[2];
 #pragma unroll
@@ -274,8 +322,9 @@ attn_fwd_mfma(FwdArgs a) {
       for (int j = 0; j < 8; ++j) pb[j] = (T)s[t >> 1][8 * (t & 1) + j];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const T* vr = Vt_s + (32 * mt + l32) * VLD + 16 * t + 4 * g;
-        o[mt] = M::mma(ld4x2<T>(vr, vr + 8), pb, o[mt]);
+        const int row = 32 * mt + l32;
+        o[mt] = M::mma(ld4x2<T>(Vt_s + tr_off(row, 4 * t + g), Vt_s + tr_off(row, 4 * t + 2 + g)),
+                       pb, o[mt]);
       }
     }
   }
@@ -292,6 +341,209 @@ attn_fwd_mfma(FwdArgs a) {
         if (d0 < D)
           store4<T>(orow + d0, o[mt][4 * rr] * inv, o[mt][4 * rr + 1] * inv,
                     o[mt][4 * rr + 2] * inv, o[mt][4 * rr + 3] * inv);
+      }
+    }
+    if (g == 0) a.lse[(int64_t)bh * a.Tq + qrow] = (m + log2f(lt)) * kLn2;
+  }
+}
+
+// ------------------------------------------------- MFMA forward, v2 (DMA) --
+// One workgroup = 8 wavefronts = 256 query rows of one (batch, head); each
+// wavefront owns 32 query rows (Q in registers) and computes, per 64-row K/V
+// tile, S^T = K Q^T (K fragments: 16-byte LDS reads) and O^T += V^T P^T
+// (V^T fragments: ds_read_b64_tr_b16 transposing reads of the row-major V
+// tile, P^T straight from the S^T accumulators).  K and V tiles arrive by
+// global_load_lds_dwordx4 into two LDS stages (the next tile streams in
+// while the current one is multiplied); rows are XOR-swizzled per tile so
+// that both the 16-byte K reads and the transposing V reads are conflict-free.
+constexpr int kF2Waves = 8;
+constexpr int kF2BM = 32 * kF2Waves;  // query rows per workgroup
+constexpr int kF2BN = 64;             // K/V rows per tile
+
+template <int D>
+struct F2 {
+  static constexpr int RB = D * 2;        // bytes per K/V row (16-bit)
+  static constexpr int GR = RB / 16;      // 16-byte granules per row
+  static constexpr int TILE = kF2BN * RB;  // bytes per K or V tile
+  static constexpr int STAGE = 2 * TILE;  // K + V
+  static constexpr int DMA_ROWS = 1024 / RB;
+  static constexpr int DMA_PER_WAVE = 2 * kF2BN / DMA_ROWS / kF2Waves;
+  static_assert(D == 64 || D == 128, "head_dim");
+  // K tile: a 16-byte read of one granule of 16 consecutive rows (one
+  // 256-byte LDS cycle) touches 16 distinct bank groups.
+  static __device__ __forceinline__ int key_k(int r) {
+    if constexpr (GR == 16) return r & 15;
+    else return (r >> 1) & 7;
+  }
+  // V tile: a transposing read covers 4 consecutive rows x 4 granules per
+  // 32-lane cycle; the key puts each row in its own block of 4 slots.
+  static __device__ __forceinline__ int key_v(int r) {
+    if constexpr (GR == 16) return 4 * (r & 3);
+    else return 4 * ((r >> 1) & 1);
+  }
+};
+
+template <typename T, int D>
+__device__ __forceinline__ void f2_dma(char* stage, const T* kp, const T* vp, int64_t sk,
+                                       int64_t sv, int kv0, int Tkv) {
+  typedef F2<D> P;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int rr = lane / P::GR;
+  const int slot = lane % P::GR;
+#pragma unroll
+  for (int q = 0; q < P::DMA_PER_WAVE; ++q) {
+    const int grp = wave * P::DMA_PER_WAVE + q;  // wave-uniform run of DMA_ROWS rows
+    const int trow = (grp * P::DMA_ROWS) % kF2BN + rr;
+    const bool is_v = grp * P::DMA_ROWS >= kF2BN;
+    const int row = min(kv0 + trow, Tkv - 1);
+    const int c = slot ^ (is_v ? P::key_v(trow) : P::key_k(trow));
+    const T* src = (is_v ? vp + (int64_t)row * sv : kp + (int64_t)row * sk) + c * 8;
+    char* dst = stage + (is_v ? P::TILE : 0) + (grp * P::DMA_ROWS % kF2BN) * P::RB;
+    dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(dst)));
+  }
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(64 * kF2Waves)
+attn_fwd_v2(FwdArgs a) {
+  typedef Mfma<T> M;
+  typedef typename M::V V;
+  typedef F2<D> P;
+  constexpr int KS = D / 16;
+  constexpr int MT = D / 32;
+  __shared__ __attribute__((aligned(1024))) char smem[2 * P::STAGE];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = w / a.n_tiles;
+  const int qt = a.n_tiles - 1 - (w % a.n_tiles);
+  const int b = bh / a.H, h = bh % a.H;
+  const int hk = h / (a.H / a.Hkv);
+  const T* qp = (const T*)a.q + b * a.sq_b + h * a.sq_h;
+  const T* kp = (const T*)a.k + b * a.sk_b + hk * a.sk_h;
+  const T* vp = (const T*)a.v + b * a.sv_b + hk * a.sv_h;
+  T* op = (T*)a.o + b * a.so_b + h * a.so_h;
+  const int q0 = qt * kF2BM;
+  const int qw0 = q0 + wave * 32;
+  const int qrow = qw0 + l32;
+  const bool qvalid = qrow < a.Tq;
+  const float sl2 = a.scale * kLog2e;
+
+  V qf[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s)
+    qf[s] = qvalid ? ld8(qp + (int64_t)qrow * a.sq_s + 16 * s + 8 * g) : zero8<T>();
+
+  f32x16 o[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) o[mt] = zero16();
+  float m = -INFINITY, l = 0.f;
+
+  // transposing-read lane roles: 16-lane group G = lane/16 covers 16 head
+  // dims (half = G & 1) of 4 K/V rows (row block g = G >> 1)
+  const int ts = lane & 15, thalf = (lane >> 4) & 1;
+
+  const int kv_end = a.causal ? min(a.Tkv, q0 + kF2BM) : a.Tkv;
+  const int n_kv = (int)cdiv(kv_end, kF2BN);
+  if (n_kv > 0) f2_dma<T, D>(smem, kp, vp, a.sk_s, a.sv_s, 0, a.Tkv);
+  for (int it = 0; it < n_kv; ++it) {
+    const int kv0 = it * kF2BN;
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (it + 1 < n_kv)
+      f2_dma<T, D>(smem + ((it + 1) & 1) * P::STAGE, kp, vp, a.sk_s, a.sv_s, kv0 + kF2BN, a.Tkv);
+    const char* Ks = smem + (it & 1) * P::STAGE;
+    const char* Vs = Ks + P::TILE;
+    if (a.causal && kv0 > qw0 + 31) continue;  // this wavefront's rows see none of the tile
+
+    f32x16 s[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      s[u] = zero16();
+      const int row = 32 * u + l32;
+#pragma unroll
+      for (int st = 0; st < KS; ++st) {
+        const V kf = *reinterpret_cast<const V*>(Ks + row * P::RB +
+                                                 (((2 * st + g) ^ P::key_k(row)) << 4));
+        s[u] = M::mma(kf, qf[st], s[u]);
+      }
+    }
+    // s[u][r] = S^T[kv0 + 32u + 8(r/4) + 4g + r%4][qrow]
+    const bool need_mask = (kv0 + kF2BN > a.Tkv) || (a.causal && kv0 + kF2BN - 1 > qw0);
+    float mx = -INFINITY;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float x = s[u][r] * sl2;
+        if (need_mask) {
+          const int kv = kv0 + 32 * u + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (kv >= a.Tkv || (a.causal && kv > qrow)) x = -INFINITY;
+        }
+        s[u][r] = x;
+        mx = fmaxf(mx, x);
+      }
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m, mx);
+    const float m_use = m_new == -INFINITY ? 0.f : m_new;
+    const float alpha = exp2f(m - m_use);
+    m = m_new;
+    float rs = 0.f;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = exp2f(s[u][r] - m_use);
+        s[u][r] = p;
+        rs += p;
+      }
+    }
+    l = l * alpha + rs;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) o[mt][r] *= alpha;
+
+#pragma unroll
+    for (int t = 0; t < kF2BN / 16; ++t) {
+      V pb;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pb[j] = (T)s[t >> 1][8 * (t & 1) + j];
+      // V^T fragment: kv rows 16t + 4g + {0..3} and 16t + 8 + 4g + {0..3}
+      const int r1 = 16 * t + 4 * g + (ts >> 2), r2 = r1 + 8;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int c = 4 * mt + 2 * thalf + ((ts & 3) >> 1);
+        const int sub = (ts & 1) * 8;
+        typedef short v4s __attribute__((ext_vector_type(4)));
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4s*)(lds_addr(
+                Vs + r1 * P::RB + ((c ^ P::key_v(r1)) << 4) + sub)));
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) v4s*)(lds_addr(
+                Vs + r2 * P::RB + ((c ^ P::key_v(r2)) << 4) + sub)));
+        // whole-vector bit cast (per-element assembly of 16-bit lanes from the
+        // transposing-read results was miscompiled into lane broadcasts)
+        typedef short v8s __attribute__((ext_vector_type(8)));
+        const V vt = __builtin_bit_cast(V, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+        o[mt] = M::mma(vt, pb, o[mt]);
+      }
+    }
+  }
+
+  const float lt = l + __shfl_xor(l, 32, 64);
+  const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+  if (qvalid) {
+    T* orow = op + (int64_t)qrow * a.so_s;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d0 = 32 * mt + 8 * rr + 4 * g;
+        store4<T>(orow + d0, o[mt][4 * rr] * inv, o[mt][4 * rr + 1] * inv,
+                  o[mt][4 * rr + 2] * inv, o[mt][4 * rr + 3] * inv);
       }
     }
     if (g == 0) a.lse[(int64_t)bh * a.Tq + qrow] = (m + log2f(lt)) * kLn2;
@@ -331,12 +583,12 @@ attn_bwd_dkdv_mfma(BwdArgs a) {
   constexpr int DP = D < 32 ? 32 : D;
   constexpr int MT = DP / 32;
   constexpr int QLD = D + 8;
-  constexpr int TLD = kDkvBM + 8;
-  __shared__ __attribute__((aligned(16))) T Q_s[kDkvBM * QLD];
-  __shared__ __attribute__((aligned(16))) T dO_s[kDkvBM * QLD];
-  __shared__ __attribute__((aligned(16))) T Qt_s[DP * TLD];
-  __shared__ __attribute__((aligned(16))) T dOt_s[DP * TLD];
-  __shared__ float lse_s[kDkvBM], delta_s[kDkvBM];
+  constexpr int TLD = kDkvBM;  // transposed Q, dO: tr_off() layout
+  __shared__ __attribute__((aligned(16))) T Q_sb[2][kDkvBM * QLD];
+  __shared__ __attribute__((aligned(16))) T dO_sb[2][kDkvBM * QLD];
+  __shared__ __attribute__((aligned(16))) T Qt_sb[2][DP * TLD];
+  __shared__ __attribute__((aligned(16))) T dOt_sb[2][DP * TLD];
+  __shared__ float lse_sb[2][kDkvBM], delta_sb[2][kDkvBM];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31, g = lane >> 5;
@@ -353,8 +605,11 @@ attn_bwd_dkdv_mfma(BwdArgs a) {
   const float sl2 = a.scale * kLog2e;
 
   if (D < DP) {
-    zero_pad_rows<T, D, DP, TLD>(Qt_s);
-    zero_pad_rows<T, D, DP, TLD>(dOt_s);
+#pragma unroll
+    for (int b2 = 0; b2 < 2; ++b2) {
+      zero_pad_rows<T, D, DP, TLD>(Qt_sb[b2]);
+      zero_pad_rows<T, D, DP, TLD>(dOt_sb[b2]);
+    }
   }
 
   V kf[KS], vf[KS];
@@ -371,24 +626,47 @@ attn_bwd_dkdv_mfma(BwdArgs a) {
   }
 
   const int q_begin = a.causal ? (kv0 / kDkvBM) * kDkvBM : 0;
-  for (int hq = hk * group; hq < (hk + 1) * group; ++hq) {
-    const T* qp = (const T*)a.q + b * a.sq_b + hq * a.sq_h;
-    const T* dop = (const T*)a.dout + b * a.sdo_b + hq * a.sdo_h;
-    const float* lsep = a.lse + ((int64_t)b * a.H + hq) * a.Tq;
-    const float* delp = a.delta + ((int64_t)b * a.H + hq) * a.Tq;
-    for (int q0 = q_begin; q0 < a.Tq; q0 += kDkvBM) {
-      __syncthreads();
-      const int valid = min(kDkvBM, a.Tq - q0);
-      stage_tile<T, kDkvBM, D, QLD, TLD, true, true>(qp + (int64_t)q0 * a.sq_s, a.sq_s, valid,
-                                                     Q_s, Qt_s);
-      stage_tile<T, kDkvBM, D, QLD, TLD, true, true>(dop + (int64_t)q0 * a.sdo_s, a.sdo_s,
-                                                     valid, dO_s, dOt_s);
+  const int n_q = a.Tq > q_begin ? (int)cdiv(a.Tq - q_begin, kDkvBM) : 0;
+  const int n_steps = n_q * group;  // (query head of the group, query tile) pairs
+  // double-buffered: the loads of step i+1 are in flight during step i
+  TileRegs<T, kDkvBM, D> q_regs, do_regs;
+  float lse_r = INFINITY, del_r = 0.f;
+  auto fetch = [&](int step) {
+    const int hq = hk * group + step / n_q;
+    const int q0 = q_begin + (step % n_q) * kDkvBM;
+    const int valid = min(kDkvBM, a.Tq - q0);
+    const T* qp = (const T*)a.q + b * a.sq_b + hq * a.sq_h + (int64_t)q0 * a.sq_s;
+    const T* dop = (const T*)a.dout + b * a.sdo_b + hq * a.sdo_h + (int64_t)q0 * a.sdo_s;
+    q_regs.fetch(qp, a.sq_s, valid);
+    do_regs.fetch(dop, a.sdo_s, valid);
+    if (threadIdx.x < kDkvBM) {
+      const int qq = q0 + threadIdx.x;
+      const int64_t row = ((int64_t)b * a.H + hq) * a.Tq + qq;
+      lse_r = qq < a.Tq ? a.lse[row] * kLog2e : INFINITY;
+      del_r = qq < a.Tq ? a.delta[row] : 0.f;
+    }
+  };
+  if (n_steps > 0) fetch(0);
+  for (int step = 0; step < n_steps; ++step) {
+    const int q0 = q_begin + (step % n_q) * kDkvBM;
+    const int buf = step & 1;
+    T* Q_s = Q_sb[buf];
+    T* dO_s = dO_sb[buf];
+    T* Qt_s = Qt_sb[buf];
+    T* dOt_s = dOt_sb[buf];
+    float* lse_s = lse_sb[buf];
+    float* delta_s = delta_sb[buf];
+    {
+      q_regs.template put_rm<QLD>(Q_s);
+      q_regs.put_tr(Qt_s);
+      do_regs.template put_rm<QLD>(dO_s);
+      do_regs.put_tr(dOt_s);
       if (threadIdx.x < kDkvBM) {
-        const int qq = q0 + threadIdx.x;
-        lse_s[threadIdx.x] = qq < a.Tq ? lsep[qq] * kLog2e : INFINITY;
-        delta_s[threadIdx.x] = qq < a.Tq ? delp[qq] : 0.f;
+        lse_s[threadIdx.x] = lse_r;
+        delta_s[threadIdx.x] = del_r;
       }
       __syncthreads();
+      if (step + 1 < n_steps) fetch(step + 1);
       if (a.causal && q0 + kDkvBM - 1 < kv0 + wave * 32) continue;  // wave fully masked
 
 #pragma unroll
@@ -420,10 +698,11 @@ attn_bwd_dkdv_mfma(BwdArgs a) {
           }
 #pragma unroll
           for (int mt = 0; mt < MT; ++mt) {
-            const T* dr = dOt_s + (32 * mt + l32) * TLD + 32 * mq + 16 * t + 4 * g;
-            dv[mt] = M::mma(ld4x2<T>(dr, dr + 8), pb, dv[mt]);
-            const T* qr = Qt_s + (32 * mt + l32) * TLD + 32 * mq + 16 * t + 4 * g;
-            dk[mt] = M::mma(ld4x2<T>(qr, qr + 8), db, dk[mt]);
+            const int row = 32 * mt + l32, u = 8 * mq + 4 * t + g;
+            dv[mt] = M::mma(ld4x2<T>(dOt_s + tr_off(row, u), dOt_s + tr_off(row, u + 2)), pb,
+                            dv[mt]);
+            dk[mt] = M::mma(ld4x2<T>(Qt_s + tr_off(row, u), Qt_s + tr_off(row, u + 2)), db,
+                            dk[mt]);
           }
         }
       }
@@ -463,10 +742,10 @@ attn_bwd_dq_mfma(BwdArgs a) {
   constexpr int DP = D < 32 ? 32 : D;
   constexpr int MT = DP / 32;
   constexpr int KLD = D + 8;
-  constexpr int TLD = kDqBN + 8;
-  __shared__ __attribute__((aligned(16))) T K_s[kDqBN * KLD];
-  __shared__ __attribute__((aligned(16))) T V_s[kDqBN * KLD];
-  __shared__ __attribute__((aligned(16))) T Kt_s[DP * TLD];
+  constexpr int TLD = kDqBN;  // transposed K: tr_off() layout
+  __shared__ __attribute__((aligned(16))) T K_sb[2][kDqBN * KLD];
+  __shared__ __attribute__((aligned(16))) T V_sb[2][kDqBN * KLD];
+  __shared__ __attribute__((aligned(16))) T Kt_sb[2][DP * TLD];
 
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31, g = lane >> 5;
@@ -485,7 +764,10 @@ attn_bwd_dq_mfma(BwdArgs a) {
   const bool qvalid = qrow < a.Tq;
   const float sl2 = a.scale * kLog2e;
 
-  if (D < DP) zero_pad_rows<T, D, DP, TLD>(Kt_s);
+  if (D < DP) {
+    zero_pad_rows<T, D, DP, TLD>(Kt_sb[0]);
+    zero_pad_rows<T, D, DP, TLD>(Kt_sb[1]);
+  }
 
   V qf[KS], df[KS];
 #pragma unroll
@@ -501,14 +783,25 @@ attn_bwd_dq_mfma(BwdArgs a) {
   for (int mt = 0; mt < MT; ++mt) dq[mt] = zero16();
 
   const int kv_end = a.causal ? min(a.Tkv, q0 + kDqBM) : a.Tkv;
-  for (int kv0 = 0; kv0 < kv_end; kv0 += kDqBN) {
+  // double-buffered: the loads of K/V tile i+1 are in flight during tile i
+  TileRegs<T, kDqBN, D> k_regs, v_regs;
+  if (kv_end > 0) {
+    k_regs.fetch(kp, a.sk_s, min(kDqBN, a.Tkv));
+    v_regs.fetch(vp, a.sv_s, min(kDqBN, a.Tkv));
+  }
+  for (int kv0 = 0, it = 0; kv0 < kv_end; kv0 += kDqBN, ++it) {
+    T* K_s = K_sb[it & 1];
+    T* V_s = V_sb[it & 1];
+    T* Kt_s = Kt_sb[it & 1];
+    k_regs.template put_rm<KLD>(K_s);
+    k_regs.put_tr(Kt_s);
+    v_regs.template put_rm<KLD>(V_s);
     __syncthreads();
-    const int valid = min(kDqBN, a.Tkv - kv0);
-    stage_tile<T, kDqBN, D, KLD, TLD, true, true>(kp + (int64_t)kv0 * a.sk_s, a.sk_s, valid,
-                                                  K_s, Kt_s);
-    stage_tile<T, kDqBN, D, KLD, TLD, true, false>(vp + (int64_t)kv0 * a.sv_s, a.sv_s, valid,
-                                                   V_s, nullptr);
-    __syncthreads();
+    if (kv0 + kDqBN < kv_end) {
+      const int nxt = kv0 + kDqBN;
+      k_regs.fetch(kp + (int64_t)nxt * a.sk_s, a.sk_s, min(kDqBN, a.Tkv - nxt));
+      v_regs.fetch(vp + (int64_t)nxt * a.sv_s, a.sv_s, min(kDqBN, a.Tkv - nxt));
+    }
     if (a.causal && kv0 > qw0 + 31) continue;  // wave fully masked
 
     f32x16 ds[2];
@@ -536,8 +829,9 @@ attn_bwd_dq_mfma(BwdArgs a) {
       for (int j = 0; j < 8; ++j) db[j] = (T)ds[t >> 1][8 * (t & 1) + j];
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt) {
-        const T* kr = Kt_s + (32 * mt + l32) * TLD + 16 * t + 4 * g;
-        dq[mt] = M::mma(ld4x2<T>(kr, kr + 8), db, dq[mt]);
+        const int row = 32 * mt + l32;
+        dq[mt] = M::mma(ld4x2<T>(Kt_s + tr_off(row, 4 * t + g), Kt_s + tr_off(row, 4 * t + 2 + g)),
+                        db, dq[mt]);
       }
     }
   }
@@ -750,6 +1044,16 @@ int simt_per_lane(int64_t d) {
 
 template <typename T>
 int fwd_mfma(const FwdArgs& a, int64_t D, hipStream_t st) {
+  if (D == 64 || D == 128) {
+    FwdArgs x = a;
+    x.n_tiles = (int)cdiv(a.Tq, kF2BM);
+    const int64_t blocks = (int64_t)x.n_tiles * a.B * a.H;
+    if (D == 128)
+      attn_fwd_v2<T, 128><<<(unsigned)blocks, 64 * kF2Waves, 0, st>>>(x);
+    else
+      attn_fwd_v2<T, 64><<<(unsigned)blocks, 64 * kF2Waves, 0, st>>>(x);
+    return check_launch("attention forward (mfma)");
+  }
   FwdArgs x = a;
   x.n_tiles = (int)cdiv(a.Tq, kFwdBM);
   const int64_t blocks = (int64_t)x.n_tiles * a.B * a.H;

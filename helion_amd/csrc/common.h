@@ -65,6 +65,33 @@ __device__ __forceinline__ float wave_max(float v) {
 
 __host__ __device__ constexpr inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// ---- global -> LDS DMA -----------------------------------------------------
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(lds_void*)p;
+}
+
+// One global_load_lds_dwordx4: lane i's 16 bytes at `g` land at LDS byte
+// lds + 16 i (lds must be wave-uniform).  Issued through inline assembly on
+// purpose: the compiler models a pending LDS DMA by turning every later
+// LDS-read wait into lgkmcnt(0), which serialises fragment reads with the
+// MFMAs they should overlap (the hardware counts the DMA in vmcnt only).
+// Callers wait for it explicitly (wait_vmcnt before the barrier that
+// publishes the tile); VMEM operations the compiler does not see can only
+// make its own in-order vmcnt waits stricter.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
+               : "memory", "m0");
+}
+
+// s_waitcnt with vmcnt = N and the other counters unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline int dtype_size(int dtype) { return dtype == kF32 ? 4 : 2; }

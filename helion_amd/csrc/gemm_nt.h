@@ -33,7 +33,6 @@ namespace gemm {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-typedef __attribute__((address_space(3))) void lds_void;
 
 constexpr int kXcds = 8;
 
@@ -85,13 +84,6 @@ __device__ __forceinline__ int acc_col(int wn, int j, int l32) {
   return wn * C::WTN + 32 * j + l32;
 }
 
-// s_waitcnt with vmcnt = n and the other counters unconstrained (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
 __device__ __forceinline__ int64_t imin(int64_t a, int64_t b) { return a < b ? a : b; }
 
 __device__ __forceinline__ f32x16 zero16() {
@@ -107,22 +99,6 @@ struct Problem {
   int64_t lda, ldb;
   int64_t M, N, K;
 };
-
-// One global_load_lds_dwordx4: lane i's 16 bytes at `g` land at LDS byte
-// lds + 16 i.  Issued through inline assembly on purpose: the compiler models
-// a pending LDS DMA by turning every later LDS-read wait into lgkmcnt(0),
-// which would serialise the fragment reads of step s + 1 with the MFMAs of
-// step s.  Its completion is awaited explicitly (wait_vmcnt before the
-// barrier that publishes the tile); VMEM operations the compiler does not
-// see can only make its own in-order vmcnt waits stricter.
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
-               : "memory", "m0");
-}
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return (uint32_t)(uintptr_t)(lds_void*)p;
-}
 
 // Issue the DMA of K tile k0 of both operands into one LDS stage.
 template <class C, typename T>
