@@ -852,6 +852,327 @@ attn_bwd_dq_mfma(BwdArgs a) {
   }
 }
 
+// ------------------------------------ MFMA backward, head_dim 64 and 128 --
+// Both kernels stage 64-row tiles of Q/dO (dK/dV kernel) or K/V (dQ kernel)
+// in LDS by direct global->LDS DMA, row-major, double-buffered, and read
+// them two ways: as MFMA A operands along rows (16-byte reads of 32 rows)
+// and transposed (ds_read_b64_tr_b16: the A operand of X^T, m = column of
+// X, k = 16 rows of X).  The 16-byte granule c of row r sits at slot
+// c ^ key(r); key makes both reads bank-conflict free:
+//   * 16 consecutive rows at one granule hit 16 distinct 16-byte bank groups
+//     (256-byte rows: key is a bijection of r & 15; 128-byte rows: of
+//     (r >> 1) & 7, rows of opposite parity already use opposite halves);
+//   * 4 consecutive rows x 4 consecutive granules (one 32-lane cycle of a
+//     transposing read) land in 16 distinct groups (bits 3:2 of the key,
+//     bit 2 for 128-byte rows, differ between rows of one parity).
+template <int D>
+struct BTile {
+  static_assert(D == 64 || D == 128, "head_dim");
+  static constexpr int RB = 2 * D;              // bytes per row
+  static constexpr int GR = RB / 16;            // granules per row
+  static constexpr int BYTES = 64 * RB;         // one 64-row tile
+  static constexpr int DMA_ROWS = 1024 / RB;    // rows per wave-wide DMA
+  static constexpr int DMAS = BYTES / 1024;     // wave-wide DMAs per tile
+  static __device__ __forceinline__ int key(int r) {
+    if constexpr (GR == 16) return ((r & 3) << 2) | ((r >> 2) & 3);
+    else return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  }
+  static __device__ __forceinline__ int off(int r, int c) { return r * RB + ((c ^ key(r)) << 4); }
+};
+
+// DMA two 64-row tiles (x rows r0.. of x and y, rows clamped to n_rows - 1)
+// into dst and dst + BYTES, spread over the WAVES wavefronts.
+template <typename T, int D, int WAVES>
+__device__ __forceinline__ void bt_dma2(char* dst, const T* x, int64_t sx, const T* y, int64_t sy,
+                                        int r0, int n_rows) {
+  typedef BTile<D> P;
+  constexpr int PER = 2 * P::DMAS / WAVES;
+  static_assert(PER * WAVES == 2 * P::DMAS, "DMA split");
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int grp = wave * PER + i;
+    const bool second = grp >= P::DMAS;
+    const int part = grp % P::DMAS;
+    const int trow = part * P::DMA_ROWS + lane / P::GR;
+    const int row = min(r0 + trow, n_rows - 1);
+    const int c = (lane % P::GR) ^ P::key(trow);
+    const T* src = (second ? y + (int64_t)row * sy : x + (int64_t)row * sx) + c * 8;
+    dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(dst + (second ? P::BYTES : 0) + part * 1024)));
+  }
+}
+
+// A operand from rows rb + (lane & 31), columns 16 st + 8 (lane >> 5) .. +7.
+template <typename T, int D>
+__device__ __forceinline__ typename Mfma<T>::V bt_row(const char* tile, int rb, int st) {
+  const int lane = threadIdx.x & 63;
+  return *reinterpret_cast<const typename Mfma<T>::V*>(
+      tile + BTile<D>::off(rb + (lane & 31), 2 * st + (lane >> 5)));
+}
+
+// A operand of X^T: m = column 32 mt + (lane & 31) of X, k = rows
+// rb + 4g + {0..3} then rb + 8 + 4g + {0..3} (g = lane >> 5), rb a multiple
+// of 16.  In each 16-lane group, source lane s addresses row (s >> 2) at
+// column 4 (s & 3) of the group's 16 columns; the transposing read hands
+// destination lane j the four rows of column j.
+template <typename T, int D>
+__device__ __forceinline__ typename Mfma<T>::V bt_tr(const char* tile, int rb, int mt) {
+  typedef BTile<D> P;
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63;
+  const int ts = lane & 15, th = (lane >> 4) & 1, g = lane >> 5;
+  const int r1 = rb + 4 * g + (ts >> 2), r2 = r1 + 8;
+  const int c = 4 * mt + 2 * th + ((ts & 3) >> 1);
+  const int sub = (ts & 1) * 8;
+  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(lds_addr(tile + P::off(r1, c) + sub)));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(lds_addr(tile + P::off(r2, c) + sub)));
+  return __builtin_bit_cast(typename Mfma<T>::V,
+                            __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+// dK, dV: a workgroup owns 32 * WAVES kv rows of one (batch, kv head), a
+// wavefront 32 of them (K, V fragments in registers, lane = kv row), and
+// sweeps the 64-row query tiles of every query head of the GQA group that
+// can see them: S = Q K^T and dP = dO V^T from row reads of the Q / dO
+// tiles, dV^T += dO^T P and dK^T += Q^T dS from transposing reads.
+template <typename T, int D, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES)
+attn_bwd_dkdv_v2(BwdArgs a) {
+  typedef Mfma<T> M;
+  typedef typename M::V V;
+  typedef BTile<D> P;
+  constexpr int KS = D / 16;
+  constexpr int MT = D / 32;
+  constexpr int BN = 32 * WAVES;
+  constexpr int STAGE = 2 * P::BYTES + 512;  // Q, dO, lse[64], delta[64]
+  static_assert(WAVES >= 2 && BN % 64 == 0, "waves");
+  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int bhk = w / a.n_tiles;
+  const int kt = w % a.n_tiles;  // kt = 0 sees the most queries: heaviest first
+  const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
+  const int group = a.H / a.Hkv;
+  const int kv0 = kt * BN;
+  const int kvb = kv0 + wave * 32;
+  const int kvw = kvb + l32;  // this lane's kv row (MFMA column)
+  const bool kvvalid = kvw < a.Tkv;
+  const T* kp = (const T*)a.k + b * a.sk_b + hk * a.sk_h;
+  const T* vp = (const T*)a.v + b * a.sv_b + hk * a.sv_h;
+  const float sl2 = a.scale * kLog2e;
+
+  V kf[KS], vf[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    kf[s] = kvvalid ? ld8(kp + (int64_t)kvw * a.sk_s + 16 * s + 8 * g) : zero8<T>();
+    vf[s] = kvvalid ? ld8(vp + (int64_t)kvw * a.sv_s + 16 * s + 8 * g) : zero8<T>();
+  }
+  f32x16 dv[MT], dk[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+    dv[mt] = zero16();
+    dk[mt] = zero16();
+  }
+
+  const int q_begin = a.causal ? kv0 : 0;  // top-left causal: rows < kv0 see none
+  const int n_q = a.Tq > q_begin ? (int)cdiv(a.Tq - q_begin, 64) : 0;
+  const int n_steps = n_q * group;  // (query head of the group, query tile) pairs
+  auto issue = [&](int step, char* stage) {
+    const int hq = hk * group + step / n_q;
+    const int q0 = q_begin + (step % n_q) * 64;
+    const T* qp = (const T*)a.q + b * a.sq_b + hq * a.sq_h;
+    const T* dop = (const T*)a.dout + b * a.sdo_b + hq * a.sdo_h;
+    bt_dma2<T, D, WAVES>(stage, qp, a.sq_s, dop, a.sdo_s, q0, a.Tq);
+    const int64_t row = ((int64_t)b * a.H + hq) * a.Tq + min(q0 + lane, a.Tq - 1);
+    if (wave == 0) dma4(a.lse + row, __builtin_amdgcn_readfirstlane(lds_addr(stage + 2 * P::BYTES)));
+    if (wave == 1)
+      dma4(a.delta + row, __builtin_amdgcn_readfirstlane(lds_addr(stage + 2 * P::BYTES + 256)));
+  };
+  if (n_steps > 0) issue(0, smem);
+  for (int step = 0; step < n_steps; ++step) {
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (step + 1 < n_steps) issue(step + 1, smem + ((step + 1) & 1) * STAGE);
+    const int q0 = q_begin + (step % n_q) * 64;
+    if (a.causal && q0 + 63 < kvb) continue;  // this wavefront's kv rows see none of the tile
+    const char* Qs = smem + (step & 1) * STAGE;
+    const char* dOs = Qs + P::BYTES;
+    const float* lse_s = reinterpret_cast<const float*>(Qs + 2 * P::BYTES);
+    const float* del_s = lse_s + 64;
+    const bool need_mask = (a.causal && q0 < kvb + 31) || q0 + 64 > a.Tq;
+
+#pragma unroll
+    for (int mq = 0; mq < 2; ++mq) {
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int st = 0; st < KS; ++st) {
+        s = M::mma(bt_row<T, D>(Qs, 32 * mq, st), kf[st], s);
+        dp = M::mma(bt_row<T, D>(dOs, 32 * mq, st), vf[st], dp);
+      }
+      // s[r] = S[q0 + 32mq + 8(r/4) + 4g + r%4][kvw]
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int qi = 32 * mq + 8 * rr + 4 * g;
+        const float4 L = *reinterpret_cast<const float4*>(lse_s + qi);
+        const float4 Dl = *reinterpret_cast<const float4*>(del_s + qi);
+        const float lv[4] = {L.x, L.y, L.z, L.w};
+        const float dlv[4] = {Dl.x, Dl.y, Dl.z, Dl.w};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int r = 4 * rr + j;
+          float p = exp2f(s[r] * sl2 - lv[j] * kLog2e);
+          if (need_mask) {
+            const int q = q0 + qi + j;
+            if (q >= a.Tq || (a.causal && kvw > q)) p = 0.f;
+          }
+          s[r] = p;
+          dp[r] = p * (dp[r] - dlv[j]);
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        V pb, db;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          pb[j] = (T)s[8 * t + j];
+          db[j] = (T)dp[8 * t + j];
+        }
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) {
+          dv[mt] = M::mma(bt_tr<T, D>(dOs, 32 * mq + 16 * t, mt), pb, dv[mt]);
+          dk[mt] = M::mma(bt_tr<T, D>(Qs, 32 * mq + 16 * t, mt), db, dk[mt]);
+        }
+      }
+    }
+  }
+
+  if (kvvalid) {
+    T* dkr = (T*)a.dk + b * a.sdk_b + hk * a.sdk_h + (int64_t)kvw * a.sdk_s;
+    T* dvr = (T*)a.dv + b * a.sdv_b + hk * a.sdv_h + (int64_t)kvw * a.sdv_s;
+    const float sc = a.scale;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d0 = 32 * mt + 8 * rr + 4 * g;
+        store4<T>(dkr + d0, dk[mt][4 * rr] * sc, dk[mt][4 * rr + 1] * sc,
+                  dk[mt][4 * rr + 2] * sc, dk[mt][4 * rr + 3] * sc);
+        store4<T>(dvr + d0, dv[mt][4 * rr], dv[mt][4 * rr + 1], dv[mt][4 * rr + 2],
+                  dv[mt][4 * rr + 3]);
+      }
+    }
+  }
+}
+
+// dQ: a workgroup owns 32 * WAVES query rows of one (batch, head), a
+// wavefront 32 of them (Q, dO fragments in registers, lane = query row),
+// and sweeps the 64-row K/V tiles it can see: S^T = K Q^T and
+// dP^T = V dO^T from row reads, dQ^T += K^T dS^T from transposing reads.
+template <typename T, int D, int WAVES>
+__global__ void __launch_bounds__(64 * WAVES)
+attn_bwd_dq_v2(BwdArgs a) {
+  typedef Mfma<T> M;
+  typedef typename M::V V;
+  typedef BTile<D> P;
+  constexpr int KS = D / 16;
+  constexpr int MT = D / 32;
+  constexpr int BM = 32 * WAVES;
+  constexpr int STAGE = 2 * P::BYTES;  // K, V
+  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = w / a.n_tiles;
+  const int qt = a.n_tiles - 1 - (w % a.n_tiles);  // most kv tiles first
+  const int b = bh / a.H, h = bh % a.H;
+  const int hk = h / (a.H / a.Hkv);
+  const T* qp = (const T*)a.q + b * a.sq_b + h * a.sq_h;
+  const T* dop = (const T*)a.dout + b * a.sdo_b + h * a.sdo_h;
+  const T* kp = (const T*)a.k + b * a.sk_b + hk * a.sk_h;
+  const T* vp = (const T*)a.v + b * a.sv_b + hk * a.sv_h;
+  const int q0 = qt * BM;
+  const int qw0 = q0 + wave * 32;
+  const int qrow = qw0 + l32;
+  const bool qvalid = qrow < a.Tq;
+  const float sl2 = a.scale * kLog2e;
+
+  V qf[KS], df[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    qf[s] = qvalid ? ld8(qp + (int64_t)qrow * a.sq_s + 16 * s + 8 * g) : zero8<T>();
+    df[s] = qvalid ? ld8(dop + (int64_t)qrow * a.sdo_s + 16 * s + 8 * g) : zero8<T>();
+  }
+  const float lse2 = qvalid ? a.lse[(int64_t)bh * a.Tq + qrow] * kLog2e : INFINITY;
+  const float dl = qvalid ? a.delta[(int64_t)bh * a.Tq + qrow] : 0.f;
+
+  f32x16 dq[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) dq[mt] = zero16();
+
+  const int kv_end = a.causal ? min(a.Tkv, q0 + BM) : a.Tkv;
+  const int n_kv = (int)cdiv(kv_end, 64);
+  if (n_kv > 0) bt_dma2<T, D, WAVES>(smem, kp, a.sk_s, vp, a.sv_s, 0, a.Tkv);
+  for (int it = 0; it < n_kv; ++it) {
+    const int kv0 = it * 64;
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (it + 1 < n_kv)
+      bt_dma2<T, D, WAVES>(smem + ((it + 1) & 1) * STAGE, kp, a.sk_s, vp, a.sv_s, kv0 + 64, a.Tkv);
+    if (a.causal && kv0 > qw0 + 31) continue;  // this wavefront's rows see none of the tile
+    const char* Ks = smem + (it & 1) * STAGE;
+    const char* Vs = Ks + P::BYTES;
+    const bool need_mask = kv0 + 64 > a.Tkv || (a.causal && kv0 + 63 > qw0);
+
+    f32x16 ds[2];
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      f32x16 s = zero16(), dp = zero16();
+#pragma unroll
+      for (int st = 0; st < KS; ++st) {
+        s = M::mma(bt_row<T, D>(Ks, 32 * u, st), qf[st], s);
+        dp = M::mma(bt_row<T, D>(Vs, 32 * u, st), df[st], dp);
+      }
+      // s[r] = S^T[kv0 + 32u + 8(r/4) + 4g + r%4][qrow]
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        float p = exp2f(s[r] * sl2 - lse2);
+        if (need_mask) {
+          const int kv = kv0 + 32 * u + 8 * (r >> 2) + 4 * g + (r & 3);
+          if (kv >= a.Tkv || (a.causal && kv > qrow)) p = 0.f;
+        }
+        ds[u][r] = p * (dp[r] - dl);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      V db;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) db[j] = (T)ds[t >> 1][8 * (t & 1) + j];
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) dq[mt] = M::mma(bt_tr<T, D>(Ks, 16 * t, mt), db, dq[mt]);
+    }
+  }
+
+  if (qvalid) {
+    T* dqr = (T*)a.dq + b * a.sdq_b + h * a.sdq_h + (int64_t)qrow * a.sdq_s;
+    const float sc = a.scale;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d0 = 32 * mt + 8 * rr + 4 * g;
+        store4<T>(dqr + d0, dq[mt][4 * rr] * sc, dq[mt][4 * rr + 1] * sc,
+                  dq[mt][4 * rr + 2] * sc, dq[mt][4 * rr + 3] * sc);
+      }
+    }
+  }
+}
+
 // --------------------------------------------------------------- SIMT path --
 // One wavefront per row; lane i owns head-dim entries i, i+64, ...
 constexpr int kSimtMaxPerLane = 16;  // head_dim <= 1024
@@ -1072,8 +1393,31 @@ int fwd_simt(const FwdArgs& a, int64_t D, hipStream_t st) {
   return check_launch("attention forward (simt)");
 }
 
+#ifndef TRI_ATTN_DKDV_WAVES
+#define TRI_ATTN_DKDV_WAVES 4
+#endif
+#ifndef TRI_ATTN_DQ_WAVES
+#define TRI_ATTN_DQ_WAVES 8
+#endif
+
+template <typename T, int D>
+int bwd_v2(const BwdArgs& a, hipStream_t st) {
+  constexpr int WK = TRI_ATTN_DKDV_WAVES, WQ = TRI_ATTN_DQ_WAVES;
+  BwdArgs x = a;
+  x.n_tiles = (int)cdiv(a.Tkv, 32 * WK);
+  const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;
+  attn_bwd_dkdv_v2<T, D, WK><<<(unsigned)kv_blocks, 64 * WK, 0, st>>>(x);
+  if (int e = check_launch("attention backward (dk/dv, mfma)")) return e;
+  x.n_tiles = (int)cdiv(a.Tq, 32 * WQ);
+  const int64_t q_blocks = (int64_t)x.n_tiles * a.B * a.H;
+  attn_bwd_dq_v2<T, D, WQ><<<(unsigned)q_blocks, 64 * WQ, 0, st>>>(x);
+  return check_launch("attention backward (dq, mfma)");
+}
+
 template <typename T>
 int bwd_mfma(const BwdArgs& a, int64_t D, hipStream_t st) {
+  if (D == 128) return bwd_v2<T, 128>(a, st);
+  if (D == 64) return bwd_v2<T, 64>(a, st);
   BwdArgs x = a;
   x.n_tiles = (int)cdiv(a.Tkv, kDkvBN);
   const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;

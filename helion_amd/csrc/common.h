@@ -85,6 +85,12 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
                : "memory", "m0");
 }
 
+// Same with 4 bytes per lane: lane i's dword lands at LDS byte lds + 4 i.
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds)
+               : "memory", "m0");
+}
+
 // s_waitcnt with vmcnt = N and the other counters unconstrained (gfx9 encoding).
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {

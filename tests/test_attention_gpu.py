@@ -90,6 +90,13 @@ def test_attention_large_head_bf16_t1024():
     _check(torch.bfloat16, 1, 2, 2, 1024, 1024, 128, True, seed=13)
 
 
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_gqa_many_tiles_ragged(causal):
+    # several kv and query workgroups per head, GQA group of 4, length not a tile multiple
+    _check(torch.bfloat16, 1, 8, 2, 700, 700, 128, causal, seed=14)
+    _check(torch.float16, 2, 4, 1, 333, 333, 64, causal, seed=15)
+
+
 def test_attention_invariants():
     # T = 1 -> o = v; causal row 0 -> o[0] = v[0]; uniform v rows -> o = v
     q = randn((1, 2, 1, 64), torch.bfloat16, 1)
