@@ -297,14 +297,14 @@ attn_fwd_mfma(FwdArgs a) {
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     const float m_new = fmaxf(m, mx);
     const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2f(m - m_use);
+    const float alpha = fast_exp2(m - m_use);
     m = m_new;
     float rs = 0.f;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = exp2f(s[u][r] - m_use);
+        const float p = fast_exp2(s[u][r] - m_use);
         s[u][r] = p;
         rs += p;
       }
@@ -471,40 +471,46 @@ attn_fwd_v2(FwdArgs a) {
     }
     // s[u][r] = S^T[kv0 + 32u + 8(r/4) + 4g + r%4][qrow]
     const bool need_mask = (kv0 + kF2BN > a.Tkv) || (a.causal && kv0 + kF2BN - 1 > qw0);
+    if (need_mask) {
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kv = kv0 + 32 * u + 8 * (r >> 2) + 4 * g + (r & 3);
+          s[u][r] = (kv >= a.Tkv || (a.causal && kv > qrow)) ? -INFINITY : s[u][r];
+        }
+      }
+    }
+    // row max of the raw scores (the scale is positive), in log2 units
     float mx = -INFINITY;
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < 2; ++u)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = s[u][r] * sl2;
-        if (need_mask) {
-          const int kv = kv0 + 32 * u + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (kv >= a.Tkv || (a.causal && kv > qrow)) x = -INFINITY;
-        }
-        s[u][r] = x;
-        mx = fmaxf(mx, x);
-      }
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[u][r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sl2;
+    // Lazy rescaling: the reference point m of o and l only moves when some
+    // row's max exceeds it by more than 8 (so every p <= 2^8); o / l and
+    // lse = m + log2 l do not depend on which m is used.
+    if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
+      const float m_new = fmaxf(m, mx);
+      const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m - m_new);
+      m = m_new;
+      l *= alpha;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[mt][r] *= alpha;
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-    const float m_new = fmaxf(m, mx);
-    const float m_use = m_new == -INFINITY ? 0.f : m_new;
-    const float alpha = exp2f(m - m_use);
-    m = m_new;
-    float rs = 0.f;
+    const float nm = m == -INFINITY ? 0.f : -m;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = exp2f(s[u][r] - m_use);
+        const float p = fast_exp2(fmaf(s[u][r], sl2, nm));
         s[u][r] = p;
-        rs += p;
+        l += p;
       }
     }
-    l = l * alpha + rs;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) o[mt][r] *= alpha;
 
 #pragma unroll
     for (int t = 0; t < kF2BN / 16; ++t) {
@@ -683,7 +689,7 @@ attn_bwd_dkdv_mfma(BwdArgs a) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int qi = 32 * mq + 8 * (r >> 2) + 4 * g + (r & 3);
-          float p = exp2f(s[r] * sl2 - lse_s[qi]);
+          float p = fast_exp2(s[r] * sl2 - lse_s[qi]);
           if (!kvvalid || (a.causal && kvw > q0 + qi)) p = 0.f;
           s[r] = p;
           dp[r] = p * (dp[r] - delta_s[qi]);
@@ -817,7 +823,7 @@ attn_bwd_dq_mfma(BwdArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int kv = kv0 + 32 * u + 8 * (r >> 2) + 4 * g + (r & 3);
-        float p = exp2f(s[r] * sl2 - lse2);
+        float p = fast_exp2(s[r] * sl2 - lse2);
         if (kv >= a.Tkv || (a.causal && kv > qrow)) p = 0.f;
         ds[u][r] = p * (dp[r] - dl);
       }
@@ -932,6 +938,13 @@ __device__ __forceinline__ typename Mfma<T>::V bt_tr(const char* tile, int rb, i
                             __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
+// Scheduling fence: the compiler keeps every instruction on its side.
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+#ifndef TRI_DKDV_FENCES
+#define TRI_DKDV_FENCES 1
+#endif
+
 // dK, dV: a workgroup owns 32 * WAVES kv rows of one (batch, kv head), a
 // wavefront 32 of them (K, V fragments in registers, lane = kv row), and
 // sweeps the 64-row query tiles of every query head of the GQA group that
@@ -1013,26 +1026,30 @@ attn_bwd_dkdv_v2(BwdArgs a) {
         s = M::mma(bt_row<T, D>(Qs, 32 * mq, st), kf[st], s);
         dp = M::mma(bt_row<T, D>(dOs, 32 * mq, st), vf[st], dp);
       }
+      // phases are fenced so that no more than one phase's LDS fragments
+      // are live at a time (the wavefront's registers hold K, V, dK, dV)
+      if (TRI_DKDV_FENCES) sched_fence();
       // s[r] = S[q0 + 32mq + 8(r/4) + 4g + r%4][kvw]
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int qi = 32 * mq + 8 * rr + 4 * g;
         const float4 L = *reinterpret_cast<const float4*>(lse_s + qi);
         const float4 Dl = *reinterpret_cast<const float4*>(del_s + qi);
-        const float lv[4] = {L.x, L.y, L.z, L.w};
+        const float lv[4] = {L.x * kLog2e, L.y * kLog2e, L.z * kLog2e, L.w * kLog2e};
         const float dlv[4] = {Dl.x, Dl.y, Dl.z, Dl.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int r = 4 * rr + j;
-          float p = exp2f(s[r] * sl2 - lv[j] * kLog2e);
+          float p = fast_exp2(fmaf(s[r], sl2, -lv[j]));
           if (need_mask) {
             const int q = q0 + qi + j;
-            if (q >= a.Tq || (a.causal && kvw > q)) p = 0.f;
+            p = (q >= a.Tq || (a.causal && kvw > q)) ? 0.f : p;
           }
           s[r] = p;
           dp[r] = p * (dp[r] - dlv[j]);
         }
       }
+      if (TRI_DKDV_FENCES) sched_fence();
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         V pb, db;
@@ -1047,6 +1064,7 @@ attn_bwd_dkdv_v2(BwdArgs a) {
           dk[mt] = M::mma(bt_tr<T, D>(Qs, 32 * mq + 16 * t, mt), db, dk[mt]);
         }
       }
+      if (TRI_DKDV_FENCES) sched_fence();
     }
   }
 
@@ -1140,10 +1158,10 @@ attn_bwd_dq_v2(BwdArgs a) {
       // s[r] = S^T[kv0 + 32u + 8(r/4) + 4g + r%4][qrow]
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float p = exp2f(s[r] * sl2 - lse2);
+        float p = fast_exp2(fmaf(s[r], sl2, -lse2));
         if (need_mask) {
           const int kv = kv0 + 32 * u + 8 * (r >> 2) + 4 * g + (r & 3);
-          if (kv >= a.Tkv || (a.causal && kv > qrow)) p = 0.f;
+          p = (kv >= a.Tkv || (a.causal && kv > qrow)) ? 0.f : p;
         }
         ds[u][r] = p * (dp[r] - dl);
       }

@@ -63,6 +63,11 @@ __device__ __forceinline__ float wave_max(float v) {
   return v;
 }
 
+// 2^x as one v_exp_f32.  exp2f() wraps it in a range reduction (compare,
+// two selects, add, ldexp) that keeps results below 2^-126 exact; softmax
+// weights that small are negligible, and exp2(-inf) = 0 either way.
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 __host__ __device__ constexpr inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // ---- global -> LDS DMA -----------------------------------------------------

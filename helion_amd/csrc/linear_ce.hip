@@ -114,7 +114,7 @@ lce_fwd_kernel(FwdArgs a) {
     for (int i = 0; i < C::MT; ++i)
 #pragma unroll
       for (int r = 0; r < 16; ++r)
-        if (v0 + acc_row<C>(wm, i, r, g) < a.V) s += exp2f(acc.t[i][j][r] * kLog2e - ms);
+        if (v0 + acc_row<C>(wm, i, r, g) < a.V) s += fast_exp2(acc.t[i][j][r] * kLog2e - ms);
     s += __shfl_xor(s, 32, 64);
     if (g == 0) red[wm][col] = s;
     // the target logit: written by the single lane that holds its row
@@ -157,7 +157,7 @@ fill_f32(float* __restrict__ p, int64_t n, float value) {
 __device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2) {
   const float mn = fmaxf(m, m2);
   if (mn == -INFINITY) return;
-  s = s * exp2f((m - mn) * kLog2e) + s2 * exp2f((m2 - mn) * kLog2e);
+  s = s * fast_exp2((m - mn) * kLog2e) + s2 * fast_exp2((m2 - mn) * kLog2e);
   m = mn;
 }
 
@@ -303,7 +303,7 @@ lce_g_kernel(GArgs a) {
         float gv[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const float pr = exp2f(acc.t[i][j][4 * rr + e] * kLog2e - l2);
+          const float pr = fast_exp2(acc.t[i][j][4 * rr + e] * kLog2e - l2);
           gv[e] = (pr - (vb + e == tl ? 1.f : 0.f)) * coef;
         }
         if (gt != nullptr) {
