@@ -217,7 +217,7 @@ attn_fwd_mfma(FwdArgs a) {
   __shared__ __attribute__((aligned(16))) T K_sb[2][kFwdBN * KLD];
   __shared__ __attribute__((aligned(16))) T Vt_sb[2][DP * VLD];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int l32 = lane & 31, g = lane >> 5;
   const int w = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = w / a.n_tiles;
@@ -387,7 +387,7 @@ template <typename T, int D>
 __device__ __forceinline__ void f2_dma(char* stage, const T* kp, const T* vp, int64_t sk,
                                        int64_t sv, int kv0, int Tkv) {
   typedef F2<D> P;
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int rr = lane / P::GR;
   const int slot = lane % P::GR;
 #pragma unroll
@@ -413,7 +413,7 @@ attn_fwd_v2(FwdArgs a) {
   constexpr int MT = D / 32;
   __shared__ __attribute__((aligned(1024))) char smem[2 * P::STAGE];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int l32 = lane & 31, g = lane >> 5;
   const int w = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = w / a.n_tiles;
@@ -596,7 +596,7 @@ attn_bwd_dkdv_mfma(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) T dOt_sb[2][DP * TLD];
   __shared__ float lse_sb[2][kDkvBM], delta_sb[2][kDkvBM];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int l32 = lane & 31, g = lane >> 5;
   const int w = xcd_remap(blockIdx.x, gridDim.x);
   const int bhk = w / a.n_tiles;
@@ -753,7 +753,7 @@ attn_bwd_dq_mfma(BwdArgs a) {
   __shared__ __attribute__((aligned(16))) T V_sb[2][kDqBN * KLD];
   __shared__ __attribute__((aligned(16))) T Kt_sb[2][DP * TLD];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int l32 = lane & 31, g = lane >> 5;
   const int w = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = w / a.n_tiles;
@@ -894,7 +894,7 @@ __device__ __forceinline__ void bt_dma2(char* dst, const T* x, int64_t sx, const
   typedef BTile<D> P;
   constexpr int PER = 2 * P::DMAS / WAVES;
   static_assert(PER * WAVES == 2 * P::DMAS, "DMA split");
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
 #pragma unroll
   for (int i = 0; i < PER; ++i) {
     const int grp = wave * PER + i;
@@ -907,6 +907,47 @@ __device__ __forceinline__ void bt_dma2(char* dst, const T* x, int64_t sx, const
     dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(dst + (second ? P::BYTES : 0) + part * 1024)));
   }
 }
+
+// bt_dma2 for the steady state: each lane's byte offsets from a tile's first
+// row are computed once (init), a full tile then costs one scalar base per
+// tensor and no per-lane address arithmetic; a tile that reaches past
+// n_rows falls back to bt_dma2's clamped rows.
+template <typename T, int D, int WAVES>
+struct BtDma {
+  typedef BTile<D> P;
+  static constexpr int PER = 2 * P::DMAS / WAVES;
+  uint32_t off[PER];
+  bool fast;
+  __device__ __forceinline__ void init(int64_t sx, int64_t sy) {
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    fast = (int64_t)64 * (sx > sy ? sx : sy) * (int64_t)sizeof(T) < ((int64_t)1 << 31);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int grp = wave * PER + i;
+      const int trow = (grp % P::DMAS) * P::DMA_ROWS + lane / P::GR;
+      const int c = (lane % P::GR) ^ P::key(trow);
+      off[i] = fast ? (uint32_t)((trow * (grp >= P::DMAS ? sy : sx) + c * 8) * (int64_t)sizeof(T)) : 0u;
+    }
+  }
+  __device__ __forceinline__ void issue(char* dst, const T* x, int64_t sx, const T* y, int64_t sy,
+                                        int r0, int n_rows) const {
+    if (fast && r0 + 64 <= n_rows) {
+      const int wave = wave_id();
+      const T* bx = x + (int64_t)r0 * sx;
+      const T* by = y + (int64_t)r0 * sy;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int grp = wave * PER + i;
+        const bool second = grp >= P::DMAS;
+        dma16s(second ? by : bx, off[i],
+               __builtin_amdgcn_readfirstlane(
+                   lds_addr(dst + (second ? P::BYTES : 0) + (grp % P::DMAS) * 1024)));
+      }
+    } else {
+      bt_dma2<T, D, WAVES>(dst, x, sx, y, sy, r0, n_rows);
+    }
+  }
+};
 
 // A operand from rows rb + (lane & 31), columns 16 st + 8 (lane >> 5) .. +7.
 template <typename T, int D>
@@ -941,8 +982,17 @@ __device__ __forceinline__ typename Mfma<T>::V bt_tr(const char* tile, int rb, i
 // Scheduling fence: the compiler keeps every instruction on its side.
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
+// Pin a loop-carried value to AGPRs (pin_agpr) or VGPRs (pin_vgpr) at the
+// top of each iteration.  Without it the register allocator may home an
+// MFMA accumulator in the other register file and copy it into and out of
+// the MFMA's registers every iteration.  Emits no instruction.
+template <typename X>
+__device__ __forceinline__ void pin_agpr(X& x) { asm volatile("" : "+a"(x)); }
+template <typename X>
+__device__ __forceinline__ void pin_vgpr(X& x) { asm volatile("" : "+v"(x)); }
+
 #ifndef TRI_DKDV_FENCES
-#define TRI_DKDV_FENCES 1
+#define TRI_DKDV_FENCES 0
 #endif
 
 // dK, dV: a workgroup owns 32 * WAVES kv rows of one (batch, kv head), a
@@ -963,7 +1013,7 @@ attn_bwd_dkdv_v2(BwdArgs a) {
   static_assert(WAVES >= 2 && BN % 64 == 0, "waves");
   __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int l32 = lane & 31, g = lane >> 5;
   const int w = xcd_remap(blockIdx.x, gridDim.x);
   const int bhk = w / a.n_tiles;
@@ -994,12 +1044,14 @@ attn_bwd_dkdv_v2(BwdArgs a) {
   const int q_begin = a.causal ? kv0 : 0;  // top-left causal: rows < kv0 see none
   const int n_q = a.Tq > q_begin ? (int)cdiv(a.Tq - q_begin, 64) : 0;
   const int n_steps = n_q * group;  // (query head of the group, query tile) pairs
+  BtDma<T, D, WAVES> dma;
+  dma.init(a.sq_s, a.sdo_s);
   auto issue = [&](int step, char* stage) {
     const int hq = hk * group + step / n_q;
     const int q0 = q_begin + (step % n_q) * 64;
     const T* qp = (const T*)a.q + b * a.sq_b + hq * a.sq_h;
     const T* dop = (const T*)a.dout + b * a.sdo_b + hq * a.sdo_h;
-    bt_dma2<T, D, WAVES>(stage, qp, a.sq_s, dop, a.sdo_s, q0, a.Tq);
+    dma.issue(stage, qp, a.sq_s, dop, a.sdo_s, q0, a.Tq);
     const int64_t row = ((int64_t)b * a.H + hq) * a.Tq + min(q0 + lane, a.Tq - 1);
     if (wave == 0) dma4(a.lse + row, __builtin_amdgcn_readfirstlane(lds_addr(stage + 2 * P::BYTES)));
     if (wave == 1)
@@ -1007,6 +1059,17 @@ attn_bwd_dkdv_v2(BwdArgs a) {
   };
   if (n_steps > 0) issue(0, smem);
   for (int step = 0; step < n_steps; ++step) {
+    // 4 wavefronts: 512 registers, accumulators and K/V fragments in AGPRs
+    // (MFMA operands), VGPRs left to the softmax; 8 wavefronts: 256, VGPRs
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      if constexpr (WAVES <= 4) { pin_agpr(dv[mt]); pin_agpr(dk[mt]); }
+      else { pin_vgpr(dv[mt]); pin_vgpr(dk[mt]); }
+    }
+    if constexpr (WAVES <= 4) {
+#pragma unroll
+      for (int st = 0; st < KS; ++st) { pin_agpr(kf[st]); pin_agpr(vf[st]); }
+    }
     wait_vmcnt<0>();
     __syncthreads();
     if (step + 1 < n_steps) issue(step + 1, smem + ((step + 1) & 1) * STAGE);
@@ -1029,7 +1092,14 @@ attn_bwd_dkdv_v2(BwdArgs a) {
       // phases are fenced so that no more than one phase's LDS fragments
       // are live at a time (the wavefront's registers hold K, V, dK, dV)
       if (TRI_DKDV_FENCES) sched_fence();
-      // s[r] = S[q0 + 32mq + 8(r/4) + 4g + r%4][kvw]
+      // s[r] = S[q0 + 32mq + 8(r/4) + 4g + r%4][kvw]; masked scores -> -inf (p = 0)
+      if (need_mask) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int q = q0 + 32 * mq + 8 * (r >> 2) + 4 * g + (r & 3);
+          s[r] = (q >= a.Tq || (a.causal && kvw > q)) ? -INFINITY : s[r];
+        }
+      }
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int qi = 32 * mq + 8 * rr + 4 * g;
@@ -1040,11 +1110,7 @@ attn_bwd_dkdv_v2(BwdArgs a) {
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const int r = 4 * rr + j;
-          float p = fast_exp2(fmaf(s[r], sl2, -lv[j]));
-          if (need_mask) {
-            const int q = q0 + qi + j;
-            p = (q >= a.Tq || (a.causal && kvw > q)) ? 0.f : p;
-          }
+          const float p = fast_exp2(fmaf(s[r], sl2, -lv[j]));
           s[r] = p;
           dp[r] = p * (dp[r] - dlv[j]);
         }
@@ -1102,7 +1168,7 @@ attn_bwd_dq_v2(BwdArgs a) {
   constexpr int STAGE = 2 * P::BYTES;  // K, V
   __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
 
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lane = threadIdx.x & 63, wave = wave_id();
   const int l32 = lane & 31, g = lane >> 5;
   const int w = xcd_remap(blockIdx.x, gridDim.x);
   const int bh = w / a.n_tiles;
@@ -1126,7 +1192,20 @@ attn_bwd_dq_v2(BwdArgs a) {
     df[s] = qvalid ? ld8(dop + (int64_t)qrow * a.sdo_s + 16 * s + 8 * g) : zero8<T>();
   }
   const float lse2 = qvalid ? a.lse[(int64_t)bh * a.Tq + qrow] * kLog2e : INFINITY;
-  const float dl = qvalid ? a.delta[(int64_t)bh * a.Tq + qrow] : 0.f;
+  // delta = rowsum(dO * O) for this lane's query row (the two lanes of a row
+  // hold alternate 8-column halves); written out for the dK/dV kernel
+  float dl = 0.f;
+  if (qvalid) {
+    const T* orow = (const T*)a.o + b * a.so_b + h * a.so_h + (int64_t)qrow * a.so_s;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const V of = ld8(orow + 16 * s + 8 * g);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dl += (float)df[s][j] * (float)of[j];
+    }
+  }
+  dl += __shfl_xor(dl, 32, 64);
+  if (qvalid && g == 0) a.delta[(int64_t)bh * a.Tq + qrow] = dl;
 
   f32x16 dq[MT];
 #pragma unroll
@@ -1134,13 +1213,17 @@ attn_bwd_dq_v2(BwdArgs a) {
 
   const int kv_end = a.causal ? min(a.Tkv, q0 + BM) : a.Tkv;
   const int n_kv = (int)cdiv(kv_end, 64);
-  if (n_kv > 0) bt_dma2<T, D, WAVES>(smem, kp, a.sk_s, vp, a.sv_s, 0, a.Tkv);
+  BtDma<T, D, WAVES> dma;
+  dma.init(a.sk_s, a.sv_s);
+  if (n_kv > 0) dma.issue(smem, kp, a.sk_s, vp, a.sv_s, 0, a.Tkv);
   for (int it = 0; it < n_kv; ++it) {
     const int kv0 = it * 64;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) pin_vgpr(dq[mt]);
     wait_vmcnt<0>();
     __syncthreads();
     if (it + 1 < n_kv)
-      bt_dma2<T, D, WAVES>(smem + ((it + 1) & 1) * STAGE, kp, a.sk_s, vp, a.sv_s, kv0 + 64, a.Tkv);
+      dma.issue(smem + ((it + 1) & 1) * STAGE, kp, a.sk_s, vp, a.sv_s, kv0 + 64, a.Tkv);
     if (a.causal && kv0 > qw0 + 31) continue;  // this wavefront's rows see none of the tile
     const char* Ks = smem + (it & 1) * STAGE;
     const char* Vs = Ks + P::BYTES;
@@ -1155,14 +1238,17 @@ attn_bwd_dq_v2(BwdArgs a) {
         s = M::mma(bt_row<T, D>(Ks, 32 * u, st), qf[st], s);
         dp = M::mma(bt_row<T, D>(Vs, 32 * u, st), df[st], dp);
       }
-      // s[r] = S^T[kv0 + 32u + 8(r/4) + 4g + r%4][qrow]
+      // s[r] = S^T[kv0 + 32u + 8(r/4) + 4g + r%4][qrow]; masked scores -> -inf (p = 0)
+      if (need_mask) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kv = kv0 + 32 * u + 8 * (r >> 2) + 4 * g + (r & 3);
+          s[r] = (kv >= a.Tkv || (a.causal && kv > qrow)) ? -INFINITY : s[r];
+        }
+      }
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        float p = fast_exp2(fmaf(s[r], sl2, -lse2));
-        if (need_mask) {
-          const int kv = kv0 + 32 * u + 8 * (r >> 2) + 4 * g + (r & 3);
-          p = (kv >= a.Tkv || (a.causal && kv > qrow)) ? 0.f : p;
-        }
+        const float p = fast_exp2(fmaf(s[r], sl2, -lse2));
         ds[u][r] = p * (dp[r] - dl);
       }
     }
@@ -1418,24 +1504,23 @@ int fwd_simt(const FwdArgs& a, int64_t D, hipStream_t st) {
 #define TRI_ATTN_DQ_WAVES 8
 #endif
 
+// dQ first: it also computes delta, which the dK/dV kernel reads.
 template <typename T, int D>
 int bwd_v2(const BwdArgs& a, hipStream_t st) {
   constexpr int WK = TRI_ATTN_DKDV_WAVES, WQ = TRI_ATTN_DQ_WAVES;
   BwdArgs x = a;
-  x.n_tiles = (int)cdiv(a.Tkv, 32 * WK);
-  const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;
-  attn_bwd_dkdv_v2<T, D, WK><<<(unsigned)kv_blocks, 64 * WK, 0, st>>>(x);
-  if (int e = check_launch("attention backward (dk/dv, mfma)")) return e;
   x.n_tiles = (int)cdiv(a.Tq, 32 * WQ);
   const int64_t q_blocks = (int64_t)x.n_tiles * a.B * a.H;
   attn_bwd_dq_v2<T, D, WQ><<<(unsigned)q_blocks, 64 * WQ, 0, st>>>(x);
-  return check_launch("attention backward (dq, mfma)");
+  if (int e = check_launch("attention backward (dq, mfma)")) return e;
+  x.n_tiles = (int)cdiv(a.Tkv, 32 * WK);
+  const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;
+  attn_bwd_dkdv_v2<T, D, WK><<<(unsigned)kv_blocks, 64 * WK, 0, st>>>(x);
+  return check_launch("attention backward (dk/dv, mfma)");
 }
 
 template <typename T>
 int bwd_mfma(const BwdArgs& a, int64_t D, hipStream_t st) {
-  if (D == 128) return bwd_v2<T, 128>(a, st);
-  if (D == 64) return bwd_v2<T, 64>(a, st);
   BwdArgs x = a;
   x.n_tiles = (int)cdiv(a.Tkv, kDkvBN);
   const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;
@@ -1453,6 +1538,10 @@ int bwd_mfma(const BwdArgs& a, int64_t D, hipStream_t st) {
 
 template <typename T>
 int bwd_impl(const BwdArgs& a, int64_t D, bool mfma, hipStream_t st) {
+  if constexpr (!std::is_same<T, float>::value) {
+    if (mfma && D == 128) return bwd_v2<T, 128>(a, st);
+    if (mfma && D == 64) return bwd_v2<T, 64>(a, st);
+  }
   const int64_t rows = (int64_t)a.B * a.H * a.Tq;
   attn_bwd_delta<T><<<(unsigned)cdiv(rows, 4), 256, 0, st>>>(a, (int)D);
   if (int e = check_launch("attention backward (delta)")) return e;
@@ -1558,7 +1647,8 @@ extern "C" int tritium_attention_bwd(const void* dout, const void* q, const void
                     rows_aligned(q, a.sq_b, a.sq_h, a.sq_s) &&
                     rows_aligned(k, a.sk_b, a.sk_h, a.sk_s) &&
                     rows_aligned(v, a.sv_b, a.sv_h, a.sv_s) &&
-                    rows_aligned(dout, a.sdo_b, a.sdo_h, a.sdo_s) && out_ok;
+                    rows_aligned(dout, a.sdo_b, a.sdo_h, a.sdo_s) &&
+                    rows_aligned(o, a.so_b, a.so_h, a.so_s) && out_ok;
   hipStream_t st = (hipStream_t)stream;
   TRI_DISPATCH_FLOAT(dtype, T, return bwd_impl<T>(a, D, mfma, st));
   return TRI_OK;

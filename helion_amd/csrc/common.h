@@ -57,6 +57,11 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v;
 }
 
+// Index of the calling wavefront in its workgroup, as a wave-uniform
+// (scalar) value: conditions built from it become scalar branches instead
+// of per-lane exec masking.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, kWave));
@@ -87,6 +92,13 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
 // make its own in-order vmcnt waits stricter.
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds)
+               : "memory", "m0");
+}
+
+// dma16 with a wave-uniform 64-bit base and a 32-bit per-lane byte offset
+// (the scalar-base addressing form: no 64-bit address arithmetic per lane).
+__device__ __forceinline__ void dma16s(const void* base, uint32_t voff, uint32_t lds) {
+  asm volatile("s_mov_b32 m0, %2\n\tglobal_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "s"(lds)
                : "memory", "m0");
 }
 
