@@ -89,6 +89,18 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
+// Scheduling fence: the compiler keeps every instruction on its side.
+__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
+
+// Pin a loop-carried value to AGPRs (pin_agpr) or VGPRs (pin_vgpr) at the
+// top of each iteration.  Without it the register allocator may home an
+// MFMA accumulator in the other register file and copy it into and out of
+// the MFMA's registers every iteration.  Emits no instruction.
+template <typename X>
+__device__ __forceinline__ void pin_agpr(X& x) { asm volatile("" : "+a"(x)); }
+template <typename X>
+__device__ __forceinline__ void pin_vgpr(X& x) { asm volatile("" : "+v"(x)); }
+
 // Workgroup id -> work id such that each XCD (block id mod 8) processes a
 // contiguous range of work ids.
 __device__ __forceinline__ int xcd_remap(int bid, int n) {
@@ -356,9 +368,20 @@ attn_fwd_mfma(FwdArgs a) {
 // global_load_lds_dwordx4 into two LDS stages (the next tile streams in
 // while the current one is multiplied); rows are XOR-swizzled per tile so
 // that both the 16-byte K reads and the transposing V reads are conflict-free.
-constexpr int kF2Waves = 8;
+#ifndef TRI_ATTN_FWD_WAVES
+#define TRI_ATTN_FWD_WAVES 4
+#endif
+constexpr int kF2Waves = TRI_ATTN_FWD_WAVES;
 constexpr int kF2BM = 32 * kF2Waves;  // query rows per workgroup
 constexpr int kF2BN = 64;             // K/V rows per tile
+#ifndef TRI_ATTN_RING
+#define TRI_ATTN_RING 4
+#endif
+constexpr int kRing = TRI_ATTN_RING;  // MFMA operands in flight ahead of use
+#ifndef TRI_ATTN_FWD_STAGES
+#define TRI_ATTN_FWD_STAGES 2
+#endif
+constexpr int kF2Stages = TRI_ATTN_FWD_STAGES;  // K/V tiles in the LDS ring
 
 template <int D>
 struct F2 {
@@ -404,14 +427,14 @@ __device__ __forceinline__ void f2_dma(char* stage, const T* kp, const T* vp, in
 }
 
 template <typename T, int D>
-__global__ void __launch_bounds__(64 * kF2Waves)
+__global__ void __launch_bounds__(64 * kF2Waves, 8 / kF2Waves)  // 2 wavefronts per SIMD
 attn_fwd_v2(FwdArgs a) {
   typedef Mfma<T> M;
   typedef typename M::V V;
   typedef F2<D> P;
   constexpr int KS = D / 16;
   constexpr int MT = D / 32;
-  __shared__ __attribute__((aligned(1024))) char smem[2 * P::STAGE];
+  __shared__ __attribute__((aligned(1024))) char smem[kF2Stages * P::STAGE];
 
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int l32 = lane & 31, g = lane >> 5;
@@ -446,29 +469,64 @@ attn_fwd_v2(FwdArgs a) {
 
   const int kv_end = a.causal ? min(a.Tkv, q0 + kF2BM) : a.Tkv;
   const int n_kv = (int)cdiv(kv_end, kF2BN);
-  if (n_kv > 0) f2_dma<T, D>(smem, kp, vp, a.sk_s, a.sv_s, 0, a.Tkv);
+  // kF2Stages-deep ring: tile it + kF2Stages - 1 streams in while tile it
+  // is multiplied, so a tile has kF2Stages - 1 tiles of compute to land
+#pragma unroll
+  for (int j = 0; j < kF2Stages - 1; ++j)
+    if (j < n_kv) f2_dma<T, D>(smem + j * P::STAGE, kp, vp, a.sk_s, a.sv_s, j * kF2BN, a.Tkv);
   for (int it = 0; it < n_kv; ++it) {
     const int kv0 = it * kF2BN;
-    wait_vmcnt<0>();
+    // tile it has landed once at most the DMAs of the kF2Stages - 2 younger
+    // tiles (issued in order, counted in order) are outstanding
+    if (it + kF2Stages - 2 < n_kv) wait_vmcnt<(kF2Stages - 2) * P::DMA_PER_WAVE>();
+    else wait_vmcnt<0>();
     __syncthreads();
-    if (it + 1 < n_kv)
-      f2_dma<T, D>(smem + ((it + 1) & 1) * P::STAGE, kp, vp, a.sk_s, a.sv_s, kv0 + kF2BN, a.Tkv);
-    const char* Ks = smem + (it & 1) * P::STAGE;
+    if (it + kF2Stages - 1 < n_kv)
+      f2_dma<T, D>(smem + ((it + kF2Stages - 1) % kF2Stages) * P::STAGE, kp, vp, a.sk_s, a.sv_s,
+                   kv0 + (kF2Stages - 1) * kF2BN, a.Tkv);
+    const char* Ks = smem + (it % kF2Stages) * P::STAGE;
     const char* Vs = Ks + P::TILE;
     if (a.causal && kv0 > qw0 + 31) continue;  // this wavefront's rows see none of the tile
 
-    f32x16 s[2];
+    // S^T = K Q^T: MFMA i = 2 st + u (the two 32-row halves interleaved);
+    // each K fragment is read kRing MFMAs before its use, and the fences
+    // keep the compiler from pulling reads back next to their MFMAs
+    auto kread = [&](int i) {
+      const int row = 32 * (i & 1) + l32;
+      return *reinterpret_cast<const V*>(Ks + row * P::RB +
+                                         (((2 * (i >> 1) + g) ^ P::key_k(row)) << 4));
+    };
+    f32x16 s[2] = {zero16(), zero16()};
+    V kb[kRing];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      s[u] = zero16();
-      const int row = 32 * u + l32;
+    for (int i = 0; i < kRing; ++i) kb[i] = kread(i);
 #pragma unroll
-      for (int st = 0; st < KS; ++st) {
-        const V kf = *reinterpret_cast<const V*>(Ks + row * P::RB +
-                                                 (((2 * st + g) ^ P::key_k(row)) << 4));
-        s[u] = M::mma(kf, qf[st], s[u]);
-      }
+    for (int i = 0; i < 2 * KS; ++i) {
+      sched_fence();
+      s[i & 1] = M::mma(kb[i % kRing], qf[i >> 1], s[i & 1]);
+      if (i + kRing < 2 * KS) kb[i % kRing] = kread(i + kRing);
     }
+    sched_fence();
+    // V^T fragments for the first O^T MFMAs, in flight during the softmax
+    auto vread = [&](int i) {  // MFMA i = MT t + mt
+      const int t = i / MT, mt = i % MT;
+      const int r1 = 16 * t + 4 * g + (ts >> 2), r2 = r1 + 8;
+      const int c = 4 * mt + 2 * thalf + ((ts & 3) >> 1);
+      const int sub = (ts & 1) * 8;
+      typedef short v4s __attribute__((ext_vector_type(4)));
+      const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) v4s*)(lds_addr(
+              Vs + r1 * P::RB + ((c ^ P::key_v(r1)) << 4) + sub)));
+      const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) v4s*)(lds_addr(
+              Vs + r2 * P::RB + ((c ^ P::key_v(r2)) << 4) + sub)));
+      // whole-vector bit cast (per-element assembly of 16-bit lanes from the
+      // transposing-read results was miscompiled into lane broadcasts)
+      return __builtin_bit_cast(V, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+    };
+    V vb[kRing];
+#pragma unroll
+    for (int i = 0; i < kRing; ++i) vb[i] = vread(i);
     // s[u][r] = S^T[kv0 + 32u + 8(r/4) + 4g + r%4][qrow]
     const bool need_mask = (kv0 + kF2BN > a.Tkv) || (a.causal && kv0 + kF2BN - 1 > qw0);
     if (need_mask) {
@@ -512,31 +570,21 @@ attn_fwd_v2(FwdArgs a) {
       }
     }
 
+    // O^T += V^T P^T: MFMA i = MT t + mt, kv rows 16t + 4g + {0..3} and
+    // 16t + 8 + 4g + {0..3} (the P^T operand order of the S^T accumulator)
+    V pb;
 #pragma unroll
-    for (int t = 0; t < kF2BN / 16; ++t) {
-      V pb;
+    for (int i = 0; i < (kF2BN / 16) * MT; ++i) {
+      const int t = i / MT, mt = i % MT;
+      sched_fence();
+      if (mt == 0) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pb[j] = (T)s[t >> 1][8 * (t & 1) + j];
-      // V^T fragment: kv rows 16t + 4g + {0..3} and 16t + 8 + 4g + {0..3}
-      const int r1 = 16 * t + 4 * g + (ts >> 2), r2 = r1 + 8;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        const int c = 4 * mt + 2 * thalf + ((ts & 3) >> 1);
-        const int sub = (ts & 1) * 8;
-        typedef short v4s __attribute__((ext_vector_type(4)));
-        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) v4s*)(lds_addr(
-                Vs + r1 * P::RB + ((c ^ P::key_v(r1)) << 4) + sub)));
-        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) v4s*)(lds_addr(
-                Vs + r2 * P::RB + ((c ^ P::key_v(r2)) << 4) + sub)));
-        // whole-vector bit cast (per-element assembly of 16-bit lanes from the
-        // transposing-read results was miscompiled into lane broadcasts)
-        typedef short v8s __attribute__((ext_vector_type(8)));
-        const V vt = __builtin_bit_cast(V, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-        o[mt] = M::mma(vt, pb, o[mt]);
+        for (int j = 0; j < 8; ++j) pb[j] = (T)s[t >> 1][8 * (t & 1) + j];
       }
+      o[mt] = M::mma(vb[i % kRing], pb, o[mt]);
+      if (i + kRing < (kF2BN / 16) * MT) vb[i % kRing] = vread(i + kRing);
     }
+    sched_fence();
   }
 
   const float lt = l + __shfl_xor(l, 32, 64);
@@ -979,17 +1027,7 @@ __device__ __forceinline__ typename Mfma<T>::V bt_tr(const char* tile, int rb, i
                             __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
-// Scheduling fence: the compiler keeps every instruction on its side.
-__device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
-// Pin a loop-carried value to AGPRs (pin_agpr) or VGPRs (pin_vgpr) at the
-// top of each iteration.  Without it the register allocator may home an
-// MFMA accumulator in the other register file and copy it into and out of
-// the MFMA's registers every iteration.  Emits no instruction.
-template <typename X>
-__device__ __forceinline__ void pin_agpr(X& x) { asm volatile("" : "+a"(x)); }
-template <typename X>
-__device__ __forceinline__ void pin_vgpr(X& x) { asm volatile("" : "+v"(x)); }
 
 #ifndef TRI_DKDV_FENCES
 #define TRI_DKDV_FENCES 0
@@ -1157,7 +1195,7 @@ attn_bwd_dkdv_v2(BwdArgs a) {
 // and sweeps the 64-row K/V tiles it can see: S^T = K Q^T and
 // dP^T = V dO^T from row reads, dQ^T += K^T dS^T from transposing reads.
 template <typename T, int D, int WAVES>
-__global__ void __launch_bounds__(64 * WAVES)
+__global__ void __launch_bounds__(64 * WAVES, 8 / WAVES)  // 2 wavefronts per SIMD
 attn_bwd_dq_v2(BwdArgs a) {
   typedef Mfma<T> M;
   typedef typename M::V V;
@@ -1501,7 +1539,7 @@ int fwd_simt(const FwdArgs& a, int64_t D, hipStream_t st) {
 #define TRI_ATTN_DKDV_WAVES 4
 #endif
 #ifndef TRI_ATTN_DQ_WAVES
-#define TRI_ATTN_DQ_WAVES 8
+#define TRI_ATTN_DQ_WAVES 4
 #endif
 
 // dQ first: it also computes delta, which the dK/dV kernel reads.
