@@ -8,7 +8,8 @@
 //
 // Each block updates one CHUNK of one tensor with 16-byte accesses (4 fp32 or
 // 8 fp16/bf16 parameters per access).  28 bytes move per fp32 parameter
-// (read p, g, m, v; write p, m, v) -- the whole step is one HBM pass.
+// (read p, g, m, v; write p, m, v) -- the whole step is one HBM pass, every
+// access streamed with the nontemporal hint.
 //
 // Multi-tensor table (int64, kDescWords per tensor, built by the host):
 //   [param_ptr, grad_ptr, exp_avg_ptr, exp_avg_sq_ptr, numel, flags,
@@ -23,7 +24,10 @@ namespace tri {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kVecPerThread = 2;
+#ifndef TRI_ADAMW_VEC_PER_THREAD
+#define TRI_ADAMW_VEC_PER_THREAD 2
+#endif
+constexpr int kVecPerThread = TRI_ADAMW_VEC_PER_THREAD;
 constexpr int64_t kChunk = (int64_t)kBlock * kVecPerThread * 8;  // 4096 elements
 
 struct Hyper {
@@ -59,10 +63,10 @@ __device__ __forceinline__ void adam_chunk(T* __restrict__ p, const T* __restric
     for (int u = 0; u < NVEC; ++u) {
       const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
       if (e < vec_end) {
-        load_f32<T, VEC>(p + e, pv[u]);
-        load_f32<T, VEC>(g + e, gv[u]);
-        load_f32<float, VEC>(m + e, mv[u]);
-        load_f32<float, VEC>(v + e, vv[u]);
+        load_stream<T, VEC>(p + e, pv[u]);
+        load_stream<T, VEC>(g + e, gv[u]);
+        load_stream<float, VEC>(m + e, mv[u]);
+        load_stream<float, VEC>(v + e, vv[u]);
       }
     }
 #pragma unroll
@@ -71,9 +75,9 @@ __device__ __forceinline__ void adam_chunk(T* __restrict__ p, const T* __restric
       if (e < vec_end) {
 #pragma unroll
         for (int i = 0; i < VEC; ++i) adam_update(pv[u][i], gv[u][i], mv[u][i], vv[u][i], h, lr_wd, step_size);
-        store_f32<float, VEC>(m + e, mv[u]);
-        store_f32<float, VEC>(v + e, vv[u]);
-        store_f32<T, VEC>(p + e, pv[u]);
+        store_stream<float, VEC>(m + e, mv[u]);
+        store_stream<float, VEC>(v + e, vv[u]);
+        store_stream<T, VEC>(p + e, pv[u]);
       }
     }
     for (int64_t e = vec_end + threadIdx.x; e < end; e += kBlock) {

@@ -22,7 +22,10 @@
 namespace tri {
 namespace {
 
-constexpr int kMaxPartialRows = 512;   // fast-path dweight partial rows
+#ifndef TRI_RMS_BWD_BLOCKS
+#define TRI_RMS_BWD_BLOCKS 512
+#endif
+constexpr int kMaxPartialRows = TRI_RMS_BWD_BLOCKS;  // fast-path backward grid = dweight partial rows
 constexpr int kGenericBlock = 256;
 constexpr int kStage1Rows = 128;       // streaming-path rows per dweight partial
 
@@ -62,6 +65,10 @@ __device__ __forceinline__ void row_sum2(float& a, float& b, float2* red) {
 }
 
 // ---------------------------------------------------------------- forward --
+// Persistent rows: row group g of block b takes rows b * RPB + g, then
+// advances by gridDim.x * RPB.  The weight is read once per lane; the next
+// row's raw vectors are loaded while the current row is reduced; x / residual
+// are read and y / residual_out written with the nontemporal hint.
 template <typename T, int TPR, int NV>
 __global__ void __launch_bounds__(block_of<TPR>())
 rmsnorm_fwd_kernel(const T* __restrict__ x, const T* __restrict__ res,
@@ -72,58 +79,79 @@ rmsnorm_fwd_kernel(const T* __restrict__ x, const T* __restrict__ res,
   __shared__ float2 red[block_of<TPR>() / kWave];
   const int g = threadIdx.x / TPR;
   const int lt = threadIdx.x % TPR;
-  const int64_t row = (int64_t)blockIdx.x * RPB + g;
-  const bool active = row < n_rows;
   const int nvec = hidden / VEC;
-  const int64_t base = row * (int64_t)hidden;
+  const int64_t first = (int64_t)blockIdx.x * RPB;
+  const int64_t stride = (int64_t)gridDim.x * RPB;
+  const int64_t iters = first < n_rows ? cdiv(n_rows - first, stride) : 0;  // block-uniform
 
-  float v[NV][VEC];
-  float ss = 0.f, unused = 0.f;
+  u32x4 wr[NV], xr[NV], rr[NV];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int vi = lt + j * TPR;
-    if (active && vi < nvec) {
-      load_f32<T, VEC>(x + base + (int64_t)vi * VEC, v[j]);
+    wr[j] = vi < nvec ? ld16(w + (int64_t)vi * VEC) : u32x4{0u, 0u, 0u, 0u};
+    xr[j] = rr[j] = u32x4{0u, 0u, 0u, 0u};
+  }
+  auto fetch = [&](int64_t row) {
+    if (row >= n_rows) return;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int vi = lt + j * TPR;
+      if (vi < nvec) {
+        xr[j] = ld16_nt(x + row * hidden + (int64_t)vi * VEC);
+        if (res != nullptr) rr[j] = ld16_nt(res + row * hidden + (int64_t)vi * VEC);
+      }
+    }
+  };
+  fetch(first + g);
+  for (int64_t it = 0; it < iters; ++it) {
+    const int64_t row = first + g + it * stride;
+    const bool active = row < n_rows;
+    float v[NV][VEC];
+    float ss = 0.f, unused = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      unpack<T>(xr[j], v[j]);
       if (res != nullptr) {
         float r[VEC];
-        load_f32<T, VEC>(res + base + (int64_t)vi * VEC, r);
+        unpack<T>(rr[j], r);
 #pragma unroll
         for (int i = 0; i < VEC; ++i) v[j][i] += r[i];
       }
 #pragma unroll
       for (int i = 0; i < VEC; ++i) ss += v[j][i] * v[j][i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) v[j][i] = 0.f;
     }
-  }
-  row_sum2<TPR>(ss, unused, red);
-  const float rs = 1.0f / sqrtf(ss / (float)hidden + eps);
+    fetch(row + stride);
+    row_sum2<TPR>(ss, unused, red);
+    const float rs = 1.0f / sqrtf(ss / (float)hidden + eps);
 #pragma unroll
-  for (int j = 0; j < NV; ++j) {
-    const int vi = lt + j * TPR;
-    if (active && vi < nvec) {
-      float wv[VEC], o[VEC];
-      load_f32<T, VEC>(w + (int64_t)vi * VEC, wv);
+    for (int j = 0; j < NV; ++j) {
+      const int vi = lt + j * TPR;
+      if (active && vi < nvec) {
+        float wv[VEC], o[VEC];
+        unpack<T>(wr[j], wv);
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) o[i] = v[j][i] * rs * wv[i];
-      store_f32<T, VEC>(y + base + (int64_t)vi * VEC, o);
-      if (z != nullptr) store_f32<T, VEC>(z + base + (int64_t)vi * VEC, v[j]);
+        for (int i = 0; i < VEC; ++i) o[i] = v[j][i] * rs * wv[i];
+        st16_nt(y + row * hidden + (int64_t)vi * VEC, pack<T>(o));
+        if (z != nullptr) st16_nt(z + row * hidden + (int64_t)vi * VEC, pack<T>(v[j]));
+      }
     }
+    if (active && lt == 0) rstd[row] = rs;
   }
-  if (active && lt == 0) rstd[row] = rs;
 }
 
 // --------------------------------------------------------------- backward --
-// dx for rows [blockIdx.x*rows_per_block, ...) and, when dw_partial != null,
-// one dweight partial row per block.
+// dx for the rows of this block (persistent, as the forward) and, when
+// dw_partial != null, one dweight partial row per block: the row groups
+// accumulate sum(dy * x * rstd) over their rows in registers and are added
+// through LDS in a fixed order.  Raw x / dy of the next row stream in while
+// the current row is reduced.
 template <typename T, int TPR, int NV>
 __global__ void __launch_bounds__(block_of<TPR>())
 rmsnorm_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x,
                    const T* __restrict__ w, const float* __restrict__ rstd_in,
                    const T* __restrict__ dres, T* __restrict__ dx,
                    typename DwAcc<T>::type* __restrict__ dw_partial, int64_t n_rows, int hidden,
-                   float eps, int64_t rows_per_block) {
+                   float eps) {
   typedef typename DwAcc<T>::type A;
   constexpr int VEC = 16 / sizeof(T);
   constexpr int RPB = block_of<TPR>() / TPR;
@@ -134,73 +162,89 @@ rmsnorm_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x,
   const int lt = threadIdx.x % TPR;
   const int nvec = hidden / VEC;
   const float inv_h = 1.0f / (float)hidden;
+  const int64_t first = (int64_t)blockIdx.x * RPB;
+  const int64_t stride = (int64_t)gridDim.x * RPB;
+  const int64_t iters = first < n_rows ? cdiv(n_rows - first, stride) : 0;  // block-uniform
 
-  float wv[NV][VEC];
+  u32x4 wr[NV], xr[NV], gr[NV], xn[NV], gn[NV];
   A acc[NV][VEC];
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int vi = lt + j * TPR;
-    if (vi < nvec) {
-      load_f32<T, VEC>(w + (int64_t)vi * VEC, wv[j]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < VEC; ++i) wv[j][i] = 0.f;
-    }
+    wr[j] = vi < nvec ? ld16(w + (int64_t)vi * VEC) : u32x4{0u, 0u, 0u, 0u};
+    xr[j] = gr[j] = xn[j] = gn[j] = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int i = 0; i < VEC; ++i) acc[j][i] = 0;
   }
-
-  const int64_t row0 = (int64_t)blockIdx.x * rows_per_block;
-  const int64_t row_end = min(row0 + rows_per_block, n_rows);
-  const int64_t iters = cdiv(rows_per_block, RPB);
-  for (int64_t it = 0; it < iters; ++it) {
-    const int64_t row = row0 + it * RPB + g;
-    const bool active = row < row_end;
-    const int64_t base = row * (int64_t)hidden;
-    float xv[NV][VEC], gv[NV][VEC];
-    float ss = 0.f, c = 0.f;
+  float rs_next = 0.f;
+  auto fetch = [&](int64_t row, u32x4 (&xb)[NV], u32x4 (&gb)[NV], float& rsb) {
+    if (row >= n_rows) return;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int vi = lt + j * TPR;
-      if (active && vi < nvec) {
-        load_f32<T, VEC>(x + base + (int64_t)vi * VEC, xv[j]);
-        load_f32<T, VEC>(dy + base + (int64_t)vi * VEC, gv[j]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) xv[j][i] = gv[j][i] = 0.f;
+      if (vi < nvec) {
+        xb[j] = ld16_nt(x + row * hidden + (int64_t)vi * VEC);
+        gb[j] = ld16_nt(dy + row * hidden + (int64_t)vi * VEC);
       }
+    }
+    if (rstd_in != nullptr) rsb = rstd_in[row];
+  };
+  fetch(first + g, xr, gr, rs_next);
+  for (int64_t it = 0; it < iters; ++it) {
+    const int64_t row = first + g + it * stride;
+    const bool active = row < n_rows;
+    float rs = rs_next;
+    float ss = 0.f, c = 0.f;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      float xv[VEC], gv[VEC], wv[VEC];
+      unpack<T>(xr[j], xv);
+      unpack<T>(gr[j], gv);
+      unpack<T>(wr[j], wv);
 #pragma unroll
       for (int i = 0; i < VEC; ++i) {
-        ss += xv[j][i] * xv[j][i];
-        c += gv[j][i] * wv[j][i] * xv[j][i];
+        ss += xv[i] * xv[i];
+        c += gv[i] * wv[i] * xv[i];
+      }
+    }
+    fetch(row + stride, xn, gn, rs_next);
+    u32x4 rr[NV];
+    if (dres != nullptr && active) {
+#pragma unroll
+      for (int j = 0; j < NV; ++j) {
+        const int vi = lt + j * TPR;
+        if (vi < nvec) rr[j] = ld16_nt(dres + row * hidden + (int64_t)vi * VEC);
       }
     }
     row_sum2<TPR>(ss, c, red);
-    float rs;
-    if (rstd_in != nullptr) {
-      rs = active ? rstd_in[row] : 0.f;
-    } else {
-      rs = 1.0f / sqrtf(ss * inv_h + eps);
-    }
+    if (rstd_in == nullptr) rs = 1.0f / sqrtf(ss * inv_h + eps);
     const float k3 = rs * rs * rs * inv_h;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int vi = lt + j * TPR;
       if (active && vi < nvec) {
-        float o[VEC];
+        float xv[VEC], gv[VEC], wv[VEC], o[VEC];
+        unpack<T>(xr[j], xv);
+        unpack<T>(gr[j], gv);
+        unpack<T>(wr[j], wv);
 #pragma unroll
         for (int i = 0; i < VEC; ++i) {
-          o[i] = rs * (gv[j][i] * wv[j][i]) - k3 * xv[j][i] * c;
-          acc[j][i] += (A)gv[j][i] * (A)xv[j][i] * (A)rs;
+          o[i] = rs * (gv[i] * wv[i]) - k3 * xv[i] * c;
+          acc[j][i] += (A)gv[i] * (A)xv[i] * (A)rs;
         }
         if (dres != nullptr) {
           float r[VEC];
-          load_f32<T, VEC>(dres + base + (int64_t)vi * VEC, r);
+          unpack<T>(rr[j], r);
 #pragma unroll
           for (int i = 0; i < VEC; ++i) o[i] += r[i];
         }
-        store_f32<T, VEC>(dx + base + (int64_t)vi * VEC, o);
+        st16_nt(dx + row * hidden + (int64_t)vi * VEC, pack<T>(o));
       }
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      xr[j] = xn[j];
+      gr[j] = gn[j];
     }
   }
 
@@ -233,26 +277,58 @@ rmsnorm_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x,
   }
 }
 
-// Sum `n_part` fp32 partial rows into dweight (cast to the weight dtype).
-// Block: 64 columns x 4 wavefronts; wavefront k adds rows k, k+4, ... and the
-// four column sums are then added in a fixed order.
+// Column sums of partial rows, in two levels with a fixed order: level 1
+// (grid = column blocks x row groups) adds kDwGroup consecutive partial rows
+// per column; level 2 adds the group sums and casts to the weight dtype.
+constexpr int kDwGroup = 8;
+
+// The loads of a group are independent (issued together); the adds run in
+// row order, so the result does not depend on timing.
+template <typename A>
+__global__ void __launch_bounds__(256)
+dw_sum_groups_kernel(const A* __restrict__ partial, int64_t n_part, int hidden,
+                     A* __restrict__ sums) {
+  const int col = blockIdx.x * 256 + threadIdx.x;
+  if (col >= hidden) return;
+  const int64_t p0 = (int64_t)blockIdx.y * kDwGroup;
+  A v[kDwGroup];
+#pragma unroll
+  for (int i = 0; i < kDwGroup; ++i) v[i] = p0 + i < n_part ? partial[(p0 + i) * hidden + col] : 0;
+  A s = 0;
+#pragma unroll
+  for (int i = 0; i < kDwGroup; ++i) s += v[i];
+  sums[(int64_t)blockIdx.y * hidden + col] = s;
+}
+
 template <typename T, typename A>
 __global__ void __launch_bounds__(256)
-dw_reduce_kernel(const A* __restrict__ partial, int64_t n_part, int hidden,
-                 T* __restrict__ dw) {
-  __shared__ A red[4][kWave];
-  const int lane = threadIdx.x % kWave;
-  const int wave = threadIdx.x / kWave;
-  const int col = blockIdx.x * kWave + lane;
+dw_finish_kernel(const A* __restrict__ sums, int64_t n_groups, int hidden, T* __restrict__ dw) {
+  const int col = blockIdx.x * 256 + threadIdx.x;
+  if (col >= hidden) return;
   A s = 0;
-  if (col < hidden) {
-    for (int64_t p = wave; p < n_part; p += 4) s += partial[p * hidden + col];
+  int64_t p = 0;
+  for (; p + 8 <= n_groups; p += 8) {
+    A v[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = sums[(p + i) * hidden + col];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) s += v[i];
   }
-  red[wave][lane] = s;
-  __syncthreads();
-  if (wave == 0 && col < hidden) {
-    dw[col] = from_f32<T>((float)(((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane]));
-  }
+  for (; p < n_groups; ++p) s += sums[p * hidden + col];
+  dw[col] = from_f32<T>((float)s);
+}
+
+// Two-level column sum of n_part partial rows into dw; `sums` holds
+// cdiv(n_part, kDwGroup) rows.
+template <typename T, typename A>
+int dw_reduce(const A* partial, int64_t n_part, int hidden, A* sums, T* dw, hipStream_t stream) {
+  const int64_t n_groups = cdiv(n_part, kDwGroup);
+  dw_sum_groups_kernel<A><<<dim3((unsigned)cdiv(hidden, 256), (unsigned)n_groups), 256, 0,
+                            stream>>>(partial, n_part, hidden, sums);
+  if (int e = check_launch("rmsnorm dweight reduce (groups)")) return e;
+  dw_finish_kernel<T, A><<<(unsigned)cdiv(hidden, 256), 256, 0, stream>>>(sums, n_groups, hidden,
+                                                                          dw);
+  return check_launch("rmsnorm dweight reduce");
 }
 
 // -------------------------------------------------------- streaming path --
@@ -365,8 +441,18 @@ FastCfg pick_fast(int64_t hidden, int vec, int max_nv) {
     default: return fail(TRI_EINVAL, "rmsnorm: no kernel for tpr=%d nv=%d", cfg.tpr, cfg.nv); \
   }
 
-constexpr int kFwdMaxNV = 8;
-constexpr int kBwdMaxNV = 4;
+#ifndef TRI_RMS_FWD_MAX_NV
+#define TRI_RMS_FWD_MAX_NV 1
+#endif
+#ifndef TRI_RMS_FWD_BLOCKS
+#define TRI_RMS_FWD_BLOCKS 2048
+#endif
+constexpr int kFwdMaxNV = TRI_RMS_FWD_MAX_NV;
+constexpr int64_t kFwdBlocks = TRI_RMS_FWD_BLOCKS;  // persistent forward grid (rows loop inside)
+#ifndef TRI_RMS_BWD_MAX_NV
+#define TRI_RMS_BWD_MAX_NV 4
+#endif
+constexpr int kBwdMaxNV = TRI_RMS_BWD_MAX_NV;
 
 template <typename T>
 int fwd_impl(const void* x, const void* res, const void* w, void* y, void* z, float* rstd,
@@ -377,7 +463,7 @@ int fwd_impl(const void* x, const void* res, const void* w, void* y, void* z, fl
   FastCfg cfg = aligned ? pick_fast(hidden, VEC, kFwdMaxNV) : FastCfg{};
   if (cfg.tpr != 0) {
     const int rpb = (cfg.tpr < 256 ? 256 : cfg.tpr) / cfg.tpr;
-    const dim3 grid((unsigned)cdiv(n_rows, rpb));
+    const dim3 grid((unsigned)std::min<int64_t>(cdiv(n_rows, rpb), kFwdBlocks));
 #define LAUNCH(TPR, NV)                                                                  \
   rmsnorm_fwd_kernel<T, TPR, NV><<<grid, block_of<TPR>(), 0, stream>>>(                  \
       (const T*)x, (const T*)res, (const T*)w, (T*)y, (T*)z, rstd, n_rows, (int)hidden, eps)
@@ -394,6 +480,12 @@ int64_t fast_bwd_blocks(int64_t n_rows, int rpb) {
   return std::min<int64_t>(cdiv(n_rows, rpb), kMaxPartialRows);
 }
 
+// Workspace of the dweight reduction: partial rows, then their group sums.
+template <typename A>
+int64_t dw_ws_bytes(int64_t n_part, int64_t hidden) {
+  return (n_part + cdiv(n_part, kDwGroup)) * hidden * (int64_t)sizeof(A);
+}
+
 template <typename T>
 int bwd_impl(const void* dy, const void* x, const void* w, const float* rstd, const void* dres,
              void* dx, void* dw, void* ws, size_t ws_bytes, int64_t n_rows, int64_t hidden,
@@ -405,30 +497,26 @@ int bwd_impl(const void* dy, const void* x, const void* w, const float* rstd, co
   FastCfg cfg = aligned ? pick_fast(hidden, VEC, kBwdMaxNV) : FastCfg{};
   if (cfg.tpr != 0) {
     const int rpb = (cfg.tpr < 256 ? 256 : cfg.tpr) / cfg.tpr;
-    const int64_t blocks = fast_bwd_blocks(n_rows, rpb);
-    const int64_t rows_per_block = cdiv(n_rows, blocks);
-    const int64_t n_part = cdiv(n_rows, rows_per_block);
+    const int64_t n_part = fast_bwd_blocks(n_rows, rpb);
     A* partial = dw != nullptr ? (A*)ws : nullptr;
-    if (dw != nullptr && (size_t)(n_part * hidden * sizeof(A)) > ws_bytes)
+    if (dw != nullptr && (size_t)dw_ws_bytes<A>(n_part, hidden) > ws_bytes)
       return fail(TRI_EINVAL, "rmsnorm backward: workspace too small");
 #define LAUNCH(TPR, NV)                                                                   \
   rmsnorm_bwd_kernel<T, TPR, NV><<<(unsigned)n_part, block_of<TPR>(), 0, stream>>>(        \
       (const T*)dy, (const T*)x, (const T*)w, rstd, (const T*)dres, (T*)dx, partial, n_rows, \
-      (int)hidden, eps, rows_per_block)
+      (int)hidden, eps)
     TRI_FAST_SWITCH(cfg, LAUNCH)
 #undef LAUNCH
     if (int e = check_launch("rmsnorm backward")) return e;
-    if (dw != nullptr) {
-      dw_reduce_kernel<T, A><<<(unsigned)cdiv(hidden, kWave), 256, 0, stream>>>(
-          partial, n_part, (int)hidden, (T*)dw);
-      return check_launch("rmsnorm dweight reduce");
-    }
+    if (dw != nullptr)
+      return dw_reduce<T, A>(partial, n_part, (int)hidden, partial + n_part * hidden, (T*)dw,
+                             stream);
     return TRI_OK;
   }
   // streaming path: workspace = rstd_used[n_rows] then partial[row_blocks][hidden]
   const int64_t rstd_bytes = cdiv(n_rows * 4, 256) * 256;
   const int64_t n_rb = cdiv(n_rows, kStage1Rows);
-  if ((size_t)(rstd_bytes + n_rb * hidden * sizeof(A)) > ws_bytes)
+  if ((size_t)(rstd_bytes + dw_ws_bytes<A>(n_rb, hidden)) > ws_bytes)
     return fail(TRI_EINVAL, "rmsnorm backward: workspace too small");
   float* rstd_used = (float*)ws;
   A* partial = (A*)((char*)ws + rstd_bytes);
@@ -441,9 +529,7 @@ int bwd_impl(const void* dy, const void* x, const void* w, const float* rstd, co
                         kGenericBlock, 0, stream>>>((const T*)dy, (const T*)x, rstd_used,
                                                     partial, n_rows, (int)hidden);
   if (int e = check_launch("rmsnorm dweight stage1")) return e;
-  dw_reduce_kernel<T, A><<<(unsigned)cdiv(hidden, kWave), 256, 0, stream>>>(partial, n_rb,
-                                                                         (int)hidden, (T*)dw);
-  return check_launch("rmsnorm dweight reduce");
+  return dw_reduce<T, A>(partial, n_rb, (int)hidden, partial + n_rb * hidden, (T*)dw, stream);
 }
 
 int check_shape(int64_t n_rows, int64_t hidden) {
@@ -473,8 +559,9 @@ extern "C" int tritium_rmsnorm_fwd(const void* x, const void* residual, const vo
 
 extern "C" size_t tritium_rmsnorm_bwd_workspace_size(int64_t n_rows, int64_t hidden) {
   if (n_rows <= 0 || hidden <= 0) return 0;
-  const int64_t fast = kMaxPartialRows * hidden * 8;
-  const int64_t streaming = cdiv(n_rows * 4, 256) * 256 + cdiv(n_rows, kStage1Rows) * hidden * 8;
+  const int64_t fast = dw_ws_bytes<double>(kMaxPartialRows, hidden);
+  const int64_t streaming =
+      cdiv(n_rows * 4, 256) * 256 + dw_ws_bytes<double>(cdiv(n_rows, kStage1Rows), hidden);
   return (size_t)std::max(fast, streaming);
 }
 

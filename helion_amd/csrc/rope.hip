@@ -9,7 +9,8 @@
 // One lane rotates P pairs of q AND the same P pairs of k for one
 // (token, head): the cos/sin values it loads serve both tensors, and the 32+
 // lanes of a token that read the same cos/sin row hit in L1.  q/k accesses
-// are 16-byte vectors when the layout allows it.
+// are 16-byte vectors when the layout allows it, streamed with the
+// nontemporal hint (each element is read and written once).
 //
 // A position outside [0, max_position) has no table row; the kernel then
 // writes NaN for that token instead of reading out of bounds.
@@ -60,10 +61,10 @@ rope_kernel(const T* q, const T* k, const CT* __restrict__ cos_t,
 
   if (!interleaved) {
     float qa[P], qb[P], ka[P], kb[P];
-    load_f32<T, P>(q + base + p0, qa);
-    load_f32<T, P>(q + base + half + p0, qb);
-    load_f32<T, P>(k + base + p0, ka);
-    load_f32<T, P>(k + base + half + p0, kb);
+    load_stream<T, P>(q + base + p0, qa);
+    load_stream<T, P>(q + base + half + p0, qb);
+    load_stream<T, P>(k + base + p0, ka);
+    load_stream<T, P>(k + base + half + p0, kb);
     float oqa[P], oqb[P], oka[P], okb[P];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
@@ -72,17 +73,17 @@ rope_kernel(const T* q, const T* k, const CT* __restrict__ cos_t,
       oka[i] = valid ? ka[i] * c[i] - kb[i] * s[i] : nan;
       okb[i] = valid ? kb[i] * c[i] + ka[i] * s[i] : nan;
     }
-    store_f32<T, P>(q_out + base + p0, oqa);
-    store_f32<T, P>(q_out + base + half + p0, oqb);
-    store_f32<T, P>(k_out + base + p0, oka);
-    store_f32<T, P>(k_out + base + half + p0, okb);
+    store_stream<T, P>(q_out + base + p0, oqa);
+    store_stream<T, P>(q_out + base + half + p0, oqb);
+    store_stream<T, P>(k_out + base + p0, oka);
+    store_stream<T, P>(k_out + base + half + p0, okb);
   } else {
     // elements [2*p0, 2*p0 + 2P) hold P adjacent (a, b) pairs
     float qv[2 * P], kv[2 * P];
-    load_f32<T, P>(q + base + 2 * p0, *reinterpret_cast<float(*)[P]>(qv));
-    load_f32<T, P>(q + base + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(qv + P));
-    load_f32<T, P>(k + base + 2 * p0, *reinterpret_cast<float(*)[P]>(kv));
-    load_f32<T, P>(k + base + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(kv + P));
+    load_stream<T, P>(q + base + 2 * p0, *reinterpret_cast<float(*)[P]>(qv));
+    load_stream<T, P>(q + base + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(qv + P));
+    load_stream<T, P>(k + base + 2 * p0, *reinterpret_cast<float(*)[P]>(kv));
+    load_stream<T, P>(k + base + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(kv + P));
     float oq[2 * P], ok[2 * P];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
@@ -93,10 +94,10 @@ rope_kernel(const T* q, const T* k, const CT* __restrict__ cos_t,
       ok[2 * i] = valid ? ka * c[i] - kb * s[i] : nan;
       ok[2 * i + 1] = valid ? kb * c[i] + ka * s[i] : nan;
     }
-    store_f32<T, P>(q_out + base + 2 * p0, *reinterpret_cast<float(*)[P]>(oq));
-    store_f32<T, P>(q_out + base + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(oq + P));
-    store_f32<T, P>(k_out + base + 2 * p0, *reinterpret_cast<float(*)[P]>(ok));
-    store_f32<T, P>(k_out + base + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(ok + P));
+    store_stream<T, P>(q_out + base + 2 * p0, *reinterpret_cast<float(*)[P]>(oq));
+    store_stream<T, P>(q_out + base + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(oq + P));
+    store_stream<T, P>(k_out + base + 2 * p0, *reinterpret_cast<float(*)[P]>(ok));
+    store_stream<T, P>(k_out + base + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(ok + P));
   }
 }
 

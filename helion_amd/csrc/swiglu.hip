@@ -6,7 +6,8 @@
 // Pure streaming kernels: each lane moves U 16-byte vectors per operand, the
 // U loads of a lane are issued before any math so a wavefront keeps
 // U * (#operands) * 1 KiB in flight; a block covers one contiguous
-// 256 * U * VEC element span, so every access is fully coalesced.
+// 256 * U * VEC element span, so every access is fully coalesced.  Every
+// operand is touched once: loads and stores carry the nontemporal hint.
 #include "common.h"
 #include "../../include/tritium_hip.h"
 
@@ -29,8 +30,8 @@ swiglu_fwd_kernel(const T* __restrict__ x, const T* __restrict__ g, T* __restric
   for (int u = 0; u < U; ++u) {
     const int64_t iv = first + (int64_t)u * kBlock;
     if (iv < nvec) {
-      load_f32<T, VEC>(x + iv * VEC, xv[u]);
-      load_f32<T, VEC>(g + iv * VEC, gv[u]);
+      load_stream<T, VEC>(x + iv * VEC, xv[u]);
+      load_stream<T, VEC>(g + iv * VEC, gv[u]);
     }
   }
 #pragma unroll
@@ -40,7 +41,7 @@ swiglu_fwd_kernel(const T* __restrict__ x, const T* __restrict__ g, T* __restric
       float o[VEC];
 #pragma unroll
       for (int i = 0; i < VEC; ++i) o[i] = xv[u][i] * sigmoid_f32(xv[u][i]) * gv[u][i];
-      store_f32<T, VEC>(out + iv * VEC, o);
+      store_stream<T, VEC>(out + iv * VEC, o);
     }
   }
   if (VEC > 1 && blockIdx.x == gridDim.x - 1) {
@@ -62,9 +63,9 @@ swiglu_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x, const T* __
   for (int u = 0; u < U; ++u) {
     const int64_t iv = first + (int64_t)u * kBlock;
     if (iv < nvec) {
-      load_f32<T, VEC>(dy + iv * VEC, dv[u]);
-      load_f32<T, VEC>(x + iv * VEC, xv[u]);
-      load_f32<T, VEC>(g + iv * VEC, gv[u]);
+      load_stream<T, VEC>(dy + iv * VEC, dv[u]);
+      load_stream<T, VEC>(x + iv * VEC, xv[u]);
+      load_stream<T, VEC>(g + iv * VEC, gv[u]);
     }
   }
 #pragma unroll
@@ -80,8 +81,8 @@ swiglu_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x, const T* __
         ox[i] = dv[u][i] * gv[u][i] * dsilu;
         og[i] = dv[u][i] * silu;
       }
-      store_f32<T, VEC>(dx + iv * VEC, ox);
-      store_f32<T, VEC>(dg + iv * VEC, og);
+      store_stream<T, VEC>(dx + iv * VEC, ox);
+      store_stream<T, VEC>(dg + iv * VEC, og);
     }
   }
   if (VEC > 1 && blockIdx.x == gridDim.x - 1) {
