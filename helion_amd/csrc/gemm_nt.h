@@ -104,7 +104,7 @@ struct Problem {
 template <class C, typename T>
 __device__ __forceinline__ void dma_tile(char* stage, const Problem& p, int64_t m0, int64_t n0,
                                          int64_t k0) {
-  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rr = lane / C::GRAN;  // row inside the instruction's run of DMA_ROWS rows
   constexpr int VE = vec<T>();
 #pragma unroll
@@ -286,7 +286,10 @@ __device__ __forceinline__ void tile_of(int64_t bid, int64_t n_blocks, int tiles
 template <class C, typename T>
 __device__ __forceinline__ void mainloop(const Problem& p, int tm, int tn, char* smem,
                                          Acc<C>& acc) {
-  const int wave = wave_id();
+  // the wavefront index stays a per-lane value here: it is part of every
+  // fragment's LDS address, which then folds into one VGPR base plus
+  // immediate offsets (a scalar index costs an add per read: -12% measured)
+  const int wave = threadIdx.x >> 6;
   const int wm = wave / C::WN, wn = wave % C::WN;
   const int64_t m0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
   constexpr int BK = bk<C, T>();

@@ -76,7 +76,7 @@ lce_fwd_kernel(FwdArgs a) {
   Acc<C> acc;
   gemm::mainloop<C, T>(p, tm, tn, smem, acc);
 
-  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31, g = lane >> 5;
   const int wm = wave / C::WN, wn = wave % C::WN;
   const int64_t v0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
@@ -280,7 +280,7 @@ lce_g_kernel(GArgs a) {
   Acc<C> acc;
   gemm::mainloop<C, T>(p, tm, tn, smem, acc);
 
-  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31, g = lane >> 5;
   const int wm = wave / C::WN, wn = wave % C::WN;
   const int64_t v0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
@@ -337,7 +337,7 @@ gemm_store_kernel(gemm::Problem p, const float* acc_in, OT* out, int64_t ldc, in
   gemm::tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
   Acc<C> acc;
   gemm::mainloop<C, T>(p, tm, tn, smem, acc);
-  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31, g = lane >> 5;
   const int wm = wave / C::WN, wn = wave % C::WN;
   const int64_t m0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
