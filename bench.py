@@ -285,6 +285,22 @@ def lce_leg(torch, tritium, iters: int = 3, warmup: int = 1, n=8192, d=4096, v=1
 
 
 # ------------------------------------------------------------ CPU leg --
+def gpt_leg(torch, steps: int = 10, warmup: int = 3):
+    """Config 5: the 151.9M-parameter GPT (12 x 768, SwiGLU 3072, vocab 50304, tied
+    embeddings) training step at B=16 x T=1024 on the kernel layer: bf16 compute,
+    fp32 master weights, fused AdamW; random-init weights, uniform random tokens."""
+    from helion_amd import gpt
+
+    cfg, tc = gpt.GPTConfig(), gpt.TrainConfig()
+    model = gpt.HipGPT(cfg, tc, gpt.init_params(cfg, tc.seed), torch.device("cuda"))
+    res = gpt.time_steps(model, cfg, tc, steps, warmup)
+    del model
+    torch.cuda.empty_cache()
+    return {"tokens_per_s": round(res["tokens_per_s"], 1), "ms_per_step": round(res["ms_per_step"], 3),
+            "mfu_vs_2.5PF": round(res["mfu"], 4), "loss": round(res["loss"], 4),
+            "params": gpt.n_params(cfg), "tokens_per_step": tc.batch * tc.seq_len}
+
+
 def cpu_baseline(budget_s: float = 12.0):
     """The reference's PyTorch formulas on this host's cores, over a bounded
     sample of the headline workload (1/4 of every op), in the same unit."""
@@ -368,8 +384,8 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--legs", default="rows,attention,lce",
-                    help="comma list of rows,attention,lce (rows is the headline)")
+    ap.add_argument("--legs", default="rows,attention,lce,gpt",
+                    help="comma list of rows,attention,lce,gpt (rows is the headline)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device copy 5 times (calibrates the HBM "
                          "byte counters of a profiler against a kernel of known traffic)")
@@ -407,6 +423,8 @@ def main(argv=None) -> int:
         if "lce" in legs:
             ops["linear_ce_fwd_bwd"] = lce_leg(torch, tritium, iters=args.steps,
                                                warmup=args.warmup)
+        if "gpt" in legs:
+            ops["gpt_train_step"] = gpt_leg(torch, steps=args.steps, warmup=args.warmup)
         print(json.dumps({"metric": METRIC, "partial": True, "ops": ops}), flush=True)
         return 0
     rows = row_leg(torch, tritium, args.steps, args.warmup)
@@ -420,6 +438,9 @@ def main(argv=None) -> int:
         if res is not None:
             ops["linear_ce_fwd_bwd"] = res
             print(f"[bench] linear-ce: {res}", file=sys.stderr, flush=True)
+    if "gpt" in legs:
+        ops["gpt_train_step"] = gpt_leg(torch)
+        print(f"[bench] gpt: {ops['gpt_train_step']}", file=sys.stderr, flush=True)
 
     adamw_gbs = rows["adamw_bytes"] / (rows["adamw_ms"] * 1e-3) / 1e9
     traffic = None

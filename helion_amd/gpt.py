@@ -1,0 +1,348 @@
+"""GPT training step on the MI355X kernel layer, and its pure-PyTorch twin.
+
+The model is the reference's decoder (examples/common.py:54-131:
+``TransformerBlock`` = residual-RMSNorm -> attention (helion/nn.py:169-220:
+q/k/v/o projections, RoPE on q and k, causal attention) -> residual-RMSNorm
+-> SwiGLU MLP, final residual-RMSNorm, ``linear_cross_entropy`` against the
+embedding matrix) at the 124M-class size of the benchmark: 12 layers,
+d_model 768, 12 heads x 64, MLP 3072, vocab 50304, tied embeddings
+(151,898,880 parameters), RoPE theta 1e4.
+
+Precision boundary.  The optimizer owns fp32 master weights in one flat
+buffer; each step runs on a bf16 working copy (one flat buffer, the model's
+parameters are views into it) and autograd accumulates the bf16 gradients
+into a flat buffer of pre-assigned ``.grad`` views.  After backward the
+gradients are widened to fp32 in one pass, ``adamw_step`` updates the whole
+flat master buffer in one launch, and one pass rounds it back into the
+working copy.  Activations are bf16 throughout; every op computes in fp32
+internally (the kernels' own rule), the residual stream is stored in bf16
+as the reference's residual-RMSNorm does (rmsnorm.py:72-83).
+
+Plain projections (q/k/v/o, gate/up/down) are library GEMMs (``torch.matmul``,
+hipBLASLt); everything on the kernel layer's hot path is a HIP kernel:
+residual-RMSNorm, RoPE, causal attention, SwiGLU, fused linear-cross-entropy
+and AdamW.
+
+``TorchTwin`` computes the same step with PyTorch only (F.rms_norm,
+F.scaled_dot_product_attention, F.silu, F.cross_entropy on materialised
+logits, torch.optim.AdamW) from identical initial weights and data, for the
+loss-curve parity check; its attention and norms run in fp32.
+
+Run ``python -m helion_amd.gpt --steps 200`` on a GPU for the parity report.
+"""
+
+from __future__ import annotations
+
+import argparse
+import dataclasses
+import json
+import math
+import time
+
+import torch
+import torch.nn.functional as F
+
+from .adamw import adamw_step
+from .attention import attention
+from .linear_ce import linear_cross_entropy
+from .rmsnorm import residual_rmsnorm
+from .rope import rope
+from .swiglu import swiglu
+
+
+@dataclasses.dataclass(frozen=True)
+class GPTConfig:
+    vocab_size: int = 50304
+    d_model: int = 768
+    n_layers: int = 12
+    n_heads: int = 12
+    head_dim: int = 64
+    d_ff: int = 3072
+    max_seq_len: int = 1024
+    rope_theta: float = 10000.0
+    eps: float = 1e-6
+
+
+@dataclasses.dataclass(frozen=True)
+class TrainConfig:
+    batch: int = 16
+    seq_len: int = 1024
+    lr: float = 6e-4
+    beta1: float = 0.9
+    beta2: float = 0.95
+    eps: float = 1e-8
+    weight_decay: float = 0.1
+    seed: int = 0
+
+
+def param_shapes(cfg: GPTConfig) -> list[tuple[str, tuple[int, ...]]]:
+    """Parameter names and shapes in a fixed order (the flat-buffer layout)."""
+    d, f = cfg.d_model, cfg.d_ff
+    qd = cfg.n_heads * cfg.head_dim
+    out = [("embed", (cfg.vocab_size, d))]
+    for i in range(cfg.n_layers):
+        p = f"blocks.{i}."
+        out += [
+            (p + "attn_norm", (d,)),
+            (p + "wq", (qd, d)),
+            (p + "wk", (qd, d)),
+            (p + "wv", (qd, d)),
+            (p + "wo", (d, qd)),
+            (p + "ffn_norm", (d,)),
+            (p + "w_gate", (f, d)),
+            (p + "w_up", (f, d)),
+            (p + "w_down", (d, f)),
+        ]
+    out.append(("final_norm", (d,)))
+    return out
+
+
+def init_params(cfg: GPTConfig, seed: int = 0) -> dict[str, torch.Tensor]:
+    """fp32 initial weights on the CPU: N(0, 0.02) for matrices and the
+    embedding (helion/nn.py:24, 48; examples/common.py:111), ones for norms."""
+    g = torch.Generator().manual_seed(seed)
+    params = {}
+    for name, shape in param_shapes(cfg):
+        if len(shape) == 1:
+            params[name] = torch.ones(shape, dtype=torch.float32)
+        else:
+            params[name] = torch.randn(shape, generator=g, dtype=torch.float32) * 0.02
+    return params
+
+
+def rope_tables(cfg: GPTConfig, device) -> tuple[torch.Tensor, torch.Tensor]:
+    """fp32 cos / sin [max_seq_len, head_dim/2] (helion/nn.py:179-184)."""
+    half = cfg.head_dim // 2
+    inv_freq = 1.0 / (cfg.rope_theta ** (torch.arange(0, half, dtype=torch.float64) / half))
+    t = torch.arange(cfg.max_seq_len, dtype=torch.float64)
+    freqs = torch.outer(t, inv_freq)
+    return (freqs.cos().to(device=device, dtype=torch.float32),
+            freqs.sin().to(device=device, dtype=torch.float32))
+
+
+def lm_batch(cfg: GPTConfig, tc: TrainConfig, gen: torch.Generator, device,
+             learnable: bool = False):
+    """Uniform random tokens (examples/common.py:146-153), drawn on the CPU
+    from ``gen`` so both models see the same batches.  ``learnable`` gives
+    each row consecutive ids from a random start instead (the next token is
+    predictable, so a working step lowers the loss)."""
+    shape = (tc.batch, tc.seq_len + 1)
+    if learnable:
+        start = torch.randint(cfg.vocab_size, (tc.batch, 1), generator=gen)
+        tokens = (start + torch.arange(shape[1])) % cfg.vocab_size
+    else:
+        tokens = torch.randint(cfg.vocab_size, shape, generator=gen)
+    tokens = tokens.to(device)
+    return tokens[:, :-1].contiguous(), tokens[:, 1:].contiguous()
+
+
+class _Flat:
+    """Views of ``param_shapes`` into one flat tensor."""
+
+    def __init__(self, cfg: GPTConfig, flat: torch.Tensor):
+        self.flat = flat
+        self.views: dict[str, torch.Tensor] = {}
+        off = 0
+        for name, shape in param_shapes(cfg):
+            n = math.prod(shape)
+            self.views[name] = flat[off:off + n].view(shape)
+            off += n
+        assert off == flat.numel()
+
+
+def n_params(cfg: GPTConfig) -> int:
+    return sum(math.prod(s) for _, s in param_shapes(cfg))
+
+
+class HipGPT:
+    """The model and its optimizer state on the HIP kernel layer."""
+
+    def __init__(self, cfg: GPTConfig, tc: TrainConfig, init: dict[str, torch.Tensor], device):
+        self.cfg, self.tc, self.device = cfg, tc, device
+        n = n_params(cfg)
+        self.master = _Flat(cfg, torch.empty(n, device=device, dtype=torch.float32))
+        for name, t in init.items():
+            self.master.views[name].copy_(t)
+        self.work = _Flat(cfg, self.master.flat.to(torch.bfloat16))
+        self.grad = _Flat(cfg, torch.zeros(n, device=device, dtype=torch.bfloat16))
+        self.grad32 = torch.empty(n, device=device, dtype=torch.float32)
+        self.exp_avg = torch.zeros(n, device=device, dtype=torch.float32)
+        self.exp_avg_sq = torch.zeros(n, device=device, dtype=torch.float32)
+        for name, p in self.work.views.items():
+            p.requires_grad_(True)
+            p.grad = self.grad.views[name]
+        self.cos, self.sin = rope_tables(cfg, device)
+        self.step_count = 0
+
+    def _w(self, name: str) -> torch.Tensor:
+        return self.work.views[name]
+
+    def loss(self, tokens: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
+        cfg = self.cfg
+        b, s = tokens.shape
+        nh, hd = cfg.n_heads, cfg.head_dim
+        pos = torch.arange(s, device=tokens.device).repeat(b)
+        cos, sin = self.cos[:s], self.sin[:s]
+        delta = self._w("embed")[tokens]
+        residual = torch.zeros_like(delta)
+        for i in range(cfg.n_layers):
+            p = f"blocks.{i}."
+            normed, residual = residual_rmsnorm(delta, residual, self._w(p + "attn_norm"), cfg.eps)
+            q = torch.matmul(normed, self._w(p + "wq").t()).reshape(b * s, nh, hd)
+            k = torch.matmul(normed, self._w(p + "wk").t()).reshape(b * s, nh, hd)
+            v = torch.matmul(normed, self._w(p + "wv").t())
+            q, k = rope(q, k, cos, sin, position_ids=pos)
+            o = attention(q.view(b, s, nh, hd).transpose(1, 2), k.view(b, s, nh, hd).transpose(1, 2),
+                          v.view(b, s, nh, hd).transpose(1, 2), is_causal=True)
+            o = o.transpose(1, 2).reshape(b, s, nh * hd)
+            delta = torch.matmul(o, self._w(p + "wo").t())
+            normed, residual = residual_rmsnorm(delta, residual, self._w(p + "ffn_norm"), cfg.eps)
+            h = swiglu(torch.matmul(normed, self._w(p + "w_gate").t()),
+                       torch.matmul(normed, self._w(p + "w_up").t()))
+            delta = torch.matmul(h, self._w(p + "w_down").t())
+        hidden, _ = residual_rmsnorm(delta, residual, self._w("final_norm"), cfg.eps)
+        return linear_cross_entropy(hidden, self._w("embed"), targets)
+
+    def train_step(self, tokens: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
+        """One step: forward, backward, fp32-master AdamW; returns the loss."""
+        tc = self.tc
+        self.grad.flat.zero_()
+        loss = self.loss(tokens, targets)
+        loss.backward()
+        self.step_count += 1
+        self.grad32.copy_(self.grad.flat)
+        adamw_step(self.master.flat, self.grad32, self.exp_avg, self.exp_avg_sq, lr=tc.lr,
+                   beta1=tc.beta1, beta2=tc.beta2, eps=tc.eps, weight_decay=tc.weight_decay,
+                   step=self.step_count)
+        with torch.no_grad():
+            self.work.flat.copy_(self.master.flat)
+        return loss.detach()
+
+    def grad_norm(self) -> float:
+        return float(self.grad32.norm())
+
+
+class TorchTwin:
+    """The same model, data and update in plain PyTorch (no kernel-layer op)."""
+
+    def __init__(self, cfg: GPTConfig, tc: TrainConfig, init: dict[str, torch.Tensor], device):
+        self.cfg, self.tc = cfg, tc
+        self.master = {k: v.to(device).clone().requires_grad_(True) for k, v in init.items()}
+        self.opt = torch.optim.AdamW(list(self.master.values()), lr=tc.lr,
+                                     betas=(tc.beta1, tc.beta2), eps=tc.eps,
+                                     weight_decay=tc.weight_decay, foreach=False)
+        self.cos, self.sin = rope_tables(cfg, device)
+
+    def _rope(self, x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+        half = x.shape[-1] // 2
+        x = x.float()
+        a, b = x[..., :half], x[..., half:]
+        return torch.cat([a * cos - b * sin, b * cos + a * sin], dim=-1).to(torch.bfloat16)
+
+    def _norm(self, delta, residual, w):
+        z = delta.float() + residual.float()
+        out = F.rms_norm(z, (z.shape[-1],), w.float(), self.cfg.eps)
+        return out.to(torch.bfloat16), z.to(torch.bfloat16)
+
+    def loss(self, work: dict[str, torch.Tensor], tokens, targets) -> torch.Tensor:
+        cfg = self.cfg
+        b, s = tokens.shape
+        nh, hd = cfg.n_heads, cfg.head_dim
+        cos = self.cos[:s].view(1, s, 1, hd // 2)
+        sin = self.sin[:s].view(1, s, 1, hd // 2)
+        delta = work["embed"][tokens]
+        residual = torch.zeros_like(delta)
+        for i in range(cfg.n_layers):
+            p = f"blocks.{i}."
+            normed, residual = self._norm(delta, residual, work[p + "attn_norm"])
+            q = self._rope((normed @ work[p + "wq"].t()).view(b, s, nh, hd), cos, sin)
+            k = self._rope((normed @ work[p + "wk"].t()).view(b, s, nh, hd), cos, sin)
+            v = (normed @ work[p + "wv"].t()).view(b, s, nh, hd)
+            o = F.scaled_dot_product_attention(q.transpose(1, 2).float(), k.transpose(1, 2).float(),
+                                               v.transpose(1, 2).float(), is_causal=True)
+            o = o.transpose(1, 2).reshape(b, s, nh * hd).to(torch.bfloat16)
+            delta = o @ work[p + "wo"].t()
+            normed, residual = self._norm(delta, residual, work[p + "ffn_norm"])
+            gate = (normed @ work[p + "w_gate"].t()).float()
+            up = (normed @ work[p + "w_up"].t()).float()
+            delta = (F.silu(gate) * up).to(torch.bfloat16) @ work[p + "w_down"].t()
+        hidden, _ = self._norm(delta, residual, work["final_norm"])
+        logits = hidden.reshape(-1, cfg.d_model) @ work["embed"].t()
+        return F.cross_entropy(logits.float(), targets.reshape(-1))
+
+    def train_step(self, tokens, targets) -> torch.Tensor:
+        work = {k: v.detach().to(torch.bfloat16).requires_grad_(True)
+                for k, v in self.master.items()}
+        loss = self.loss(work, tokens, targets)
+        loss.backward()
+        for k, p in self.master.items():
+            p.grad = work[k].grad.float()
+        self.opt.step()
+        self.opt.zero_grad(set_to_none=True)
+        self.last_grad_norm = float(torch.norm(torch.stack([
+            work[k].grad.float().norm() for k in self.master])))
+        return loss.detach()
+
+
+def time_steps(model: HipGPT, cfg: GPTConfig, tc: TrainConfig, steps: int, warmup: int,
+               seed: int = 0) -> dict:
+    """Tokens per second of ``model.train_step`` (batches pre-generated)."""
+    gen = torch.Generator().manual_seed(seed)
+    batches = [lm_batch(cfg, tc, gen, model.device) for _ in range(steps + warmup)]
+    for i in range(warmup):
+        model.train_step(*batches[i])
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(warmup, warmup + steps):
+        loss = model.train_step(*batches[i])
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    tokens = tc.batch * tc.seq_len
+    flops = 6 * n_params(cfg) * tokens + 6 * cfg.n_layers * tc.seq_len * cfg.d_model * tokens
+    return {"ms_per_step": dt * 1e3, "tokens_per_s": tokens / dt, "loss": float(loss),
+            "mfu": flops / dt / 2.5e15}
+
+
+def parity(steps: int, cfg: GPTConfig, tc: TrainConfig, device, learnable: bool = False) -> dict:
+    """Loss curves of HipGPT and TorchTwin over ``steps`` steps from the same
+    weights and batches; returns both curves and the largest relative gap."""
+    init = init_params(cfg, tc.seed)
+    ours = HipGPT(cfg, tc, init, device)
+    twin = TorchTwin(cfg, tc, init, device)
+    gen = torch.Generator().manual_seed(tc.seed + 1)
+    la, lb, ga, gb = [], [], [], []
+    for _ in range(steps):
+        tokens, targets = lm_batch(cfg, tc, gen, device, learnable)
+        la.append(float(ours.train_step(tokens, targets)))
+        ga.append(ours.grad_norm())
+        lb.append(float(twin.train_step(tokens, targets)))
+        gb.append(twin.last_grad_norm)
+    gap = max(abs(a - b) / abs(b) for a, b in zip(la, lb))
+    return {"steps": steps, "loss_hip": la, "loss_torch": lb, "grad_norm_hip": ga,
+            "grad_norm_torch": gb, "max_rel_loss_gap": gap}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description="config-5 GPT: loss parity and tokens/s")
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--out", default="")
+    ap.add_argument("--layers", type=int, default=12)
+    ap.add_argument("--batch", type=int, default=16)
+    args = ap.parse_args(argv)
+    cfg = GPTConfig(n_layers=args.layers)
+    tc = TrainConfig(batch=args.batch)
+    dev = torch.device("cuda")
+    res = parity(args.steps, cfg, tc, dev)
+    summary = {k: v for k, v in res.items() if not isinstance(v, list)}
+    summary["loss_first_last_hip"] = [res["loss_hip"][0], res["loss_hip"][-1]]
+    summary["loss_first_last_torch"] = [res["loss_torch"][0], res["loss_torch"][-1]]
+    summary["grad_norm_step1"] = [res["grad_norm_hip"][0], res["grad_norm_torch"][0]]
+    print(json.dumps(summary))
+    if args.out:
+        with open(args.out, "w") as f:
+            json.dump(res, f)
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())
