@@ -18,8 +18,9 @@ working copy.  Activations are bf16 throughout; every op computes in fp32
 internally (the kernels' own rule), the residual stream is stored in bf16
 as the reference's residual-RMSNorm does (rmsnorm.py:72-83).
 
-Plain projections (q/k/v/o, gate/up/down) are library GEMMs (``torch.matmul``,
-hipBLASLt); everything on the kernel layer's hot path is a HIP kernel:
+Plain projections (q/k/v fused into one, o, gate/up/down) are library GEMMs
+(``torch.matmul``, hipBLASLt); everything on the kernel layer's hot path is a
+HIP kernel:
 residual-RMSNorm, RoPE, causal attention, SwiGLU, fused linear-cross-entropy
 and AdamW.
 
@@ -137,17 +138,31 @@ def lm_batch(cfg: GPTConfig, tc: TrainConfig, gen: torch.Generator, device,
 
 
 class _Flat:
-    """Views of ``param_shapes`` into one flat tensor."""
+    """Views of ``param_shapes`` into one flat tensor, plus each layer's fused
+    q/k/v projection ``blocks.i.wqkv`` [3 * n_heads * head_dim, d_model]
+    (wq, wk, wv are adjacent in the layout, so it is a view too)."""
 
     def __init__(self, cfg: GPTConfig, flat: torch.Tensor):
         self.flat = flat
         self.views: dict[str, torch.Tensor] = {}
+        offsets = {}
         off = 0
         for name, shape in param_shapes(cfg):
             n = math.prod(shape)
             self.views[name] = flat[off:off + n].view(shape)
+            offsets[name] = off
             off += n
         assert off == flat.numel()
+        qd = cfg.n_heads * cfg.head_dim
+        for i in range(cfg.n_layers):
+            o = offsets[f"blocks.{i}.wq"]
+            self.views[f"blocks.{i}.wqkv"] = flat[o:o + 3 * qd * cfg.d_model].view(3 * qd, cfg.d_model)
+
+    def leaves(self) -> dict[str, torch.Tensor]:
+        """The tensors the model differentiates: every parameter except the
+        separate q/k/v views, which the fused wqkv covers."""
+        return {k: v for k, v in self.views.items()
+                if not k.endswith((".wq", ".wk", ".wv"))}
 
 
 def n_params(cfg: GPTConfig) -> int:
@@ -168,7 +183,7 @@ class HipGPT:
         self.grad32 = torch.empty(n, device=device, dtype=torch.float32)
         self.exp_avg = torch.zeros(n, device=device, dtype=torch.float32)
         self.exp_avg_sq = torch.zeros(n, device=device, dtype=torch.float32)
-        for name, p in self.work.views.items():
+        for name, p in self.work.leaves().items():
             p.requires_grad_(True)
             p.grad = self.grad.views[name]
         self.cos, self.sin = rope_tables(cfg, device)
@@ -188,12 +203,12 @@ class HipGPT:
         for i in range(cfg.n_layers):
             p = f"blocks.{i}."
             normed, residual = residual_rmsnorm(delta, residual, self._w(p + "attn_norm"), cfg.eps)
-            q = torch.matmul(normed, self._w(p + "wq").t()).reshape(b * s, nh, hd)
-            k = torch.matmul(normed, self._w(p + "wk").t()).reshape(b * s, nh, hd)
-            v = torch.matmul(normed, self._w(p + "wv").t())
+            qkv = torch.matmul(normed, self._w(p + "wqkv").t()).view(b, s, 3, nh, hd)
+            q = qkv[:, :, 0].reshape(b * s, nh, hd).contiguous()
+            k = qkv[:, :, 1].reshape(b * s, nh, hd).contiguous()
             q, k = rope(q, k, cos, sin, position_ids=pos)
             o = attention(q.view(b, s, nh, hd).transpose(1, 2), k.view(b, s, nh, hd).transpose(1, 2),
-                          v.view(b, s, nh, hd).transpose(1, 2), is_causal=True)
+                          qkv[:, :, 2].transpose(1, 2), is_causal=True)
             o = o.transpose(1, 2).reshape(b, s, nh * hd)
             delta = torch.matmul(o, self._w(p + "wo").t())
             normed, residual = residual_rmsnorm(delta, residual, self._w(p + "ffn_norm"), cfg.eps)
