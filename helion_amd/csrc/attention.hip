@@ -1190,6 +1190,197 @@ attn_bwd_dkdv_v2(BwdArgs a) {
   }
 }
 
+// dK, dV with wavefront pairs: a workgroup owns 128 kv rows of one
+// (batch, kv head); wavefronts p and p + 4 (same SIMD) share kv rows
+// 32p .. 32p + 31.  Per 64-row query tile, in two phases split by barriers:
+//   phase 1  A (p):     S = Q K^T -> P = exp(S*scale - lse), masked; P goes
+//                       to LDS (fp32) and stays in registers as bf16;
+//            B (p + 4): dP = dO V^T (kept in registers);
+//   phase 2  A:         dV^T += dO^T P;
+//            B:         dS = P (dP - D_i) from A's P, dK^T += Q^T dS.
+// Each role keeps one set of fragments (K for A, V for B) and one set of
+// accumulators (dV / dK), half of what one wavefront doing both needs, so
+// two wavefronts fit per SIMD, and the roles' VALU work (A's exponentials in
+// phase 1, B's dS in phase 2) runs while the other role's MFMAs execute.
+constexpr int kPairWaves = 8;
+constexpr int kPairBN = 128;
+
+template <typename T, int D>
+__global__ void __launch_bounds__(64 * kPairWaves)
+attn_bwd_dkdv_pair(BwdArgs a) {
+  typedef Mfma<T> M;
+  typedef typename M::V V;
+  typedef BTile<D> P;
+  constexpr int KS = D / 16;
+  constexpr int MT = D / 32;
+  constexpr int STAGE = 2 * P::BYTES + 512;  // Q, dO, lse[64], delta[64]
+  constexpr int XCH = 2 * 4 * 64 * 16;       // per pair: 2 query halves x [4][64 lanes][4 fp32]
+  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+  __shared__ __attribute__((aligned(16))) char xch_all[4 * XCH];
+
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int l32 = lane & 31, g = lane >> 5;
+  const int pair = wave & 3;
+  const bool role_b = wave >= 4;  // wave-uniform
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int bhk = w / a.n_tiles;
+  const int kt = w % a.n_tiles;  // kt = 0 sees the most queries: heaviest first
+  const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
+  const int group = a.H / a.Hkv;
+  const int kv0 = kt * kPairBN;
+  const int kvb = kv0 + pair * 32;
+  const int kvw = kvb + l32;
+  const bool kvvalid = kvw < a.Tkv;
+  const float sl2 = a.scale * kLog2e;
+  char* xch = xch_all + pair * XCH;
+
+  // A: K rows, B: V rows of this lane's kv row
+  const T* fp = role_b ? (const T*)a.v + b * a.sv_b + hk * a.sv_h + (int64_t)kvw * a.sv_s
+                       : (const T*)a.k + b * a.sk_b + hk * a.sk_h + (int64_t)kvw * a.sk_s;
+  V frag[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) frag[s] = kvvalid ? ld8(fp + 16 * s + 8 * g) : zero8<T>();
+  f32x16 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = zero16();
+
+  const int q_begin = a.causal ? kv0 : 0;
+  const int n_q = a.Tq > q_begin ? (int)cdiv(a.Tq - q_begin, 64) : 0;
+  const int n_steps = n_q * group;
+  BtDma<T, D, kPairWaves> dma;
+  dma.init(a.sq_s, a.sdo_s);
+  auto issue = [&](int step, char* stage) {
+    const int hq = hk * group + step / n_q;
+    const int q0 = q_begin + (step % n_q) * 64;
+    const T* qp = (const T*)a.q + b * a.sq_b + hq * a.sq_h;
+    const T* dop = (const T*)a.dout + b * a.sdo_b + hq * a.sdo_h;
+    dma.issue(stage, qp, a.sq_s, dop, a.sdo_s, q0, a.Tq);
+    const int64_t row = ((int64_t)b * a.H + hq) * a.Tq + min(q0 + lane, a.Tq - 1);
+    if (wave == 0) dma4(a.lse + row, __builtin_amdgcn_readfirstlane(lds_addr(stage + 2 * P::BYTES)));
+    if (wave == 1)
+      dma4(a.delta + row, __builtin_amdgcn_readfirstlane(lds_addr(stage + 2 * P::BYTES + 256)));
+  };
+  if (n_steps > 0) issue(0, smem);
+  for (int step = 0; step < n_steps; ++step) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) pin_vgpr(acc[mt]);
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (step + 1 < n_steps) issue(step + 1, smem + ((step + 1) & 1) * STAGE);
+    const int q0 = q_begin + (step % n_q) * 64;
+    const bool active = !(a.causal && q0 + 63 < kvb);  // pair-uniform
+    const char* Qs = smem + (step & 1) * STAGE;
+    const char* dOs = Qs + P::BYTES;
+    const float* lse_s = reinterpret_cast<const float*>(Qs + 2 * P::BYTES);
+    const float* del_s = lse_s + 64;
+    const char* T1 = role_b ? dOs : Qs;  // phase-1 row operand
+    const char* T2 = role_b ? Qs : dOs;  // phase-2 transposed operand
+    const bool need_mask = (a.causal && q0 < kvb + 31) || q0 + 64 > a.Tq;
+
+    // phase 1: x = T1 * frag^T for both 32-row query halves
+    f32x16 x[2];
+    V op[2][2];
+    if (active) {
+      // MFMA i = 2 st + mq (the two query halves interleaved); row fragments
+      // are read kRing MFMAs ahead of use, fenced so the order holds
+      x[0] = zero16();
+      x[1] = zero16();
+      V rb[kRing];
+#pragma unroll
+      for (int i = 0; i < kRing; ++i) rb[i] = bt_row<T, D>(T1, 32 * (i & 1), i >> 1);
+#pragma unroll
+      for (int i = 0; i < 2 * KS; ++i) {
+        sched_fence();
+        x[i & 1] = M::mma(rb[i % kRing], frag[i >> 1], x[i & 1]);
+        if (i + kRing < 2 * KS) rb[i % kRing] = bt_row<T, D>(T1, 32 * ((i + kRing) & 1), (i + kRing) >> 1);
+      }
+      sched_fence();
+      if (!role_b) {
+#pragma unroll
+        for (int mq = 0; mq < 2; ++mq) {
+          // x[mq][r] = S[q0 + 32mq + 8(r/4) + 4g + r%4][kvw]; masked scores -> -inf (P = 0)
+          if (need_mask) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int q = q0 + 32 * mq + 8 * (r >> 2) + 4 * g + (r & 3);
+              x[mq][r] = (q >= a.Tq || (a.causal && kvw > q)) ? -INFINITY : x[mq][r];
+            }
+          }
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const float4 L = *reinterpret_cast<const float4*>(lse_s + 32 * mq + 8 * rr + 4 * g);
+            const float lv[4] = {L.x * kLog2e, L.y * kLog2e, L.z * kLog2e, L.w * kLog2e};
+            float4 pv;
+            float* pf = reinterpret_cast<float*>(&pv);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              const float p = fast_exp2(fmaf(x[mq][4 * rr + j], sl2, -lv[j]));
+              x[mq][4 * rr + j] = p;
+              pf[j] = p;
+            }
+            *reinterpret_cast<float4*>(xch + ((mq * 4 + rr) * 64 + lane) * 16) = pv;
+          }
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) op[mq][t][j] = (T)x[mq][8 * t + j];
+        }
+      }
+    }
+    __syncthreads();  // A's P is visible to B
+    if (active) {
+      if (role_b) {
+#pragma unroll
+        for (int mq = 0; mq < 2; ++mq) {
+          float ds[16];
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const float4 pv = *reinterpret_cast<const float4*>(xch + ((mq * 4 + rr) * 64 + lane) * 16);
+            const float4 Dl = *reinterpret_cast<const float4*>(del_s + 32 * mq + 8 * rr + 4 * g);
+            ds[4 * rr + 0] = pv.x * (x[mq][4 * rr + 0] - Dl.x);
+            ds[4 * rr + 1] = pv.y * (x[mq][4 * rr + 1] - Dl.y);
+            ds[4 * rr + 2] = pv.z * (x[mq][4 * rr + 2] - Dl.z);
+            ds[4 * rr + 3] = pv.w * (x[mq][4 * rr + 3] - Dl.w);
+          }
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) op[mq][t][j] = (T)ds[8 * t + j];
+        }
+      }
+      // phase 2: acc^T += T2^T * op (A: dV^T += dO^T P, B: dK^T += Q^T dS);
+      // MFMA i = MT (2 mq + t) + mt, transposed fragments kRing ahead
+      constexpr int N2 = 4 * MT;
+      auto tread = [&](int i) { return bt_tr<T, D>(T2, 16 * (i / MT), i % MT); };
+      V tb[kRing];
+#pragma unroll
+      for (int i = 0; i < kRing; ++i) tb[i] = tread(i);
+#pragma unroll
+      for (int i = 0; i < N2; ++i) {
+        sched_fence();
+        acc[i % MT] = M::mma(tb[i % kRing], op[(i / MT) >> 1][(i / MT) & 1], acc[i % MT]);
+        if (i + kRing < N2) tb[i % kRing] = tread(i + kRing);
+      }
+      sched_fence();
+    }
+  }
+
+  if (kvvalid) {
+    T* out = role_b ? (T*)a.dk + b * a.sdk_b + hk * a.sdk_h + (int64_t)kvw * a.sdk_s
+                    : (T*)a.dv + b * a.sdv_b + hk * a.sdv_h + (int64_t)kvw * a.sdv_s;
+    const float sc = role_b ? a.scale : 1.0f;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d0 = 32 * mt + 8 * rr + 4 * g;
+        store4<T>(out + d0, acc[mt][4 * rr] * sc, acc[mt][4 * rr + 1] * sc,
+                  acc[mt][4 * rr + 2] * sc, acc[mt][4 * rr + 3] * sc);
+      }
+    }
+  }
+}
+
 // dQ: a workgroup owns 32 * WAVES query rows of one (batch, head), a
 // wavefront 32 of them (Q, dO fragments in registers, lane = query row),
 // and sweeps the 64-row K/V tiles it can see: S^T = K Q^T and
@@ -1538,6 +1729,9 @@ int fwd_simt(const FwdArgs& a, int64_t D, hipStream_t st) {
 #ifndef TRI_ATTN_DKDV_WAVES
 #define TRI_ATTN_DKDV_WAVES 4
 #endif
+#ifndef TRI_ATTN_DKDV_PAIR
+#define TRI_ATTN_DKDV_PAIR 1
+#endif
 #ifndef TRI_ATTN_DQ_WAVES
 #define TRI_ATTN_DQ_WAVES 4
 #endif
@@ -1551,6 +1745,12 @@ int bwd_v2(const BwdArgs& a, hipStream_t st) {
   const int64_t q_blocks = (int64_t)x.n_tiles * a.B * a.H;
   attn_bwd_dq_v2<T, D, WQ><<<(unsigned)q_blocks, 64 * WQ, 0, st>>>(x);
   if (int e = check_launch("attention backward (dq, mfma)")) return e;
+  if (TRI_ATTN_DKDV_PAIR) {
+    x.n_tiles = (int)cdiv(a.Tkv, kPairBN);
+    const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;
+    attn_bwd_dkdv_pair<T, D><<<(unsigned)kv_blocks, 64 * kPairWaves, 0, st>>>(x);
+    return check_launch("attention backward (dk/dv, mfma pairs)");
+  }
   x.n_tiles = (int)cdiv(a.Tkv, 32 * WK);
   const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;
   attn_bwd_dkdv_v2<T, D, WK><<<(unsigned)kv_blocks, 64 * WK, 0, st>>>(x);
