@@ -568,6 +568,29 @@ int bwd_impl(const float* grad_out, const void* hidden, const void* weight, cons
   return TRI_OK;
 }
 
+// G for vocabulary rows [v0, v0 + vc) only (no G^T), row stride ld_g.
+template <typename T, typename TT>
+int grad_logits_impl(const float* grad_out, const float* n_valid, const void* hidden,
+                     const void* weight, const void* target, int64_t ignore_index,
+                     const float* lse, void* g, int64_t ld_g, int64_t N, int64_t D, int64_t v0,
+                     int64_t vc, hipStream_t st) {
+  GArgs ga;
+  ga.hidden = hidden;
+  ga.weight = (const T*)weight + v0 * D;
+  ga.target = target;
+  ga.lse = lse;
+  ga.grad_out = grad_out;
+  ga.n_valid = n_valid;
+  ga.gt = nullptr;
+  ga.gm = g;
+  ga.N = N; ga.D = D; ga.Vc = vc; ga.ld = D;
+  ga.ld_gt = 0; ga.ld_g = ld_g; ga.vc0 = v0; ga.ignore_index = ignore_index;
+  ga.tiles_v = (int)cdiv(vc, CfgT<T>::BM);
+  ga.tiles_n = (int)cdiv(N, CfgT<T>::BN);
+  lce_g_kernel<T, TT><<<(unsigned)((int64_t)ga.tiles_v * ga.tiles_n), CfgT<T>::THREADS, 0, st>>>(ga);
+  return check_launch("linear_ce gradient of the logits");
+}
+
 #define TRI_DISPATCH_TARGET(kind, TT, ...)                                         \
   do {                                                                             \
     if ((kind) == 1) { typedef int32_t TT; __VA_ARGS__; }                          \
@@ -630,5 +653,27 @@ extern "C" int tritium_linear_ce_bwd(const float* grad_out, const void* hidden, 
       return bwd_impl<T, TT>(grad_out, hidden, weight, target, ignore_index, lse, dhidden,
                              dweight, workspace, workspace_bytes, n_rows, hidden_size, vocab,
                              chunk_rows, st)));
+  return TRI_OK;
+}
+
+extern "C" int tritium_linear_ce_grad_logits(const float* grad_out, const float* n_valid,
+                                             const void* hidden, const void* weight,
+                                             const void* target, int target_kind,
+                                             int64_t ignore_index, const float* lse, void* g,
+                                             int64_t ld_g, int64_t n_rows, int64_t hidden_size,
+                                             int64_t vocab, int64_t v0, int64_t vc, int dtype,
+                                             void* stream) {
+  if (int e = check_sizes(n_rows, hidden_size, vocab, dtype)) return e;
+  if (v0 < 0 || vc < 0 || v0 + vc > vocab || ld_g < vc)
+    return fail(TRI_EINVAL, "linear_ce grad_logits: bad chunk v0=%lld vc=%lld ld_g=%lld of vocab %lld",
+                (long long)v0, (long long)vc, (long long)ld_g, (long long)vocab);
+  if (n_rows == 0 || vc == 0) return TRI_OK;
+  if (!aligned16(hidden) || !aligned16(weight) || !aligned16(g) || ld_g % 8 != 0)
+    return fail(TRI_EINVAL, "linear_ce grad_logits: buffers must be 16-byte aligned, ld_g a multiple of 8");
+  hipStream_t st = (hipStream_t)stream;
+  TRI_DISPATCH_TARGET(target_kind, TT,
+    TRI_DISPATCH_FLOAT(dtype, T,
+      return grad_logits_impl<T, TT>(grad_out, n_valid, hidden, weight, target, ignore_index, lse,
+                                     g, ld_g, n_rows, hidden_size, v0, vc, st)));
   return TRI_OK;
 }

@@ -140,8 +140,84 @@ def _linear_cross_entropy_forward(hidden, weight, target, ignore_index: int = IG
     return loss, lse
 
 
+_G_CHUNK_BYTES = 1 << 30  # gradient-of-logits tile per chunk
+_mm_out_dtype: bool | None = None  # torch.mm(..., out_dtype=float32) available on this device
+
+
+def _mm_f32_into(acc: torch.Tensor, a: torch.Tensor, b: torch.Tensor) -> None:
+    """acc += a @ b with fp32 accumulation: one library GEMM with an fp32
+    output where torch offers it, else a 16-bit product added in fp32."""
+    global _mm_out_dtype
+    if _mm_out_dtype is not False:
+        try:
+            acc.add_(torch.mm(a, b, out_dtype=torch.float32))
+            _mm_out_dtype = True
+            return
+        except (RuntimeError, NotImplementedError, TypeError):
+            _mm_out_dtype = False
+    acc.add_(torch.mm(a, b))
+
+
 def _backward(grad_out, hidden_2d, weight, target_1d, lse, need_dh, need_dw, ignore_index,
               chunk_rows: int = 0):
+    """Per vocabulary chunk: the HIP kernel recomputes the logits in registers
+    and writes only G = (softmax - onehot) * grad_out / n_valid
+    (``tritium_linear_ce_grad_logits``); dH += G W_c and dW_c = G^T H are
+    plain GEMMs on views of G, H and W (library GEMMs, no transposed copies).
+    dH accumulates over chunks in fp32; each dW chunk reduces over all rows
+    in one GEMM and is rounded once (cross_entropy.py:928-957 does the same
+    chunking with bf16 accumulation)."""
+    n_rows, hidden_size = hidden_2d.shape
+    vocab_size = weight.shape[0]
+    dev = hidden_2d.device
+    h2 = _kernel_operand(hidden_2d)
+    w2 = _kernel_operand(weight)
+    dp = h2.shape[-1]
+    g = grad_out.detach().to(device=dev, dtype=torch.float32).reshape(())
+    n_valid = (target_1d != ignore_index).sum(dtype=torch.float32)
+    chunk = int(chunk_rows) if chunk_rows > 0 else max(256, (_G_CHUNK_BYTES // (2 * n_rows)) // 256 * 256)
+    chunk = min(chunk, vocab_size)
+    ld_g = -(-chunk // 8) * 8
+    gbuf = torch.empty((n_rows, ld_g), device=dev, dtype=weight.dtype)
+    n_chunks = -(-vocab_size // chunk)
+    dh = dh32 = None
+    if need_dh:
+        if n_chunks == 1:
+            dh = torch.empty((n_rows, dp), device=dev, dtype=hidden_2d.dtype)
+        else:
+            dh32 = torch.zeros((n_rows, dp), device=dev, dtype=torch.float32)
+    dw = torch.empty((vocab_size, dp), device=dev, dtype=weight.dtype) if need_dw else None
+    for c in range(n_chunks):
+        v0 = c * chunk
+        vc = min(chunk, vocab_size - v0)
+        _lib.call(
+            "tritium_linear_ce_grad_logits", g.data_ptr(), n_valid.data_ptr(), h2.data_ptr(),
+            w2.data_ptr(), target_1d.data_ptr(), _target_kind(target_1d), int(ignore_index),
+            lse.data_ptr(), gbuf.data_ptr(), ld_g, n_rows, dp, vocab_size, v0, vc,
+            _lib.dtype_code(weight.dtype), _lib.stream_of(hidden_2d),
+        )
+        gc = gbuf[:, :vc]
+        if need_dh:
+            if dh is not None:
+                torch.mm(gc, w2[v0:v0 + vc], out=dh)
+            else:
+                _mm_f32_into(dh32, gc, w2[v0:v0 + vc])
+        if need_dw:
+            torch.mm(gc.t(), h2, out=dw[v0:v0 + vc])
+    if dh32 is not None:
+        dh = dh32.to(hidden_2d.dtype)
+    if dp != hidden_size:
+        dh = dh[:, :hidden_size].contiguous() if dh is not None else None
+        dw = dw[:, :hidden_size].contiguous() if dw is not None else None
+    return dh, dw
+
+
+def _backward_capi(grad_out, hidden_2d, weight, target_1d, lse, need_dh, need_dw, ignore_index,
+                   chunk_rows: int = 0):
+    """The whole backward inside the library (``tritium_linear_ce_bwd``: the
+    same gradient tiles plus its own GEMM core for dH and dW) -- the entry a
+    C caller uses; the autograd path above hands the two plain GEMMs to the
+    GEMM library instead."""
     n_rows, hidden_size = hidden_2d.shape
     vocab_size = weight.shape[0]
     dev = hidden_2d.device

@@ -164,6 +164,21 @@ int tritium_linear_ce_bwd(const float* grad_out, const void* hidden, const void*
                           size_t workspace_bytes, int64_t n_rows, int64_t hidden_size,
                           int64_t vocab, int64_t chunk_rows, int dtype, void* stream);
 
+/* Gradient of the logits for one vocabulary chunk, the fused part of
+ * linear_cross_entropy_backward (reference cross_entropy.py:928-946: the
+ * per-chunk F.linear + in-place CE kernel; its mm/addmm at 947-957 are plain
+ * GEMMs the caller runs on these rows): for vocabulary rows [v0, v0 + vc),
+ *   g[n, j] = (exp(hidden[n] . weight[v0 + j] - lse[n]) - [target[n] == v0 + j])
+ *             * grad_out / n_valid,   0 for rows whose target == ignore_index,
+ * written to g [n_rows, vc] with row stride ld_g (a multiple of 8) in
+ * `dtype`; the logits themselves exist only in registers.  grad_out and
+ * n_valid (the number of non-ignored targets) are device floats. */
+int tritium_linear_ce_grad_logits(const float* grad_out, const float* n_valid, const void* hidden,
+                                  const void* weight, const void* target, int target_kind,
+                                  int64_t ignore_index, const float* lse, void* g, int64_t ld_g,
+                                  int64_t n_rows, int64_t hidden_size, int64_t vocab, int64_t v0,
+                                  int64_t vc, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

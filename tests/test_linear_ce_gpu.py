@@ -41,7 +41,7 @@ def _close(got, want, atol, what):
 
 
 def _run(n, d, v, dtype, seed=0, ignore_frac=0.0, tdtype=torch.int64, chunk_rows=0,
-         wscale=0.02):
+         wscale=0.02, backward=None):
     h, w, t = _inputs(n, d, v, dtype, seed, ignore_frac, tdtype, wscale)
     loss, lse = tritium.linear_ce._linear_cross_entropy_forward(h, w, t)
     ref_loss, ref_lse = oracle.linear_ce.forward(np32(h), np32(w), np32(t))
@@ -49,7 +49,8 @@ def _run(n, d, v, dtype, seed=0, ignore_frac=0.0, tdtype=torch.int64, chunk_rows
     _close(loss, ref_loss, tol, "loss")
     _close(lse, ref_lse, tol, "lse")
     g = torch.tensor(1.0, device="cuda")
-    dh, dw = tritium.linear_ce._backward(g, h, w, t, lse, True, True, -100, chunk_rows)
+    backward = backward or tritium.linear_ce._backward
+    dh, dw = backward(g, h, w, t, lse, True, True, -100, chunk_rows)
     edh, edw = oracle.linear_ce.backward(1.0, np32(h), np32(w), np32(t), ref_lse)
     _close(dh, edh, tol, "dhidden")
     _close(dw, edw, tol, "dweight")
@@ -77,6 +78,15 @@ def test_linear_ce_ragged_and_ignore_index(dtype):
 def test_linear_ce_multi_chunk_backward(dtype):
     # five vocab chunks of 256 rows: dhidden accumulates across chunks in fp32
     _run(200, 128, 1200, dtype, seed=5, ignore_frac=0.05, chunk_rows=256)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_linear_ce_backward_c_entry(dtype):
+    # the all-in-library backward (tritium_linear_ce_bwd, its own GEMM core and
+    # transposed operands) that a C caller uses instead of the library GEMMs
+    full = tritium.linear_ce._backward_capi
+    _run(300, 96, 777, dtype, seed=9, ignore_frac=0.1, backward=full)
+    _run(200, 128, 1200, dtype, seed=10, ignore_frac=0.05, chunk_rows=256, backward=full)
 
 
 def test_linear_ce_odd_hidden_size_is_padded():
