@@ -359,6 +359,131 @@ attn_fwd_mfma(FwdArgs a) {
   }
 }
 
+// ------------------------------- 64-row tiles in LDS, head_dim 64 and 128 --
+// The head_dim 64/128 kernels stage 64-row tiles of K/V (forward, dQ) or
+// Q/dO (dK/dV) in LDS by direct global->LDS DMA, row-major, double-buffered,
+// and read them two ways: as MFMA A operands along rows (16-byte reads of 32 rows)
+// and transposed (ds_read_b64_tr_b16: the A operand of X^T, m = column of
+// X, k = 16 rows of X).  The 16-byte granule c of row r sits at slot
+// c ^ key(r); key makes both reads bank-conflict free:
+//   * 16 consecutive rows at one granule hit 16 distinct 16-byte bank groups
+//     (256-byte rows: key is a bijection of r & 15; 128-byte rows: of
+//     (r >> 1) & 7, rows of opposite parity already use opposite halves);
+//   * 4 consecutive rows x 4 consecutive granules (one 32-lane cycle of a
+//     transposing read) land in 16 distinct groups (bits 3:2 of the key,
+//     bit 2 for 128-byte rows, differ between rows of one parity).
+template <int D>
+struct BTile {
+  static_assert(D == 64 || D == 128, "head_dim");
+  static constexpr int RB = 2 * D;              // bytes per row
+  static constexpr int GR = RB / 16;            // granules per row
+  static constexpr int BYTES = 64 * RB;         // one 64-row tile
+  static constexpr int DMA_ROWS = 1024 / RB;    // rows per wave-wide DMA
+  static constexpr int DMAS = BYTES / 1024;     // wave-wide DMAs per tile
+  static __device__ __forceinline__ int key(int r) {
+    if constexpr (GR == 16) return ((r & 3) << 2) | ((r >> 2) & 3);
+    else return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
+  }
+  static __device__ __forceinline__ int off(int r, int c) { return r * RB + ((c ^ key(r)) << 4); }
+};
+
+// DMA two 64-row tiles (x rows r0.. of x and y, rows clamped to n_rows - 1)
+// into dst and dst + BYTES, spread over the WAVES wavefronts.
+template <typename T, int D, int WAVES>
+__device__ __forceinline__ void bt_dma2(char* dst, const T* x, int64_t sx, const T* y, int64_t sy,
+                                        int r0, int n_rows) {
+  typedef BTile<D> P;
+  constexpr int PER = 2 * P::DMAS / WAVES;
+  static_assert(PER * WAVES == 2 * P::DMAS, "DMA split");
+  const int lane = threadIdx.x & 63, wave = wave_id();
+#pragma unroll
+  for (int i = 0; i < PER; ++i) {
+    const int grp = wave * PER + i;
+    const bool second = grp >= P::DMAS;
+    const int part = grp % P::DMAS;
+    const int trow = part * P::DMA_ROWS + lane / P::GR;
+    const int row = min(r0 + trow, n_rows - 1);
+    const int c = (lane % P::GR) ^ P::key(trow);
+    const T* src = (second ? y + (int64_t)row * sy : x + (int64_t)row * sx) + c * 8;
+    dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(dst + (second ? P::BYTES : 0) + part * 1024)));
+  }
+}
+
+// bt_dma2 for the steady state: each lane's byte offsets from a tile's first
+// row are computed once (init), a full tile then costs one scalar base per
+// tensor and no per-lane address arithmetic; a tile that reaches past
+// n_rows falls back to bt_dma2's clamped rows.
+template <typename T, int D, int WAVES>
+struct BtDma {
+  typedef BTile<D> P;
+  static constexpr int PER = 2 * P::DMAS / WAVES;
+  uint32_t off[PER];
+  bool fast;
+  __device__ __forceinline__ void init(int64_t sx, int64_t sy) {
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    fast = (int64_t)64 * (sx > sy ? sx : sy) * (int64_t)sizeof(T) < ((int64_t)1 << 31);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int grp = wave * PER + i;
+      const int trow = (grp % P::DMAS) * P::DMA_ROWS + lane / P::GR;
+      const int c = (lane % P::GR) ^ P::key(trow);
+      off[i] = fast ? (uint32_t)((trow * (grp >= P::DMAS ? sy : sx) + c * 8) * (int64_t)sizeof(T)) : 0u;
+    }
+  }
+  __device__ __forceinline__ void issue(char* dst, const T* x, int64_t sx, const T* y, int64_t sy,
+                                        int r0, int n_rows) const {
+    if (fast && r0 + 64 <= n_rows) {
+      const int wave = wave_id();
+      const T* bx = x + (int64_t)r0 * sx;
+      const T* by = y + (int64_t)r0 * sy;
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int grp = wave * PER + i;
+        const bool second = grp >= P::DMAS;
+        dma16s(second ? by : bx, off[i],
+               __builtin_amdgcn_readfirstlane(
+                   lds_addr(dst + (second ? P::BYTES : 0) + (grp % P::DMAS) * 1024)));
+      }
+    } else {
+      bt_dma2<T, D, WAVES>(dst, x, sx, y, sy, r0, n_rows);
+    }
+  }
+};
+
+// A operand from rows rb + (lane & 31), columns 16 st + 8 (lane >> 5) .. +7.
+template <typename T, int D>
+__device__ __forceinline__ typename Mfma<T>::V bt_row(const char* tile, int rb, int st) {
+  const int lane = threadIdx.x & 63;
+  return *reinterpret_cast<const typename Mfma<T>::V*>(
+      tile + BTile<D>::off(rb + (lane & 31), 2 * st + (lane >> 5)));
+}
+
+// A operand of X^T: m = column 32 mt + (lane & 31) of X, k = rows
+// rb + 4g + {0..3} then rb + 8 + 4g + {0..3} (g = lane >> 5), rb a multiple
+// of 16.  In each 16-lane group, source lane s addresses row (s >> 2) at
+// column 4 (s & 3) of the group's 16 columns; the transposing read hands
+// destination lane j the four rows of column j.
+template <typename T, int D>
+__device__ __forceinline__ typename Mfma<T>::V bt_tr(const char* tile, int rb, int mt) {
+  typedef BTile<D> P;
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63;
+  const int ts = lane & 15, th = (lane >> 4) & 1, g = lane >> 5;
+  const int r1 = rb + 4 * g + (ts >> 2), r2 = r1 + 8;
+  const int c = 4 * mt + 2 * th + ((ts & 3) >> 1);
+  const int sub = (ts & 1) * 8;
+  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(lds_addr(tile + P::off(r1, c) + sub)));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(lds_addr(tile + P::off(r2, c) + sub)));
+  // one whole-vector cast: assembling the operand element by element from
+  // the two results was miscompiled into broadcasts of their first element
+  return __builtin_bit_cast(typename Mfma<T>::V,
+                            __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
+
+
 // ------------------------------------------------- MFMA forward, v2 (DMA) --
 // One workgroup = 8 wavefronts = 256 query rows of one (batch, head); each
 // wavefront owns 32 query rows (Q in registers) and computes, per 64-row K/V
@@ -383,58 +508,16 @@ constexpr int kRing = TRI_ATTN_RING;  // MFMA operands in flight ahead of use
 #endif
 constexpr int kF2Stages = TRI_ATTN_FWD_STAGES;  // K/V tiles in the LDS ring
 
-template <int D>
-struct F2 {
-  static constexpr int RB = D * 2;        // bytes per K/V row (16-bit)
-  static constexpr int GR = RB / 16;      // 16-byte granules per row
-  static constexpr int TILE = kF2BN * RB;  // bytes per K or V tile
-  static constexpr int STAGE = 2 * TILE;  // K + V
-  static constexpr int DMA_ROWS = 1024 / RB;
-  static constexpr int DMA_PER_WAVE = 2 * kF2BN / DMA_ROWS / kF2Waves;
-  static_assert(D == 64 || D == 128, "head_dim");
-  // K tile: a 16-byte read of one granule of 16 consecutive rows (one
-  // 256-byte LDS cycle) touches 16 distinct bank groups.
-  static __device__ __forceinline__ int key_k(int r) {
-    if constexpr (GR == 16) return r & 15;
-    else return (r >> 1) & 7;
-  }
-  // V tile: a transposing read covers 4 consecutive rows x 4 granules per
-  // 32-lane cycle; the key puts each row in its own block of 4 slots.
-  static __device__ __forceinline__ int key_v(int r) {
-    if constexpr (GR == 16) return 4 * (r & 3);
-    else return 4 * ((r >> 1) & 1);
-  }
-};
-
-template <typename T, int D>
-__device__ __forceinline__ void f2_dma(char* stage, const T* kp, const T* vp, int64_t sk,
-                                       int64_t sv, int kv0, int Tkv) {
-  typedef F2<D> P;
-  const int lane = threadIdx.x & 63, wave = wave_id();
-  const int rr = lane / P::GR;
-  const int slot = lane % P::GR;
-#pragma unroll
-  for (int q = 0; q < P::DMA_PER_WAVE; ++q) {
-    const int grp = wave * P::DMA_PER_WAVE + q;  // wave-uniform run of DMA_ROWS rows
-    const int trow = (grp * P::DMA_ROWS) % kF2BN + rr;
-    const bool is_v = grp * P::DMA_ROWS >= kF2BN;
-    const int row = min(kv0 + trow, Tkv - 1);
-    const int c = slot ^ (is_v ? P::key_v(trow) : P::key_k(trow));
-    const T* src = (is_v ? vp + (int64_t)row * sv : kp + (int64_t)row * sk) + c * 8;
-    char* dst = stage + (is_v ? P::TILE : 0) + (grp * P::DMA_ROWS % kF2BN) * P::RB;
-    dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(dst)));
-  }
-}
-
 template <typename T, int D>
 __global__ void __launch_bounds__(64 * kF2Waves, 8 / kF2Waves)  // 2 wavefronts per SIMD
 attn_fwd_v2(FwdArgs a) {
   typedef Mfma<T> M;
   typedef typename M::V V;
-  typedef F2<D> P;
+  typedef BTile<D> P;
   constexpr int KS = D / 16;
   constexpr int MT = D / 32;
-  __shared__ __attribute__((aligned(1024))) char smem[kF2Stages * P::STAGE];
+  constexpr int STAGE = 2 * P::BYTES;  // K, V
+  __shared__ __attribute__((aligned(1024))) char smem[kF2Stages * STAGE];
 
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int l32 = lane & 31, g = lane >> 5;
@@ -463,39 +546,33 @@ attn_fwd_v2(FwdArgs a) {
   for (int mt = 0; mt < MT; ++mt) o[mt] = zero16();
   float m = -INFINITY, l = 0.f;
 
-  // transposing-read lane roles: 16-lane group G = lane/16 covers 16 head
-  // dims (half = G & 1) of 4 K/V rows (row block g = G >> 1)
-  const int ts = lane & 15, thalf = (lane >> 4) & 1;
-
   const int kv_end = a.causal ? min(a.Tkv, q0 + kF2BM) : a.Tkv;
   const int n_kv = (int)cdiv(kv_end, kF2BN);
   // kF2Stages-deep ring: tile it + kF2Stages - 1 streams in while tile it
   // is multiplied, so a tile has kF2Stages - 1 tiles of compute to land
+  BtDma<T, D, kF2Waves> dma;
+  dma.init(a.sk_s, a.sv_s);
 #pragma unroll
   for (int j = 0; j < kF2Stages - 1; ++j)
-    if (j < n_kv) f2_dma<T, D>(smem + j * P::STAGE, kp, vp, a.sk_s, a.sv_s, j * kF2BN, a.Tkv);
+    if (j < n_kv) dma.issue(smem + j * STAGE, kp, a.sk_s, vp, a.sv_s, j * kF2BN, a.Tkv);
   for (int it = 0; it < n_kv; ++it) {
     const int kv0 = it * kF2BN;
     // tile it has landed once at most the DMAs of the kF2Stages - 2 younger
     // tiles (issued in order, counted in order) are outstanding
-    if (it + kF2Stages - 2 < n_kv) wait_vmcnt<(kF2Stages - 2) * P::DMA_PER_WAVE>();
+    if (it + kF2Stages - 2 < n_kv) wait_vmcnt<(kF2Stages - 2) * BtDma<T, D, kF2Waves>::PER>();
     else wait_vmcnt<0>();
     __syncthreads();
     if (it + kF2Stages - 1 < n_kv)
-      f2_dma<T, D>(smem + ((it + kF2Stages - 1) % kF2Stages) * P::STAGE, kp, vp, a.sk_s, a.sv_s,
-                   kv0 + (kF2Stages - 1) * kF2BN, a.Tkv);
-    const char* Ks = smem + (it % kF2Stages) * P::STAGE;
-    const char* Vs = Ks + P::TILE;
+      dma.issue(smem + ((it + kF2Stages - 1) % kF2Stages) * STAGE, kp, a.sk_s, vp, a.sv_s,
+                kv0 + (kF2Stages - 1) * kF2BN, a.Tkv);
+    const char* Ks = smem + (it % kF2Stages) * STAGE;
+    const char* Vs = Ks + P::BYTES;
     if (a.causal && kv0 > qw0 + 31) continue;  // this wavefront's rows see none of the tile
 
     // S^T = K Q^T: MFMA i = 2 st + u (the two 32-row halves interleaved);
     // each K fragment is read kRing MFMAs before its use, and the fences
     // keep the compiler from pulling reads back next to their MFMAs
-    auto kread = [&](int i) {
-      const int row = 32 * (i & 1) + l32;
-      return *reinterpret_cast<const V*>(Ks + row * P::RB +
-                                         (((2 * (i >> 1) + g) ^ P::key_k(row)) << 4));
-    };
+    auto kread = [&](int i) { return bt_row<T, D>(Ks, 32 * (i & 1), i >> 1); };
     f32x16 s[2] = {zero16(), zero16()};
     V kb[kRing];
 #pragma unroll
@@ -508,22 +585,7 @@ attn_fwd_v2(FwdArgs a) {
     }
     sched_fence();
     // V^T fragments for the first O^T MFMAs, in flight during the softmax
-    auto vread = [&](int i) {  // MFMA i = MT t + mt
-      const int t = i / MT, mt = i % MT;
-      const int r1 = 16 * t + 4 * g + (ts >> 2), r2 = r1 + 8;
-      const int c = 4 * mt + 2 * thalf + ((ts & 3) >> 1);
-      const int sub = (ts & 1) * 8;
-      typedef short v4s __attribute__((ext_vector_type(4)));
-      const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) v4s*)(lds_addr(
-              Vs + r1 * P::RB + ((c ^ P::key_v(r1)) << 4) + sub)));
-      const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-          (__attribute__((address_space(3))) v4s*)(lds_addr(
-              Vs + r2 * P::RB + ((c ^ P::key_v(r2)) << 4) + sub)));
-      // whole-vector bit cast (per-element assembly of 16-bit lanes from the
-      // transposing-read results was miscompiled into lane broadcasts)
-      return __builtin_bit_cast(V, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-    };
+    auto vread = [&](int i) { return bt_tr<T, D>(Vs, 16 * (i / MT), i % MT); };  // MFMA i = MT t + mt
     V vb[kRing];
 #pragma unroll
     for (int i = 0; i < kRing; ++i) vb[i] = vread(i);
@@ -905,129 +967,6 @@ attn_bwd_dq_mfma(BwdArgs a) {
     }
   }
 }
-
-// ------------------------------------ MFMA backward, head_dim 64 and 128 --
-// Both kernels stage 64-row tiles of Q/dO (dK/dV kernel) or K/V (dQ kernel)
-// in LDS by direct global->LDS DMA, row-major, double-buffered, and read
-// them two ways: as MFMA A operands along rows (16-byte reads of 32 rows)
-// and transposed (ds_read_b64_tr_b16: the A operand of X^T, m = column of
-// X, k = 16 rows of X).  The 16-byte granule c of row r sits at slot
-// c ^ key(r); key makes both reads bank-conflict free:
-//   * 16 consecutive rows at one granule hit 16 distinct 16-byte bank groups
-//     (256-byte rows: key is a bijection of r & 15; 128-byte rows: of
-//     (r >> 1) & 7, rows of opposite parity already use opposite halves);
-//   * 4 consecutive rows x 4 consecutive granules (one 32-lane cycle of a
-//     transposing read) land in 16 distinct groups (bits 3:2 of the key,
-//     bit 2 for 128-byte rows, differ between rows of one parity).
-template <int D>
-struct BTile {
-  static_assert(D == 64 || D == 128, "head_dim");
-  static constexpr int RB = 2 * D;              // bytes per row
-  static constexpr int GR = RB / 16;            // granules per row
-  static constexpr int BYTES = 64 * RB;         // one 64-row tile
-  static constexpr int DMA_ROWS = 1024 / RB;    // rows per wave-wide DMA
-  static constexpr int DMAS = BYTES / 1024;     // wave-wide DMAs per tile
-  static __device__ __forceinline__ int key(int r) {
-    if constexpr (GR == 16) return ((r & 3) << 2) | ((r >> 2) & 3);
-    else return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
-  }
-  static __device__ __forceinline__ int off(int r, int c) { return r * RB + ((c ^ key(r)) << 4); }
-};
-
-// DMA two 64-row tiles (x rows r0.. of x and y, rows clamped to n_rows - 1)
-// into dst and dst + BYTES, spread over the WAVES wavefronts.
-template <typename T, int D, int WAVES>
-__device__ __forceinline__ void bt_dma2(char* dst, const T* x, int64_t sx, const T* y, int64_t sy,
-                                        int r0, int n_rows) {
-  typedef BTile<D> P;
-  constexpr int PER = 2 * P::DMAS / WAVES;
-  static_assert(PER * WAVES == 2 * P::DMAS, "DMA split");
-  const int lane = threadIdx.x & 63, wave = wave_id();
-#pragma unroll
-  for (int i = 0; i < PER; ++i) {
-    const int grp = wave * PER + i;
-    const bool second = grp >= P::DMAS;
-    const int part = grp % P::DMAS;
-    const int trow = part * P::DMA_ROWS + lane / P::GR;
-    const int row = min(r0 + trow, n_rows - 1);
-    const int c = (lane % P::GR) ^ P::key(trow);
-    const T* src = (second ? y + (int64_t)row * sy : x + (int64_t)row * sx) + c * 8;
-    dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(dst + (second ? P::BYTES : 0) + part * 1024)));
-  }
-}
-
-// bt_dma2 for the steady state: each lane's byte offsets from a tile's first
-// row are computed once (init), a full tile then costs one scalar base per
-// tensor and no per-lane address arithmetic; a tile that reaches past
-// n_rows falls back to bt_dma2's clamped rows.
-template <typename T, int D, int WAVES>
-struct BtDma {
-  typedef BTile<D> P;
-  static constexpr int PER = 2 * P::DMAS / WAVES;
-  uint32_t off[PER];
-  bool fast;
-  __device__ __forceinline__ void init(int64_t sx, int64_t sy) {
-    const int lane = threadIdx.x & 63, wave = wave_id();
-    fast = (int64_t)64 * (sx > sy ? sx : sy) * (int64_t)sizeof(T) < ((int64_t)1 << 31);
-#pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int grp = wave * PER + i;
-      const int trow = (grp % P::DMAS) * P::DMA_ROWS + lane / P::GR;
-      const int c = (lane % P::GR) ^ P::key(trow);
-      off[i] = fast ? (uint32_t)((trow * (grp >= P::DMAS ? sy : sx) + c * 8) * (int64_t)sizeof(T)) : 0u;
-    }
-  }
-  __device__ __forceinline__ void issue(char* dst, const T* x, int64_t sx, const T* y, int64_t sy,
-                                        int r0, int n_rows) const {
-    if (fast && r0 + 64 <= n_rows) {
-      const int wave = wave_id();
-      const T* bx = x + (int64_t)r0 * sx;
-      const T* by = y + (int64_t)r0 * sy;
-#pragma unroll
-      for (int i = 0; i < PER; ++i) {
-        const int grp = wave * PER + i;
-        const bool second = grp >= P::DMAS;
-        dma16s(second ? by : bx, off[i],
-               __builtin_amdgcn_readfirstlane(
-                   lds_addr(dst + (second ? P::BYTES : 0) + (grp % P::DMAS) * 1024)));
-      }
-    } else {
-      bt_dma2<T, D, WAVES>(dst, x, sx, y, sy, r0, n_rows);
-    }
-  }
-};
-
-// A operand from rows rb + (lane & 31), columns 16 st + 8 (lane >> 5) .. +7.
-template <typename T, int D>
-__device__ __forceinline__ typename Mfma<T>::V bt_row(const char* tile, int rb, int st) {
-  const int lane = threadIdx.x & 63;
-  return *reinterpret_cast<const typename Mfma<T>::V*>(
-      tile + BTile<D>::off(rb + (lane & 31), 2 * st + (lane >> 5)));
-}
-
-// A operand of X^T: m = column 32 mt + (lane & 31) of X, k = rows
-// rb + 4g + {0..3} then rb + 8 + 4g + {0..3} (g = lane >> 5), rb a multiple
-// of 16.  In each 16-lane group, source lane s addresses row (s >> 2) at
-// column 4 (s & 3) of the group's 16 columns; the transposing read hands
-// destination lane j the four rows of column j.
-template <typename T, int D>
-__device__ __forceinline__ typename Mfma<T>::V bt_tr(const char* tile, int rb, int mt) {
-  typedef BTile<D> P;
-  typedef short v4s __attribute__((ext_vector_type(4)));
-  const int lane = threadIdx.x & 63;
-  const int ts = lane & 15, th = (lane >> 4) & 1, g = lane >> 5;
-  const int r1 = rb + 4 * g + (ts >> 2), r2 = r1 + 8;
-  const int c = 4 * mt + 2 * th + ((ts & 3) >> 1);
-  const int sub = (ts & 1) * 8;
-  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) v4s*)(lds_addr(tile + P::off(r1, c) + sub)));
-  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-      (__attribute__((address_space(3))) v4s*)(lds_addr(tile + P::off(r2, c) + sub)));
-  return __builtin_bit_cast(typename Mfma<T>::V,
-                            __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
-}
-
-
 
 #ifndef TRI_DKDV_FENCES
 #define TRI_DKDV_FENCES 0
