@@ -450,6 +450,49 @@ struct BtDma {
   }
 };
 
+// One 64-row tile (rows r0.. of x, clamped to n_rows - 1) by DMA, spread
+// over WAVES wavefronts (wavefront index taken relative to wave0); the
+// per-lane offsets are computed once (init), and a tile that reaches past
+// n_rows takes the clamped per-lane path.
+template <typename T, int D, int WAVES>
+struct BtDma1 {
+  typedef BTile<D> P;
+  static constexpr int PER = P::DMAS / WAVES;
+  static_assert(PER * WAVES == P::DMAS, "DMA split");
+  uint32_t off[PER];
+  int wv;
+  bool fast;
+  __device__ __forceinline__ void init(int64_t sx, int wave0) {
+    const int lane = threadIdx.x & 63;
+    wv = wave_id() - wave0;
+    fast = (int64_t)64 * sx * (int64_t)sizeof(T) < ((int64_t)1 << 31);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int trow = (wv * PER + i) * P::DMA_ROWS + lane / P::GR;
+      const int c = (lane % P::GR) ^ P::key(trow);
+      off[i] = fast ? (uint32_t)((trow * sx + c * 8) * (int64_t)sizeof(T)) : 0u;
+    }
+  }
+  __device__ __forceinline__ void issue(char* dst, const T* x, int64_t sx, int r0, int n_rows) const {
+    const int lane = threadIdx.x & 63;
+    if (fast && r0 + 64 <= n_rows) {
+      const T* bx = x + (int64_t)r0 * sx;
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        dma16s(bx, off[i], __builtin_amdgcn_readfirstlane(lds_addr(dst + (wv * PER + i) * 1024)));
+    } else {
+#pragma unroll
+      for (int i = 0; i < PER; ++i) {
+        const int trow = (wv * PER + i) * P::DMA_ROWS + lane / P::GR;
+        const int row = min(r0 + trow, n_rows - 1);
+        const int c = (lane % P::GR) ^ P::key(trow);
+        dma16(x + (int64_t)row * sx + c * 8,
+              __builtin_amdgcn_readfirstlane(lds_addr(dst + (wv * PER + i) * 1024)));
+      }
+    }
+  }
+};
+
 // A operand from rows rb + (lane & 31), columns 16 st + 8 (lane >> 5) .. +7.
 template <typename T, int D>
 __device__ __forceinline__ typename Mfma<T>::V bt_row(const char* tile, int rb, int st) {
@@ -481,6 +524,44 @@ __device__ __forceinline__ typename Mfma<T>::V bt_tr(const char* tile, int rb, i
   return __builtin_bit_cast(typename Mfma<T>::V,
                             __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
 }
+
+// bt_row / bt_tr with the per-lane byte offsets computed once: the swizzle
+// key of row r depends on r mod 16 only, so a row block rb (a multiple of
+// 16) adds rb * RB, which the reads take as an immediate offset.  Without
+// this the compiler keeps one address per distinct read (about 50 registers
+// for D = 128) and spills them.
+template <typename T, int D>
+struct BtOffs {
+  typedef BTile<D> P;
+  typedef typename Mfma<T>::V V;
+  static constexpr int KS = D / 16, MT = D / 32;
+  uint32_t row[KS];    // bt_row(tile, 0, st)
+  uint32_t tr[MT][2];  // bt_tr(tile, 0, mt): rows 4g + {0..3} and 8 + 4g + {0..3}
+  __device__ __forceinline__ void init() {
+    const int lane = threadIdx.x & 63;
+    const int ts = lane & 15, th = (lane >> 4) & 1, g = lane >> 5;
+#pragma unroll
+    for (int st = 0; st < KS; ++st) row[st] = (uint32_t)P::off(lane & 31, 2 * st + g);
+    const int r1 = 4 * g + (ts >> 2);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int c = 4 * mt + 2 * th + ((ts & 3) >> 1);
+      tr[mt][0] = (uint32_t)(P::off(r1, c) + (ts & 1) * 8);
+      tr[mt][1] = (uint32_t)(P::off(r1 + 8, c) + (ts & 1) * 8);
+    }
+  }
+  __device__ __forceinline__ V rd_row(const char* tile, int rb, int st) const {
+    return *reinterpret_cast<const V*>(tile + row[st] + rb * P::RB);
+  }
+  __device__ __forceinline__ V rd_tr(const char* tile, int rb, int mt) const {
+    typedef short v4s __attribute__((ext_vector_type(4)));
+    const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4s*)(lds_addr(tile + tr[mt][0] + rb * P::RB)));
+    const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) v4s*)(lds_addr(tile + tr[mt][1] + rb * P::RB)));
+    return __builtin_bit_cast(V, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+};
 
 
 
@@ -663,6 +744,246 @@ attn_fwd_v2(FwdArgs a) {
       }
     }
     if (g == 0) a.lse[(int64_t)bh * a.Tq + qrow] = (m + log2f(lt)) * kLn2;
+  }
+}
+
+// ------------------------------------------ MFMA forward, ping-pong (8 waves) --
+// attn_fwd_v2's tile step is an MFMA stretch (S^T, then O^T) and a VALU
+// stretch (mask, max, exp2, row sums, bf16 packing) of about the same length,
+// and every wavefront of a workgroup runs the same stretch at the same time,
+// so the MFMA pipe idles through the softmax.  Here one workgroup = 8
+// wavefronts in two groups of 4; SIMD s hosts wavefront s of group 0 and
+// wavefront s + 4 of group 1, and a half-step barrier keeps the groups in
+// opposite phases: while one group multiplies (O^T += V_{j-1}^T P_{j-1}^T,
+// then S_j^T = K_j Q^T), the other runs the softmax of its S_j^T.  P_j waits
+// in registers (bf16 operands) for the group's next MFMA phase.  The
+// multiplying group raises its wave priority so its MFMAs issue as soon as
+// the pipe frees and the softmax fills the gaps.
+//
+// K/V tiles stream through a 4-stage LDS ring with two iterations of lead,
+// issued from the softmax phases (group 0 the K tiles, group 1 the V tiles);
+// the half-step barriers wait for LDS operations only, so the DMAs stay in
+// flight across them.  Each wavefront owns 32 query rows; the two groups
+// take alternate 32-row blocks so that near the causal diagonal both stop
+// within a tile of each other.
+#ifndef TRI_ATTN_FWD_PP
+#define TRI_ATTN_FWD_PP 1
+#endif
+constexpr int kPPWaves = 8;
+constexpr int kPPBM = 32 * kPPWaves;  // query rows per workgroup
+constexpr int kPPStages = 4;          // tile j + 2 streams in during iteration j
+#ifndef TRI_ATTN_PP_PRIO
+#define TRI_ATTN_PP_PRIO 1
+#endif
+
+// MFMA phase of the ping-pong forward: O^T += V^T P^T over the previous
+// tile (DPV; MFMA i = MT t + mt, t the 16-row slice of the tile), then
+// S^T = K Q^T over the current one (DS; MFMA i = 2 st + u, u the 32-row
+// half of the tile).  Operands stream through one kRing-deep ring that runs
+// on from the first chain into the second; with DPV the caller has already
+// read the first kRing V^T operands into it (before the phase barrier).
+template <typename T, int D>
+__device__ __forceinline__ void pp_mfma(bool dpv, bool ds, const char* Vs, const char* Ks,
+                                        const BtOffs<T, D>& fo,
+                                        const typename Mfma<T>::V (&qf)[D / 16],
+                                        const typename Mfma<T>::V (&pb)[4],
+                                        typename Mfma<T>::V (&rb)[kRing], f32x16 (&s)[2],
+                                        f32x16 (&o)[D / 32]) {
+  typedef Mfma<T> M;
+  constexpr int MT = D / 32, NP = 4 * MT, NS = 2 * (D / 16);
+  static_assert(NP % kRing == 0 && NS >= kRing, "ring");
+  auto kread = [&](int i) { return fo.rd_row(Ks, 32 * (i & 1), i >> 1); };
+  auto vread = [&](int i) { return fo.rd_tr(Vs, 16 * (i / MT), i % MT); };
+  if (dpv) {
+#pragma unroll
+    for (int i = 0; i < NP; ++i) {
+      sched_fence();
+      o[i % MT] = M::mma(rb[i % kRing], pb[i / MT], o[i % MT]);
+      if (i + kRing < NP) rb[i % kRing] = vread(i + kRing);
+      else if (ds) rb[i % kRing] = kread(i + kRing - NP);
+    }
+  } else if (ds) {
+#pragma unroll
+    for (int i = 0; i < kRing; ++i) rb[i] = kread(i);
+  }
+  if (ds) {
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+      sched_fence();
+      s[i & 1] = M::mma(rb[i % kRing], qf[i >> 1], i < 2 ? zero16() : s[i & 1]);
+      if (i + kRing < NS) rb[i % kRing] = kread(i + kRing);
+    }
+  }
+  sched_fence();
+}
+
+template <typename T, int D>
+__global__ void __launch_bounds__(64 * kPPWaves, 1)  // 2 wavefronts per SIMD
+attn_fwd_pp(FwdArgs a) {
+  typedef Mfma<T> M;
+  typedef typename M::V V;
+  typedef BTile<D> P;
+  typedef BtDma1<T, D, 4> Dma;  // group 0 streams the K tiles, group 1 the V tiles
+  constexpr int KS = D / 16;
+  constexpr int MT = D / 32;
+  constexpr int STAGE = 2 * P::BYTES;  // K, V
+  __shared__ __attribute__((aligned(1024))) char smem[kPPStages * STAGE];
+
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int l32 = lane & 31, g = lane >> 5;
+  const int grp = wave >> 2;
+  const int rblk = 2 * (wave & 3) + grp;
+  // a workgroup runs the query tiles n - 1 - i and i (n = a.n_tiles): with
+  // the causal mask every workgroup then has the same number of K/V tiles
+  const int n_items = (a.n_tiles + 1) / 2;
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = w / n_items;
+  const int pi = w % n_items;
+  const int b = bh / a.H, h = bh % a.H;
+  const int hk = h / (a.H / a.Hkv);
+  const T* qp = (const T*)a.q + b * a.sq_b + h * a.sq_h;
+  const T* kp = (const T*)a.k + b * a.sk_b + hk * a.sk_h;
+  const T* vp = (const T*)a.v + b * a.sv_b + hk * a.sv_h;
+  T* op = (T*)a.o + b * a.so_b + h * a.so_h;
+  const float sl2 = a.scale * kLog2e;
+  // tile t of this group's tensor -> its slot in stage t % kPPStages
+  const T* xp = grp ? vp : kp;
+  const int64_t sx = grp ? a.sv_s : a.sk_s;
+  char* const slot0 = smem + grp * P::BYTES;
+  Dma dma;
+  dma.init(sx, 4 * grp);
+  BtOffs<T, D> fo;
+  fo.init();
+
+  for (int item = 0; item < 2; ++item) {
+    const int qt = item == 0 ? a.n_tiles - 1 - pi : pi;
+    if (item == 1 && qt == a.n_tiles - 1 - pi) break;  // odd tile count: the middle tile runs alone
+    const int q0 = qt * kPPBM;
+    const int qw0 = q0 + 32 * rblk;
+    const int qrow = qw0 + l32;
+    const bool qvalid = qrow < a.Tq;
+
+    V qf[KS];
+#pragma unroll
+    for (int st = 0; st < KS; ++st)
+      qf[st] = qvalid ? ld8(qp + (int64_t)qrow * a.sq_s + 16 * st + 8 * g) : zero8<T>();
+    f32x16 o[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) o[mt] = zero16();
+    V pb[4], rb[kRing];
+    float m = -INFINITY, l = 0.f;
+
+    // tiles of the workgroup, and of this wavefront (rows past Tq need none)
+    const int kv_end = a.causal ? min(a.Tkv, q0 + kPPBM) : a.Tkv;
+    const int n_kv = (int)cdiv(kv_end, 64);
+    const int kv_end_w = qw0 >= a.Tq ? 0 : (a.causal ? min(a.Tkv, qw0 + 32) : a.Tkv);
+    const int n_w = (int)cdiv(kv_end_w, 64);
+
+    // (the previous item's last LDS reads finished before its final barrier)
+    if (n_kv > 0) dma.issue(slot0, xp, sx, 0, a.Tkv);
+    if (n_kv > 1) dma.issue(slot0 + STAGE, xp, sx, 64, a.Tkv);
+    if (n_kv > 1) wait_vmcnt<Dma::PER>();
+    else wait_vmcnt<0>();
+    lds_barrier();
+
+    // Every wavefront runs MFMA(0), softmax(0), MFMA(1), ... with a barrier
+    // after each phase; group 1 starts one barrier later, so the two groups
+    // are always in opposite phases: global half-step 2j + grp is this
+    // group's MFMA(j) -- O^T += V_{j-1}^T P_{j-1}^T (1 <= j <= n_w), then
+    // S_j^T = K_j Q^T (j < n_w) -- and 2j + 1 + grp its softmax(j).
+    // The DMAs are issued in the softmax phases, whose VALU work hides them:
+    // group 0 loads K_{j+2} in half-step 2j + 1 (K_{j-2}'s slot, last read
+    // in 2j - 3) and has K_{j+1} landed by its end (first read in 2j + 2);
+    // group 1 loads V_{j+2} in 2j + 2 (V_{j-2}'s slot, last read in 2j - 1)
+    // and has V_{j+1} landed by its end (first read in 2j + 4).  V_j, read
+    // ahead at the end of softmax(j), landed by the end of half-step 2j.
+    if (grp == 1) lds_barrier();
+    for (int j = 0; j <= n_kv; ++j) {
+      f32x16 s[2];
+#if TRI_ATTN_PP_PRIO
+      __builtin_amdgcn_s_setprio(1);
+#endif
+      pp_mfma<T, D>(j >= 1 && j <= n_w, j < n_w,
+                    smem + ((j + kPPStages - 1) % kPPStages) * STAGE + P::BYTES,
+                    smem + (j % kPPStages) * STAGE, fo, qf, pb, rb, s, o);
+#if TRI_ATTN_PP_PRIO
+      __builtin_amdgcn_s_setprio(0);
+#endif
+      lds_barrier();
+
+      if (j + 2 < n_kv) dma.issue(slot0 + ((j + 2) % kPPStages) * STAGE, xp, sx, (j + 2) * 64, a.Tkv);
+      if (j < n_w) {
+        const int kv0 = 64 * j;
+        // s[u][r] = S^T[kv0 + 32u + 8(r/4) + 4g + r%4][qrow]
+        if ((kv0 + 64 > a.Tkv) || (a.causal && kv0 + 63 > qw0)) {
+#pragma unroll
+          for (int u = 0; u < 2; ++u) {
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int kv = kv0 + 32 * u + 8 * (r >> 2) + 4 * g + (r & 3);
+              s[u][r] = (kv >= a.Tkv || (a.causal && kv > qrow)) ? -INFINITY : s[u][r];
+            }
+          }
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[u][r]);
+        // the other half of this query row's scores sit in lane ^ 32
+        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
+                                                         false, false);
+        mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * sl2;
+        // lazy rescaling, as in attn_fwd_v2: the reference point m moves
+        // only when a row's max exceeds it by more than 8 (every p <= 2^8)
+        if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
+          const float m_new = fmaxf(m, mx);
+          const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m - m_new);
+          m = m_new;
+          l *= alpha;
+#pragma unroll
+          for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[mt][r] *= alpha;
+        }
+        const float nm = m == -INFINITY ? 0.f : -m;
+        // P^T operands: slice t holds kv rows 16t + 4g + {0..3}, 16t + 8 + 4g + {0..3}
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj) {
+            const float p = fast_exp2(fmaf(s[t >> 1][8 * (t & 1) + jj], sl2, nm));
+            l += p;
+            pb[t][jj] = (T)p;
+          }
+        }
+        // first V^T operands of MFMA(j + 1), read ahead of its barrier
+        const char* Vn = smem + (j % kPPStages) * STAGE + P::BYTES;
+#pragma unroll
+        for (int i = 0; i < kRing; ++i) rb[i] = fo.rd_tr(Vn, 16 * (i / MT), i % MT);
+      }
+      // publish tile j + 1 (tile j + 2's DMAs may stay in flight)
+      if (j + 2 < n_kv) wait_vmcnt<Dma::PER>();
+      else wait_vmcnt<0>();
+      lds_barrier();
+    }
+    if (grp == 0) lds_barrier();
+
+    const float lt = l + __shfl_xor(l, 32, 64);
+    const float inv = lt > 0.f ? 1.0f / lt : 0.f;
+    if (qvalid) {
+      T* orow = op + (int64_t)qrow * a.so_s;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int d0 = 32 * mt + 8 * rr + 4 * g;
+          store4<T>(orow + d0, o[mt][4 * rr] * inv, o[mt][4 * rr + 1] * inv,
+                    o[mt][4 * rr + 2] * inv, o[mt][4 * rr + 3] * inv);
+        }
+      }
+      if (g == 0) a.lse[(int64_t)bh * a.Tq + qrow] = (m + log2f(lt)) * kLn2;
+    }
   }
 }
 
@@ -1266,7 +1587,7 @@ attn_bwd_dkdv_pair(BwdArgs a) {
         }
       }
     }
-    __syncthreads();  // A's P is visible to B
+    lds_barrier();  // A's P is visible to B; the next step's DMA stays in flight
     if (active) {
       if (role_b) {
 #pragma unroll
@@ -1637,6 +1958,22 @@ int simt_per_lane(int64_t d) {
 
 template <typename T>
 int fwd_mfma(const FwdArgs& a, int64_t D, hipStream_t st) {
+#if TRI_ATTN_FWD_PP
+  // The ping-pong kernel (one 8-wavefront workgroup per CU, two 256-row
+  // query tiles each) measured faster than attn_fwd_v2 only for D = 128
+  // with at least 4 workgroups per CU; with fewer the CUs run out of
+  // workgroups, and for D = 64 its MFMA phase is too short to hide the
+  // softmax.
+  if (D == 128) {
+    FwdArgs x = a;
+    x.n_tiles = (int)cdiv(a.Tq, kPPBM);
+    const int64_t blocks = (int64_t)((x.n_tiles + 1) / 2) * a.B * a.H;  // tile pairs
+    if (blocks >= 4 * (int64_t)cu_count()) {
+      attn_fwd_pp<T, 128><<<(unsigned)blocks, 64 * kPPWaves, 0, st>>>(x);
+      return check_launch("attention forward (mfma)");
+    }
+  }
+#endif
   if (D == 64 || D == 128) {
     FwdArgs x = a;
     x.n_tiles = (int)cdiv(a.Tq, kF2BM);

@@ -175,9 +175,36 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
 }
 
+// Workgroup barrier for LDS hand-offs between wavefronts.  __syncthreads
+// compiles to s_waitcnt vmcnt(0) lgkmcnt(0) + s_barrier, which also drains
+// every global load in flight -- a prefetch DMA into another LDS stage
+// included.  This one waits for the wavefront's own LDS operations only
+// (its LDS writes are then visible, its LDS reads done), so prefetches stay
+// in flight across it; a DMA'd tile is published as before, by wait_vmcnt
+// ahead of the barrier.  The memory clobber keeps the compiler from moving
+// LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 inline int dtype_size(int dtype) { return dtype == kF32 ? 4 : 2; }
+
+// Compute units of the current device (cached per device; 256 on MI355X),
+// for launch-shape decisions.
+inline int cu_count() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+      n = 256;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
 
 // ---- error plumbing (defined in capi.hip) ---------------------------------
 int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));

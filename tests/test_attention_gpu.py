@@ -124,3 +124,42 @@ def test_attention_deterministic():
         grads.append((q.grad.clone(), k.grad.clone(), v.grad.clone()))
     for a, b in zip(*grads):
         assert torch.equal(a, b)
+
+
+def _check_heads(dtype, b, h, hkv, t, d, causal, heads, seed, grads=False):
+    """Run the full (b, h, t, d) problem, check the listed (batch, kv head)
+    slices -- with every query head of each kv head's group -- against the
+    oracle (the problem is independent per (batch, kv head))."""
+    group = h // hkv
+    q, k, v = randn((b, h, t, d), dtype, seed), randn((b, hkv, t, d), dtype, seed + 1), \
+        randn((b, hkv, t, d), dtype, seed + 2)
+    do = randn((b, h, t, d), dtype, seed + 3)
+    qs, ks, vs = (x.detach().requires_grad_(grads) for x in (q, k, v))
+    o = tritium.attention(qs, ks, vs, is_causal=causal)
+    if grads:
+        o.backward(do)
+    tol = ATOL[dtype]
+    for bi, kh in heads:
+        hq = slice(kh * group, (kh + 1) * group)
+        sel = lambda x, hs: np32(x[bi:bi + 1, hs])  # noqa: E731
+        eo, lse = oracle.attention.forward(sel(q, hq), sel(k, slice(kh, kh + 1)),
+                                           sel(v, slice(kh, kh + 1)), causal)
+        assert_close(o[bi:bi + 1, hq], eo, tol, tol, f"o[{bi},{kh}]")
+        if grads:
+            edq, edk, edv = oracle.attention.backward(
+                sel(do, hq), sel(q, hq), sel(k, slice(kh, kh + 1)), sel(v, slice(kh, kh + 1)),
+                lse, causal)
+            assert_close(qs.grad[bi:bi + 1, hq], edq, tol, tol, f"dq[{bi},{kh}]")
+            assert_close(ks.grad[bi:bi + 1, kh:kh + 1], edk, tol, tol, f"dk[{bi},{kh}]")
+            assert_close(vs.grad[bi:bi + 1, kh:kh + 1], edv, tol, tol, f"dv[{bi},{kh}]")
+
+
+# head_dim 128 problems with at least 4 workgroups of (256-row query tile
+# pairs) per CU take the 8-wavefront ping-pong forward; these grids (1024
+# workgroups) reach it on a 256-CU part, with one and with an odd number of
+# query tiles, ragged lengths, GQA and the non-causal mask.
+def test_attention_pingpong_forward_grid():
+    _check_heads(torch.bfloat16, 4, 256, 256, 256, 128, True,
+                 [(0, 0), (1, 77), (3, 255)], seed=21, grads=True)
+    _check_heads(torch.float16, 2, 256, 64, 731, 128, True, [(0, 0), (1, 63)], seed=22)
+    _check_heads(torch.bfloat16, 2, 256, 256, 600, 128, False, [(0, 5), (1, 250)], seed=23)
