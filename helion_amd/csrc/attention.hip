@@ -9,18 +9,21 @@
 // bf16 / fp16 inputs with head_dim in {16, 32, 64, 128} run on the MFMA path
 // (v_mfma_f32_32x32x16_{bf16,f16}, fp32 accumulation):
 //
-//  forward   one workgroup = 4 wavefronts = 128 query rows of one (batch, head);
-//            a wavefront computes S^T = K Q^T for its 32 query rows against a
-//            64-row K/V tile staged in LDS, so each lane owns ONE query column:
-//            the online-softmax max needs a single lane^32 exchange and P^T
-//            feeds the next MFMA (O^T = V^T P^T) straight from registers.  V is
-//            stored transposed in LDS so that operand is two 8-byte LDS reads.
-//  backward  (1) delta = rowsum(dO * O) pre-pass; (2) KV-parallel dK/dV kernel:
-//            a wavefront owns 32 kv rows (K, V fragments in registers) and
-//            sweeps the query tiles that can see them, accumulating dV^T and
-//            dK^T in registers (GQA: all query heads of the group), written
-//            once in the output dtype; (3) Q-parallel dQ kernel.  No atomics,
-//            results are bitwise deterministic.
+//  forward   a wavefront computes S^T = K Q^T for its 32 query rows against a
+//            64-row K/V tile staged in LDS (K and V rows by DMA, XOR-swizzled),
+//            so each lane owns ONE query column: the online-softmax max needs a
+//            single lane^32 exchange and P^T feeds the next MFMA
+//            (O^T = V^T P^T) straight from registers, V^T by transposing LDS
+//            reads.  attn_fwd_v2: 4 wavefronts = 128 query rows per workgroup;
+//            attn_fwd_pp (head_dim 128, large grids): 8 wavefronts in two
+//            groups on opposite MFMA / softmax phases, two 256-row query tiles
+//            per workgroup.
+//  backward  (1) Q-parallel dQ kernel, which also writes delta = rowsum(dO * O);
+//            (2) KV-parallel dK/dV kernel: wavefront pairs own 32 kv rows (K
+//            or V fragments in registers), sweep the query tiles that can see
+//            them in opposite phases, and accumulate dV^T and dK^T in registers
+//            (GQA: all query heads of the group), written once in the output
+//            dtype.  No atomics: results are bitwise deterministic.
 //
 // fp32 inputs (and head_dim outside the MFMA set, up to 1024) run on a SIMT
 // path: one wavefront per row, exact fp32 arithmetic.
@@ -451,9 +454,11 @@ struct BtDma {
 };
 
 // One 64-row tile (rows r0.. of x, clamped to n_rows - 1) by DMA, spread
-// over WAVES wavefronts (wavefront index taken relative to wave0); the
-// per-lane offsets are computed once (init), and a tile that reaches past
-// n_rows takes the clamped per-lane path.
+// over WAVES wavefronts (wavefront index taken relative to wave0).  A full
+// tile uses per-lane byte offsets computed once (init); a tile that reaches
+// past n_rows recomputes them with the rows clamped, from a lane index the
+// compiler cannot hoist out of the caller's loop (hoisted, that path's
+// per-lane addresses would hold registers for the whole loop).
 template <typename T, int D, int WAVES>
 struct BtDma1 {
   typedef BTile<D> P;
@@ -462,24 +467,35 @@ struct BtDma1 {
   uint32_t off[PER];
   int wv;
   bool fast;
+  // byte offset of this lane's 16 bytes of DMA i from row r0, rows past
+  // r0 + lim clamped to r0 + lim
+  static __device__ __forceinline__ uint32_t offset(int lane, int wv, int i, int64_t sx, int lim) {
+    const int trow = (wv * PER + i) * P::DMA_ROWS + lane / P::GR;
+    const int c = (lane % P::GR) ^ P::key(trow);
+    return (uint32_t)((min(trow, lim) * sx + c * 8) * (int64_t)sizeof(T));
+  }
   __device__ __forceinline__ void init(int64_t sx, int wave0) {
     const int lane = threadIdx.x & 63;
     wv = wave_id() - wave0;
     fast = (int64_t)64 * sx * (int64_t)sizeof(T) < ((int64_t)1 << 31);
 #pragma unroll
-    for (int i = 0; i < PER; ++i) {
-      const int trow = (wv * PER + i) * P::DMA_ROWS + lane / P::GR;
-      const int c = (lane % P::GR) ^ P::key(trow);
-      off[i] = fast ? (uint32_t)((trow * sx + c * 8) * (int64_t)sizeof(T)) : 0u;
-    }
+    for (int i = 0; i < PER; ++i) off[i] = fast ? offset(lane, wv, i, sx, 63) : 0u;
   }
   __device__ __forceinline__ void issue(char* dst, const T* x, int64_t sx, int r0, int n_rows) const {
-    const int lane = threadIdx.x & 63;
+    const T* bx = x + (int64_t)r0 * sx;
     if (fast && r0 + 64 <= n_rows) {
-      const T* bx = x + (int64_t)r0 * sx;
 #pragma unroll
       for (int i = 0; i < PER; ++i)
         dma16s(bx, off[i], __builtin_amdgcn_readfirstlane(lds_addr(dst + (wv * PER + i) * 1024)));
+      return;
+    }
+    int lane;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane));
+    if (fast) {
+#pragma unroll
+      for (int i = 0; i < PER; ++i)
+        dma16s(bx, offset(lane, wv, i, sx, n_rows - 1 - r0),
+               __builtin_amdgcn_readfirstlane(lds_addr(dst + (wv * PER + i) * 1024)));
     } else {
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
@@ -925,11 +941,16 @@ attn_fwd_pp(FwdArgs a) {
             }
           }
         }
-        float mx = -INFINITY;
+        // row max and (below) row sum as 4 independent chains: a lone
+        // wavefront's VALU stream would otherwise wait out each dependent step
+        float mq[4];
 #pragma unroll
-        for (int u = 0; u < 2; ++u)
+        for (int c = 0; c < 4; ++c) {
+          mq[c] = fmaxf(s[c >> 1][8 * (c & 1)], s[c >> 1][8 * (c & 1) + 1]);
 #pragma unroll
-          for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[u][r]);
+          for (int r = 2; r < 8; ++r) mq[c] = fmaxf(mq[c], s[c >> 1][8 * (c & 1) + r]);
+        }
+        float mx = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
         // the other half of this query row's scores sit in lane ^ 32
         const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
                                                          false, false);
@@ -948,15 +969,17 @@ attn_fwd_pp(FwdArgs a) {
         }
         const float nm = m == -INFINITY ? 0.f : -m;
         // P^T operands: slice t holds kv rows 16t + 4g + {0..3}, 16t + 8 + 4g + {0..3}
+        float ls[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
 #pragma unroll
           for (int jj = 0; jj < 8; ++jj) {
             const float p = fast_exp2(fmaf(s[t >> 1][8 * (t & 1) + jj], sl2, nm));
-            l += p;
+            ls[jj & 3] += p;
             pb[t][jj] = (T)p;
           }
         }
+        l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
         // first V^T operands of MFMA(j + 1), read ahead of its barrier
         const char* Vn = smem + (j % kPPStages) * STAGE + P::BYTES;
 #pragma unroll
@@ -1452,21 +1475,26 @@ attn_bwd_dkdv_v2(BwdArgs a) {
 
 // dK, dV with wavefront pairs: a workgroup owns 128 kv rows of one
 // (batch, kv head); wavefronts p and p + 4 (same SIMD) share kv rows
-// 32p .. 32p + 31.  Per 64-row query tile, in two phases split by barriers:
-//   phase 1  A (p):     S = Q K^T -> P = exp(S*scale - lse), masked; P goes
-//                       to LDS (fp32) and stays in registers as bf16;
-//            B (p + 4): dP = dO V^T (kept in registers);
-//   phase 2  A:         dV^T += dO^T P;
-//            B:         dS = P (dP - D_i) from A's P, dK^T += Q^T dS.
-// Each role keeps one set of fragments (K for A, V for B) and one set of
-// accumulators (dV / dK), half of what one wavefront doing both needs, so
-// two wavefronts fit per SIMD, and the roles' VALU work (A's exponentials in
-// phase 1, B's dS in phase 2) runs while the other role's MFMAs execute.
+// 32p .. 32p + 31, role A (p: K fragments, dV accumulators) and role B
+// (p + 4: V fragments, dK accumulators) -- one set of fragments and
+// accumulators each, so two wavefronts fit per SIMD -- in opposite phases,
+// so that one's VALU work runs under the other's MFMAs.  With tile s the
+// s-th (query head, 64-row query tile) step, half-step 2s and 2s + 1 are
+//   2s      A: dV^T += dO_{s-1}^T P_{s-1};  S_s = Q_s K^T          (MFMA)
+//           B: dS_{s-1} = P_{s-1} (dP_{s-1} - D), P from A via LDS  (VALU)
+//   2s + 1  A: P_s = exp(S_s * scale - lse), to LDS and registers  (VALU)
+//           B: dK^T += Q_{s-1}^T dS_{s-1};  dP_s = dO_s V^T        (MFMA)
+// Tiles stream through a 3-stage LDS ring, each role loading from its VALU
+// phases: B loads Q, lse and D of tile s + 1 in half-step 2s (the stage of
+// tile s - 2, last read in 2s - 1) and has them landed by the end of 2s + 1
+// (Q first read in 2s + 2); A loads dO of tile s + 1 in 2s + 1 and has it
+// landed by the end of 2s + 2 (first read in 2s + 3).
 constexpr int kPairWaves = 8;
 constexpr int kPairBN = 128;
+constexpr int kDkvPPStages = 3;
 
 template <typename T, int D>
-__global__ void __launch_bounds__(64 * kPairWaves)
+__global__ void __launch_bounds__(64 * kPairWaves, 1)  // 2 wavefronts per SIMD
 attn_bwd_dkdv_pair(BwdArgs a) {
   typedef Mfma<T> M;
   typedef typename M::V V;
@@ -1475,7 +1503,7 @@ attn_bwd_dkdv_pair(BwdArgs a) {
   constexpr int MT = D / 32;
   constexpr int STAGE = 2 * P::BYTES + 512;  // Q, dO, lse[64], delta[64]
   constexpr int XCH = 2 * 4 * 64 * 16;       // per pair: 2 query halves x [4][64 lanes][4 fp32]
-  __shared__ __attribute__((aligned(1024))) char smem[2 * STAGE];
+  __shared__ __attribute__((aligned(1024))) char smem[kDkvPPStages * STAGE];
   __shared__ __attribute__((aligned(16))) char xch_all[4 * XCH];
 
   const int lane = threadIdx.x & 63, wave = wave_id();
@@ -1499,7 +1527,7 @@ attn_bwd_dkdv_pair(BwdArgs a) {
                        : (const T*)a.k + b * a.sk_b + hk * a.sk_h + (int64_t)kvw * a.sk_s;
   V frag[KS];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) frag[s] = kvvalid ? ld8(fp + 16 * s + 8 * g) : zero8<T>();
+  for (int st = 0; st < KS; ++st) frag[st] = kvvalid ? ld8(fp + 16 * st + 8 * g) : zero8<T>();
   f32x16 acc[MT];
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) acc[mt] = zero16();
@@ -1507,55 +1535,83 @@ attn_bwd_dkdv_pair(BwdArgs a) {
   const int q_begin = a.causal ? kv0 : 0;
   const int n_q = a.Tq > q_begin ? (int)cdiv(a.Tq - q_begin, 64) : 0;
   const int n_steps = n_q * group;
-  BtDma<T, D, kPairWaves> dma;
-  dma.init(a.sq_s, a.sdo_s);
-  auto issue = [&](int step, char* stage) {
+  BtOffs<T, D> fo;
+  fo.init();
+  // role A streams the dO tiles, role B the Q tiles with lse and D
+  BtDma1<T, D, 4> dma;
+  dma.init(role_b ? a.sq_s : a.sdo_s, role_b ? 4 : 0);
+  auto q0_of = [&](int step) { return q_begin + (step % n_q) * 64; };
+  auto stage = [&](int step) { return smem + (step % kDkvPPStages) * STAGE; };
+  auto issue = [&](int step) {
     const int hq = hk * group + step / n_q;
-    const int q0 = q_begin + (step % n_q) * 64;
-    const T* qp = (const T*)a.q + b * a.sq_b + hq * a.sq_h;
-    const T* dop = (const T*)a.dout + b * a.sdo_b + hq * a.sdo_h;
-    dma.issue(stage, qp, a.sq_s, dop, a.sdo_s, q0, a.Tq);
-    const int64_t row = ((int64_t)b * a.H + hq) * a.Tq + min(q0 + lane, a.Tq - 1);
-    if (wave == 0) dma4(a.lse + row, __builtin_amdgcn_readfirstlane(lds_addr(stage + 2 * P::BYTES)));
-    if (wave == 1)
-      dma4(a.delta + row, __builtin_amdgcn_readfirstlane(lds_addr(stage + 2 * P::BYTES + 256)));
+    const int q0 = q0_of(step);
+    char* st = stage(step);
+    if (role_b) {
+      dma.issue(st, (const T*)a.q + b * a.sq_b + hq * a.sq_h, a.sq_s, q0, a.Tq);
+      const int64_t row = ((int64_t)b * a.H + hq) * a.Tq + min(q0 + lane, a.Tq - 1);
+      if (wave == 4) dma4(a.lse + row, __builtin_amdgcn_readfirstlane(lds_addr(st + 2 * P::BYTES)));
+      if (wave == 5)
+        dma4(a.delta + row, __builtin_amdgcn_readfirstlane(lds_addr(st + 2 * P::BYTES + 256)));
+    } else {
+      dma.issue(st + P::BYTES, (const T*)a.dout + b * a.sdo_b + hq * a.sdo_h, a.sdo_s, q0, a.Tq);
+    }
   };
-  if (n_steps > 0) issue(0, smem);
-  for (int step = 0; step < n_steps; ++step) {
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) pin_vgpr(acc[mt]);
-    wait_vmcnt<0>();
-    __syncthreads();
-    if (step + 1 < n_steps) issue(step + 1, smem + ((step + 1) & 1) * STAGE);
-    const int q0 = q_begin + (step % n_q) * 64;
-    const bool active = !(a.causal && q0 + 63 < kvb);  // pair-uniform
-    const char* Qs = smem + (step & 1) * STAGE;
-    const char* dOs = Qs + P::BYTES;
-    const float* lse_s = reinterpret_cast<const float*>(Qs + 2 * P::BYTES);
-    const float* del_s = lse_s + 64;
-    const char* T1 = role_b ? dOs : Qs;  // phase-1 row operand
-    const char* T2 = role_b ? Qs : dOs;  // phase-2 transposed operand
-    const bool need_mask = (a.causal && q0 < kvb + 31) || q0 + 64 > a.Tq;
+  // pair-uniform: the query tile of step has rows at or past this pair's kv rows
+  auto active = [&](int step) { return !(a.causal && q0_of(step) + 63 < kvb); };
 
-    // phase 1: x = T1 * frag^T for both 32-row query halves
-    f32x16 x[2];
-    V op[2][2];
-    if (active) {
-      // MFMA i = 2 st + mq (the two query halves interleaved); row fragments
-      // are read kRing MFMAs ahead of use, fenced so the order holds
-      x[0] = zero16();
-      x[1] = zero16();
-      V rb[kRing];
+  // x[mq] = T1 frag^T over a tile's two 32-row query halves (MFMA i = 2 st + mq)
+  auto mma_rows = [&](const char* T1, f32x16 (&x)[2]) {
+    V rb[kRing];
 #pragma unroll
-      for (int i = 0; i < kRing; ++i) rb[i] = bt_row<T, D>(T1, 32 * (i & 1), i >> 1);
+    for (int i = 0; i < kRing; ++i) rb[i] = fo.rd_row(T1, 32 * (i & 1), i >> 1);
 #pragma unroll
-      for (int i = 0; i < 2 * KS; ++i) {
-        sched_fence();
-        x[i & 1] = M::mma(rb[i % kRing], frag[i >> 1], x[i & 1]);
-        if (i + kRing < 2 * KS) rb[i % kRing] = bt_row<T, D>(T1, 32 * ((i + kRing) & 1), (i + kRing) >> 1);
-      }
+    for (int i = 0; i < 2 * KS; ++i) {
       sched_fence();
-      if (!role_b) {
+      x[i & 1] = M::mma(rb[i % kRing], frag[i >> 1], i < 2 ? zero16() : x[i & 1]);
+      if (i + kRing < 2 * KS) rb[i % kRing] = fo.rd_row(T1, 32 * ((i + kRing) & 1), (i + kRing) >> 1);
+    }
+    sched_fence();
+  };
+  // acc^T += T2^T op (MFMA i = MT t + mt, t the 16-row slice of the tile)
+  auto mma_tr = [&](const char* T2, const V (&op)[4]) {
+    constexpr int N2 = 4 * MT;
+    V tb[kRing];
+#pragma unroll
+    for (int i = 0; i < kRing; ++i) tb[i] = fo.rd_tr(T2, 16 * (i / MT), i % MT);
+#pragma unroll
+    for (int i = 0; i < N2; ++i) {
+      sched_fence();
+      acc[i % MT] = M::mma(tb[i % kRing], op[i / MT], acc[i % MT]);
+      if (i + kRing < N2) tb[i % kRing] = fo.rd_tr(T2, 16 * ((i + kRing) / MT), (i + kRing) % MT);
+    }
+    sched_fence();
+  };
+
+  if (n_steps > 0) issue(0);
+  wait_vmcnt<0>();
+  lds_barrier();
+  f32x16 x[2];
+  V op[4];  // MFMA operand: slice t = 2 mq + u holds query rows 16t + 4g + {0..3}, 16t + 8 + 4g + {0..3}
+  if (!role_b) {
+    for (int s = 0; s <= n_steps; ++s) {
+      const bool cur = s < n_steps && active(s), prev = s >= 1 && active(s - 1);
+      // half-step 2s: dV^T += dO_{s-1}^T P_{s-1}, S_s = Q_s K^T
+#if TRI_ATTN_PP_PRIO
+      __builtin_amdgcn_s_setprio(1);
+#endif
+      if (prev) mma_tr(stage(s + kDkvPPStages - 1) + P::BYTES, op);
+      if (cur) mma_rows(stage(s), x);
+#if TRI_ATTN_PP_PRIO
+      __builtin_amdgcn_s_setprio(0);
+#endif
+      wait_vmcnt<0>();  // dO_s (issued in half-step 2s - 1)
+      lds_barrier();
+      // half-step 2s + 1: P_s
+      if (s + 1 < n_steps) issue(s + 1);
+      if (cur) {
+        const int q0 = q0_of(s);
+        const float* lse_s = reinterpret_cast<const float*>(stage(s) + 2 * P::BYTES);
+        const bool need_mask = (a.causal && q0 < kvb + 31) || q0 + 64 > a.Tq;
 #pragma unroll
         for (int mq = 0; mq < 2; ++mq) {
           // x[mq][r] = S[q0 + 32mq + 8(r/4) + 4g + r%4][kvw]; masked scores -> -inf (P = 0)
@@ -1575,53 +1631,47 @@ attn_bwd_dkdv_pair(BwdArgs a) {
 #pragma unroll
             for (int j = 0; j < 4; ++j) {
               const float p = fast_exp2(fmaf(x[mq][4 * rr + j], sl2, -lv[j]));
-              x[mq][4 * rr + j] = p;
               pf[j] = p;
+              op[2 * mq + (rr >> 1)][4 * (rr & 1) + j] = (T)p;
             }
             *reinterpret_cast<float4*>(xch + ((mq * 4 + rr) * 64 + lane) * 16) = pv;
           }
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) op[mq][t][j] = (T)x[mq][8 * t + j];
         }
       }
+      lds_barrier();
     }
-    lds_barrier();  // A's P is visible to B; the next step's DMA stays in flight
-    if (active) {
-      if (role_b) {
+  } else {
+    for (int s = 0; s <= n_steps; ++s) {
+      const bool cur = s < n_steps && active(s), prev = s >= 1 && active(s - 1);
+      // half-step 2s: dS_{s-1}
+      if (s + 1 < n_steps) issue(s + 1);
+      if (prev) {
+        const float* del_s = reinterpret_cast<const float*>(stage(s + kDkvPPStages - 1) + 2 * P::BYTES + 256);
 #pragma unroll
         for (int mq = 0; mq < 2; ++mq) {
-          float ds[16];
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) {
             const float4 pv = *reinterpret_cast<const float4*>(xch + ((mq * 4 + rr) * 64 + lane) * 16);
             const float4 Dl = *reinterpret_cast<const float4*>(del_s + 32 * mq + 8 * rr + 4 * g);
-            ds[4 * rr + 0] = pv.x * (x[mq][4 * rr + 0] - Dl.x);
-            ds[4 * rr + 1] = pv.y * (x[mq][4 * rr + 1] - Dl.y);
-            ds[4 * rr + 2] = pv.z * (x[mq][4 * rr + 2] - Dl.z);
-            ds[4 * rr + 3] = pv.w * (x[mq][4 * rr + 3] - Dl.w);
+            const float pp[4] = {pv.x, pv.y, pv.z, pv.w}, dd[4] = {Dl.x, Dl.y, Dl.z, Dl.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              op[2 * mq + (rr >> 1)][4 * (rr & 1) + j] = (T)(pp[j] * (x[mq][4 * rr + j] - dd[j]));
           }
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) op[mq][t][j] = (T)ds[8 * t + j];
         }
       }
-      // phase 2: acc^T += T2^T * op (A: dV^T += dO^T P, B: dK^T += Q^T dS);
-      // MFMA i = MT (2 mq + t) + mt, transposed fragments kRing ahead
-      constexpr int N2 = 4 * MT;
-      auto tread = [&](int i) { return bt_tr<T, D>(T2, 16 * (i / MT), i % MT); };
-      V tb[kRing];
-#pragma unroll
-      for (int i = 0; i < kRing; ++i) tb[i] = tread(i);
-#pragma unroll
-      for (int i = 0; i < N2; ++i) {
-        sched_fence();
-        acc[i % MT] = M::mma(tb[i % kRing], op[(i / MT) >> 1][(i / MT) & 1], acc[i % MT]);
-        if (i + kRing < N2) tb[i % kRing] = tread(i + kRing);
-      }
-      sched_fence();
+      lds_barrier();
+      // half-step 2s + 1: dK^T += Q_{s-1}^T dS_{s-1}, dP_s = dO_s V^T
+#if TRI_ATTN_PP_PRIO
+      __builtin_amdgcn_s_setprio(1);
+#endif
+      if (prev) mma_tr(stage(s + kDkvPPStages - 1), op);
+      if (cur) mma_rows(stage(s) + P::BYTES, x);
+#if TRI_ATTN_PP_PRIO
+      __builtin_amdgcn_s_setprio(0);
+#endif
+      wait_vmcnt<0>();  // Q, lse, D of tile s + 1 (issued in half-step 2s)
+      lds_barrier();
     }
   }
 

@@ -155,11 +155,12 @@ def _check_heads(dtype, b, h, hkv, t, d, causal, heads, seed, grads=False):
 
 
 # head_dim 128 problems with at least 4 workgroups of (256-row query tile
-# pairs) per CU take the 8-wavefront ping-pong forward; these grids (1024
-# workgroups) reach it on a 256-CU part, with one and with an odd number of
-# query tiles, ragged lengths, GQA and the non-causal mask.
-def test_attention_pingpong_forward_grid():
+# pairs) per CU take the 8-wavefront ping-pong forward and dQ kernels; these
+# grids (1024 workgroups) reach them on a 256-CU part, with one and with an
+# odd number of query tiles, ragged lengths, GQA and the non-causal mask.
+def test_attention_pingpong_grid():
     _check_heads(torch.bfloat16, 4, 256, 256, 256, 128, True,
                  [(0, 0), (1, 77), (3, 255)], seed=21, grads=True)
-    _check_heads(torch.float16, 2, 256, 64, 731, 128, True, [(0, 0), (1, 63)], seed=22)
+    _check_heads(torch.float16, 2, 256, 64, 731, 128, True, [(0, 0), (1, 63)], seed=22,
+                 grads=True)
     _check_heads(torch.bfloat16, 2, 256, 256, 600, 128, False, [(0, 5), (1, 250)], seed=23)
