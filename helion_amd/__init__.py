@@ -18,6 +18,7 @@ import torch  # noqa: F401  (must be loaded before libtritium_hip.so)
 from .adamw import adamw_step, adamw_step_multi
 from .attention import attention
 from .linear_ce import linear_cross_entropy, linear_cross_entropy_backward
+from .matmul import matmul, matmul_vec
 from .rmsnorm import residual_rmsnorm, rmsnorm, rmsnorm_backward
 from .rope import rope, rope_
 from .swiglu import swiglu, swiglu_backward
@@ -31,6 +32,8 @@ __all__ = [
     "attention",
     "linear_cross_entropy",
     "linear_cross_entropy_backward",
+    "matmul",
+    "matmul_vec",
     "residual_rmsnorm",
     "rmsnorm",
     "rmsnorm_backward",

@@ -348,7 +348,9 @@ __device__ __forceinline__ void mainloop(const Problem& p, int tm, int tn, char*
         wait_vmcnt<(C::STAGES - 2) * C::DMA_PER_WAVE>();
       else
         wait_vmcnt<0>();
-      __syncthreads();
+      // LDS-only barrier: __syncthreads would also wait for the younger
+      // tiles' DMAs, leaving one tile of lead whatever STAGES is
+      lds_barrier();
       const int64_t next = kt + C::STAGES - 1;
       if (next < nfull)
         dma_tile<C, T>(smem + (int)(next % C::STAGES) * C::STAGE_BYTES, p, m0, n0, next * BK);

@@ -35,7 +35,7 @@ HOT_PATH_NAMES = {
 
 def test_public_names_cover_the_hot_path():
     assert HOT_PATH_NAMES <= set(tritium.__all__)
-    for name in HOT_PATH_NAMES | {"adamw_step_multi"}:
+    for name in HOT_PATH_NAMES | {"adamw_step_multi", "matmul", "matmul_vec"}:
         assert callable(getattr(tritium, name))
 
 
@@ -51,6 +51,8 @@ def test_public_names_cover_the_hot_path():
         lambda: tritium.adamw_step(torch.randn(8), torch.randn(8), torch.zeros(8), torch.zeros(8), lr=1e-3),
         lambda: tritium.attention(*(torch.randn(1, 2, 4, 16) for _ in range(3))),
         lambda: tritium.linear_cross_entropy(torch.randn(4, 8), torch.randn(10, 8), torch.zeros(4, dtype=torch.long)),
+        lambda: tritium.matmul(torch.randn(4, 4), torch.randn(4, 4)),
+        lambda: tritium.matmul_vec(torch.randn(4), torch.randn(4, 4)),
     ],
 )
 def test_cpu_tensors_are_rejected(call):
