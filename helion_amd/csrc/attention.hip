@@ -2071,7 +2071,11 @@ int bwd_v2(const BwdArgs& a, hipStream_t st) {
   const int64_t q_blocks = (int64_t)x.n_tiles * a.B * a.H;
   attn_bwd_dq_v2<T, D, WQ><<<(unsigned)q_blocks, 64 * WQ, 0, st>>>(x);
   if (int e = check_launch("attention backward (dq, mfma)")) return e;
-  if (TRI_ATTN_DKDV_PAIR) {
+  // head_dim 128: wavefront pairs; head_dim 64 has half the MFMAs per tile
+  // for the same VALU work, and one wavefront doing both roles with its
+  // K and V fragments (attn_bwd_dkdv_v2) measured faster there (0.27 vs
+  // 0.30 ms at [16, 12, 1024, 64], 1.35 vs 1.60 ms at [4, 32, 4096, 64])
+  if constexpr (TRI_ATTN_DKDV_PAIR && D == 128) {
     x.n_tiles = (int)cdiv(a.Tkv, kPairBN);
     const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;
     attn_bwd_dkdv_pair<T, D><<<(unsigned)kv_blocks, 64 * kPairWaves, 0, st>>>(x);
