@@ -52,6 +52,18 @@ __device__ __forceinline__ int64_t load_target(const TT* t, int64_t n) {
   return (int64_t)t[n];
 }
 
+// raw bits of a 16-bit element, and back
+template <typename T>
+__device__ __forceinline__ uint16_t bits16(T x) {
+  static_assert(sizeof(T) == 2, "16-bit type");
+  return __builtin_bit_cast(uint16_t, x);
+}
+template <typename T>
+__device__ __forceinline__ T from_bits16(uint16_t b) {
+  static_assert(sizeof(T) == 2, "16-bit type");
+  return __builtin_bit_cast(T, b);
+}
+
 // ------------------------------------------------------------- forward ----
 struct FwdArgs {
   const void* hidden;  // [N, D]
@@ -287,31 +299,48 @@ lce_g_kernel(GArgs a) {
   const float coef_all = a.grad_out[0] / a.n_valid[0];
   T* gt = (T*)a.gt;
   T* gm = (T*)a.gm;
+  // G [N, Vc] is row-major by token while a lane holds 4 consecutive vocab
+  // rows of one token: stored directly, every store instruction would touch
+  // 32 token rows.  For 16-bit G the tile goes through the (now idle) LDS as
+  // [token][vocab] and leaves as whole 512-byte token rows.  Staging layout:
+  // the 8-byte slot s of token row r sits at slot s ^ (r & 63), so that the
+  // 32 tokens of a half-wavefront write distinct banks.
+  constexpr bool kStage = sizeof(T) == 2 && C::BM * 2 == 512 && C::BM * C::BN * 2 <= C::SMEM_BYTES;
+  char* const tile = smem;
 #pragma unroll
   for (int j = 0; j < C::NT; ++j) {
-    const int64_t n = n0 + acc_col<C>(wn, j, l32);
-    if (n >= a.N) continue;
-    const float l2 = a.lse[n] * kLog2e;
-    const int64_t t = load_target((const TT*)a.target, n);
+    const int tok = acc_col<C>(wn, j, l32);  // token inside the tile
+    const int64_t n = n0 + tok;
+    const bool nvalid = n < a.N;
+    const float l2 = nvalid ? a.lse[n] * kLog2e : 0.f;
+    const int64_t t = nvalid ? load_target((const TT*)a.target, n) : a.ignore_index;
     const float coef = (t == a.ignore_index) ? 0.f : coef_all;
     const int64_t tl = t - a.vc0;  // target row inside this chunk
 #pragma unroll
     for (int i = 0; i < C::MT; ++i) {
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
-        const int64_t vb = v0 + acc_row<C>(wm, i, 4 * rr, g);  // 4 consecutive rows
+        const int vl = acc_row<C>(wm, i, 4 * rr, g);  // 4 consecutive vocab rows
+        const int64_t vb = v0 + vl;
         float gv[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const float pr = fast_exp2(acc.t[i][j][4 * rr + e] * kLog2e - l2);
           gv[e] = (pr - (vb + e == tl ? 1.f : 0.f)) * coef;
         }
-        if (gt != nullptr) {
+        if (gt != nullptr && nvalid) {
 #pragma unroll
           for (int e = 0; e < 4; ++e)
             if (vb + e < a.Vc) gt[(vb + e) * a.ld_gt + n] = from_f32<T>(gv[e]);
         }
-        if (gm != nullptr) {
+        if constexpr (kStage) {
+          if (gm != nullptr) {
+            uint2 pk;
+            pk.x = (uint32_t)bits16(from_f32<T>(gv[0])) | ((uint32_t)bits16(from_f32<T>(gv[1])) << 16);
+            pk.y = (uint32_t)bits16(from_f32<T>(gv[2])) | ((uint32_t)bits16(from_f32<T>(gv[3])) << 16);
+            *reinterpret_cast<uint2*>(tile + tok * 512 + (((vl >> 2) ^ (tok & 63)) << 3)) = pk;
+          }
+        } else if (gm != nullptr && nvalid) {
           T* dst = gm + n * a.ld_g + vb;
           if (vb + 4 <= a.Vc) {
             store_f32<T, 4>(dst, gv);
@@ -321,6 +350,32 @@ lce_g_kernel(GArgs a) {
               if (vb + e < a.Vc) dst[e] = from_f32<T>(gv[e]);
           }
         }
+      }
+    }
+  }
+  if constexpr (kStage) {
+    if (gm == nullptr) return;
+    __syncthreads();
+    // 32 lanes per 512-byte token row, 16 bytes (8 vocab entries) each
+    constexpr int ITER = C::BN * 32 / C::THREADS;
+#pragma unroll
+    for (int it = 0; it < ITER; ++it) {
+      const int idx = it * C::THREADS + threadIdx.x;
+      const int row = idx >> 5, c = idx & 31;
+      const int64_t n = n0 + row;
+      const int64_t vb = v0 + 8 * c;
+      // slots 2c and 2c + 1 sit in one 16-byte chunk, swapped for odd rows
+      u32x4 v = *reinterpret_cast<const u32x4*>(tile + row * 512 + ((((2 * c) ^ (row & 63)) & ~1) << 3));
+      if (row & 1) v = __builtin_shufflevector(v, v, 2, 3, 0, 1);
+      if (n >= a.N || vb >= a.Vc) continue;
+      T* dst = gm + n * a.ld_g + vb;
+      if (vb + 8 <= a.Vc) {
+        st16(dst, v);
+      } else {
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int e = 0; e < 8; ++e)
+          if (vb + e < a.Vc) dst[e] = from_bits16<T>((uint16_t)(w[e >> 1] >> (16 * (e & 1))));
       }
     }
   }
