@@ -100,15 +100,16 @@ struct Problem {
   int64_t M, N, K;
 };
 
-// Issue the DMA of K tile k0 of both operands into one LDS stage.
-template <class C, typename T>
+// Issue DMAs [Q0, Q1) of this wavefront's share of K tile k0 (both
+// operands) into one LDS stage; dma_tile issues all of them.
+template <class C, typename T, int Q0 = 0, int Q1 = C::DMA_PER_WAVE>
 __device__ __forceinline__ void dma_tile(char* stage, const Problem& p, int64_t m0, int64_t n0,
                                          int64_t k0) {
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int rr = lane / C::GRAN;  // row inside the instruction's run of DMA_ROWS rows
   constexpr int VE = vec<T>();
 #pragma unroll
-  for (int q = 0; q < C::DMA_PER_WAVE; ++q) {
+  for (int q = Q0; q < Q1; ++q) {
     const int grp = wave * C::DMA_PER_WAVE + q;  // wave-uniform run of rows
     const int trow = grp * C::DMA_ROWS + rr;     // tile row (A rows, then B rows)
     // the granule that lands in slot lane % GRAN of that row
@@ -196,42 +197,73 @@ template <> struct FragOf<f16_t> { typedef f16x8 V; };
 // Compiler fence: no instruction is scheduled across it.
 __device__ __forceinline__ void fence() { __builtin_amdgcn_sched_barrier(0); }
 
-template <class C, typename T>
-__device__ __forceinline__ void compute_tile(const char* stage, Acc<C>& acc, int wm, int wn) {
+struct NoHook {
+  template <int S> __device__ __forceinline__ void step() const {}
+};
+
+// 16-deep MFMA step S of a K tile and the ones after it; the fragment reads
+// of step S + 1 are issued before the MFMAs of step S (explicit order,
+// fenced against the scheduler: left alone, the compiler reuses one
+// fragment buffer and waits on every read), and hook.step<S>() runs after
+// step S's MFMAs are issued.
+template <class C, typename T, class Hook, int S, class V>
+__device__ __forceinline__ void mma_steps(const char* As, const char* Bs, Acc<C>& acc, int wm,
+                                          int wn, V (&a)[2][C::MT], V (&b)[2][C::NT],
+                                          const Hook& hook) {
+  constexpr int KS = C::RB / 32;
+  if constexpr (S < KS) {
+    const int lane = threadIdx.x & 63;
+    const int l32 = lane & 31, g = lane >> 5;
+    if constexpr (S + 1 < KS) {
+#pragma unroll
+      for (int i = 0; i < C::MT; ++i)
+        a[(S + 1) & 1][i] = *reinterpret_cast<const V*>(As + swz<C>(wm * C::WTM + 32 * i + l32, 2 * (S + 1) + g));
+#pragma unroll
+      for (int j = 0; j < C::NT; ++j)
+        b[(S + 1) & 1][j] = *reinterpret_cast<const V*>(Bs + swz<C>(wn * C::WTN + 32 * j + l32, 2 * (S + 1) + g));
+    }
+    fence();
+#pragma unroll
+    for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+      for (int j = 0; j < C::NT; ++j) acc.t[i][j] = mma(a[S & 1][i], b[S & 1][j], acc.t[i][j]);
+    hook.template step<S>();
+    fence();
+    mma_steps<C, T, Hook, S + 1>(As, Bs, acc, wm, wn, a, b, hook);
+  }
+}
+
+template <class C, class Hook, int S = 0>
+__device__ __forceinline__ void all_steps(const Hook& hook) {
+  if constexpr (S < C::RB / 32) {
+    hook.template step<S>();
+    all_steps<C, Hook, S + 1>(hook);
+  }
+}
+
+// hook.step<s>() runs after the MFMAs of 16-deep step s are issued (the
+// 2-stage loop issues the next tile's DMAs there, spread over the tile
+// instead of in one burst while the MFMA pipe waits)
+template <class C, typename T, class Hook = NoHook>
+__device__ __forceinline__ void compute_tile(const char* stage, Acc<C>& acc, int wm, int wn,
+                                             const Hook& hook = Hook()) {
   const char* As = stage;
   const char* Bs = stage + C::BM * C::RB;
   const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, g = lane >> 5;
   if constexpr (sizeof(T) == 2) {
-    // Explicit order, fenced against the scheduler: the fragment reads of
-    // 16-deep step s + 1 are issued before the MFMAs of step s, so each LDS
-    // round trip hides behind a step of MFMAs (left alone, the compiler
-    // reuses one fragment buffer and waits on every read).
     typedef typename FragOf<T>::V V;
-    constexpr int KS = C::RB / 32;  // 16-deep MFMA steps per K tile
     V a[2][C::MT], b[2][C::NT];
-    auto load = [&](int s, int buf) {
 #pragma unroll
-      for (int i = 0; i < C::MT; ++i)
-        a[buf][i] = *reinterpret_cast<const V*>(As + swz<C>(wm * C::WTM + 32 * i + l32, 2 * s + g));
+    for (int i = 0; i < C::MT; ++i)
+      a[0][i] = *reinterpret_cast<const V*>(As + swz<C>(wm * C::WTM + 32 * i + l32, g));
 #pragma unroll
-      for (int j = 0; j < C::NT; ++j)
-        b[buf][j] = *reinterpret_cast<const V*>(Bs + swz<C>(wn * C::WTN + 32 * j + l32, 2 * s + g));
-    };
-    load(0, 0);
+    for (int j = 0; j < C::NT; ++j)
+      b[0][j] = *reinterpret_cast<const V*>(Bs + swz<C>(wn * C::WTN + 32 * j + l32, g));
     fence();
-#pragma unroll
-    for (int s = 0; s < KS; ++s) {
-      if (s + 1 < KS) load(s + 1, (s + 1) & 1);
-      fence();
-#pragma unroll
-      for (int i = 0; i < C::MT; ++i)
-#pragma unroll
-        for (int j = 0; j < C::NT; ++j)
-          acc.t[i][j] = mma(a[s & 1][i], b[s & 1][j], acc.t[i][j]);
-      fence();
-    }
+    mma_steps<C, T, Hook, 0>(As, Bs, acc, wm, wn, a, b, hook);
   } else {
+    all_steps<C>(hook);  // no MFMA steps to spread over: the hook's work up front
     // fp32: exact FMAs; one float4 (one granule) per row and per column per step
 #pragma unroll 1
     for (int c = 0; c < C::GRAN; ++c) {
@@ -280,6 +312,23 @@ __device__ __forceinline__ void tile_of(int64_t bid, int64_t n_blocks, int tiles
 #ifndef TRI_GEMM_DMA
 #define TRI_GEMM_DMA 1
 #endif
+
+// compute_tile hook: DMAs of the next K tile, DMA_PER_WAVE / KS of them
+// after each 16-deep step
+template <class C, typename T>
+struct DmaSpread {
+  char* st;
+  const Problem* p;
+  int64_t m0, n0, k0;
+  template <int S>
+  __device__ __forceinline__ void step() const {
+    constexpr int KS = C::RB / 32, PER = (C::DMA_PER_WAVE + KS - 1) / KS;
+    constexpr int Q0 = S * PER < C::DMA_PER_WAVE ? S * PER : C::DMA_PER_WAVE;
+    constexpr int Q1 = Q0 + PER < C::DMA_PER_WAVE ? Q0 + PER : C::DMA_PER_WAVE;
+    if constexpr (Q0 < Q1) dma_tile<C, T, Q0, Q1>(st, *p, m0, n0, k0);
+  }
+};
+
 
 // Accumulate the (tm, tn) tile of A * B^T over all of K.  `smem` holds
 // C::SMEM_BYTES of LDS (1 KiB aligned).
@@ -331,8 +380,10 @@ __device__ __forceinline__ void mainloop(const Problem& p, int tm, int tn, char*
     for (int64_t kt = 0; kt + 1 < nfull; ++kt) {
       wait_vmcnt<0>();
       __syncthreads();
-      dma_tile<C, T>(smem + (int)((kt + 1) & 1) * C::STAGE_BYTES, p, m0, n0, (kt + 1) * BK);
-      compute_tile<C, T>(smem + (int)(kt & 1) * C::STAGE_BYTES, acc, wm, wn);
+      // the next tile's DMAs, spread over the 16-deep steps
+      const DmaSpread<C, T> spread{smem + (int)((kt + 1) & 1) * C::STAGE_BYTES, &p, m0, n0,
+                                   (kt + 1) * BK};
+      compute_tile<C, T>(smem + (int)(kt & 1) * C::STAGE_BYTES, acc, wm, wn, spread);
     }
     if (nfull > 0) {
       wait_vmcnt<0>();
