@@ -10,11 +10,11 @@ d_model 768, 12 heads x 64, MLP 3072, vocab 50304, tied embeddings
 
 Precision boundary.  The optimizer owns fp32 master weights in one flat
 buffer; each step runs on a bf16 working copy (one flat buffer, the model's
-parameters are views into it) and autograd accumulates the bf16 gradients
-into a flat buffer of pre-assigned ``.grad`` views.  After backward the
-gradients are widened to fp32 in one pass, ``adamw_step`` updates the whole
-flat master buffer in one launch, and one pass rounds it back into the
-working copy.  Activations are bf16 throughout; every op computes in fp32
+parameters are views into it).  The bf16 gradients come back from
+``torch.autograd.grad`` (nothing accumulated, so no gradient zeroing) and are
+widened straight into the matching views of one flat fp32 buffer by a
+multi-tensor copy; ``adamw_step`` updates the whole flat master buffer in one
+launch, and one pass rounds it back into the working copy.  Activations are bf16 throughout; every op computes in fp32
 internally (the kernels' own rule), the residual stream is stored in bf16
 as the reference's residual-RMSNorm does (rmsnorm.py:72-83).
 
@@ -179,13 +179,14 @@ class HipGPT:
         for name, t in init.items():
             self.master.views[name].copy_(t)
         self.work = _Flat(cfg, self.master.flat.to(torch.bfloat16))
-        self.grad = _Flat(cfg, torch.zeros(n, device=device, dtype=torch.bfloat16))
-        self.grad32 = torch.empty(n, device=device, dtype=torch.float32)
+        self.grad32 = _Flat(cfg, torch.zeros(n, device=device, dtype=torch.float32))
         self.exp_avg = torch.zeros(n, device=device, dtype=torch.float32)
         self.exp_avg_sq = torch.zeros(n, device=device, dtype=torch.float32)
-        for name, p in self.work.leaves().items():
+        leaves = self.work.leaves()
+        for p in leaves.values():
             p.requires_grad_(True)
-            p.grad = self.grad.views[name]
+        self._params = list(leaves.values())
+        self._grad32 = [self.grad32.views[name] for name in leaves]
         self.cos, self.sin = rope_tables(cfg, device)
         self.step_count = 0
 
@@ -221,12 +222,11 @@ class HipGPT:
     def train_step(self, tokens: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
         """One step: forward, backward, fp32-master AdamW; returns the loss."""
         tc = self.tc
-        self.grad.flat.zero_()
         loss = self.loss(tokens, targets)
-        loss.backward()
+        grads = torch.autograd.grad(loss, self._params)
+        torch._foreach_copy_(self._grad32, grads)  # bf16 -> fp32, grouped launches
         self.step_count += 1
-        self.grad32.copy_(self.grad.flat)
-        adamw_step(self.master.flat, self.grad32, self.exp_avg, self.exp_avg_sq, lr=tc.lr,
+        adamw_step(self.master.flat, self.grad32.flat, self.exp_avg, self.exp_avg_sq, lr=tc.lr,
                    beta1=tc.beta1, beta2=tc.beta2, eps=tc.eps, weight_decay=tc.weight_decay,
                    step=self.step_count)
         with torch.no_grad():
@@ -234,7 +234,7 @@ class HipGPT:
         return loss.detach()
 
     def grad_norm(self) -> float:
-        return float(self.grad32.norm())
+        return float(self.grad32.flat.norm())
 
 
 class TorchTwin:
