@@ -205,11 +205,14 @@ class HipGPT:
             p = f"blocks.{i}."
             normed, residual = residual_rmsnorm(delta, residual, self._w(p + "attn_norm"), cfg.eps)
             qkv = torch.matmul(normed, self._w(p + "wqkv").t()).view(b, s, 3, nh, hd)
-            q = qkv[:, :, 0].reshape(b * s, nh, hd).contiguous()
-            k = qkv[:, :, 1].reshape(b * s, nh, hd).contiguous()
+            # unbind, not three slices: its backward stacks the three gradients in
+            # one kernel, where slices would zero-fill and add full-size qkv grads
+            qv, kv, vv = qkv.unbind(2)
+            q = qv.reshape(b * s, nh, hd).contiguous()
+            k = kv.reshape(b * s, nh, hd).contiguous()
             q, k = rope(q, k, cos, sin, position_ids=pos)
             o = attention(q.view(b, s, nh, hd).transpose(1, 2), k.view(b, s, nh, hd).transpose(1, 2),
-                          qkv[:, :, 2].transpose(1, 2), is_causal=True)
+                          vv.transpose(1, 2), is_causal=True)
             o = o.transpose(1, 2).reshape(b, s, nh * hd)
             delta = torch.matmul(o, self._w(p + "wo").t())
             normed, residual = residual_rmsnorm(delta, residual, self._w(p + "ffn_norm"), cfg.eps)
