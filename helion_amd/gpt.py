@@ -30,6 +30,14 @@ logits, torch.optim.AdamW) from identical initial weights and data, for the
 loss-curve parity check; its attention and norms run in fp32.
 
 Run ``python -m helion_amd.gpt --steps 200`` on a GPU for the parity report.
+
+GEMM solutions.  The library's default solution for the weight-gradient
+projections (K = 16384 tokens, few output tiles) is a poor fit;
+``gemm_table_gfx950.csv`` beside this file records, per projection shape of
+this model at the benchmark batch, the fastest hipBLASLt/rocBLAS solution
+PyTorch's TunableOp measured on an MI355X.  ``use_gemm_table`` loads it with
+tuning switched off, so no search runs at training time;
+``python -m helion_amd.gpt --tune-gemm-table PATH`` regenerates it.
 """
 
 from __future__ import annotations
@@ -38,6 +46,8 @@ import argparse
 import dataclasses
 import json
 import math
+import os
+import pathlib
 import time
 
 import torch
@@ -302,6 +312,43 @@ class TorchTwin:
         return loss.detach()
 
 
+GEMM_TABLE = pathlib.Path(__file__).with_name("gemm_table_gfx950.csv")
+
+
+def use_gemm_table(path: str | os.PathLike = GEMM_TABLE) -> bool:
+    """Make torch's GEMMs use the solutions recorded in ``path`` (PyTorch
+    TunableOp with tuning off; shapes not in the table keep the library's
+    default choice).  Process-wide: it changes which library kernel computes
+    every later ``torch.mm`` of a recorded shape.  Returns False, leaving the
+    default choices in force, when TunableOp rejects the file (its validators
+    -- torch, HIP, hipBLASLt and rocBLAS versions, GPU arch -- differ from the
+    running ones) or the file is missing."""
+    from torch.cuda import tunable
+
+    if not pathlib.Path(path).is_file():
+        return False
+    tunable.enable(True)
+    tunable.tuning_enable(False)
+    tunable.set_filename(str(path))
+    ok = bool(tunable.read_file(str(path)))
+    if not ok:
+        tunable.enable(False)
+    return ok
+
+
+def tune_gemm_table(path: str | os.PathLike, cfg: GPTConfig, tc: TrainConfig, device) -> None:
+    """Search the GEMM solutions of one training step of this model and have
+    TunableOp record them in ``path`` (it writes the file when the process
+    exits, since tuning stays enabled)."""
+    from torch.cuda import tunable
+
+    tunable.enable(True)
+    tunable.tuning_enable(True)
+    tunable.set_filename(str(path))
+    model = HipGPT(cfg, tc, init_params(cfg, tc.seed), device)
+    time_steps(model, cfg, tc, steps=1, warmup=1)
+
+
 def time_steps(model: HipGPT, cfg: GPTConfig, tc: TrainConfig, steps: int, warmup: int,
                seed: int = 0) -> dict:
     """Tokens per second of ``model.train_step`` (batches pre-generated)."""
@@ -346,10 +393,15 @@ def main(argv=None) -> int:
     ap.add_argument("--out", default="")
     ap.add_argument("--layers", type=int, default=12)
     ap.add_argument("--batch", type=int, default=16)
+    ap.add_argument("--tune-gemm-table", default="", metavar="PATH",
+                    help="search the projections' GEMM solutions and write them to PATH")
     args = ap.parse_args(argv)
     cfg = GPTConfig(n_layers=args.layers)
     tc = TrainConfig(batch=args.batch)
     dev = torch.device("cuda")
+    if args.tune_gemm_table:
+        tune_gemm_table(args.tune_gemm_table, cfg, tc, dev)
+        return 0
     res = parity(args.steps, cfg, tc, dev)
     summary = {k: v for k, v in res.items() if not isinstance(v, list)}
     summary["loss_first_last_hip"] = [res["loss_hip"][0], res["loss_hip"][-1]]
