@@ -1,0 +1,234 @@
+// Cross-entropy on materialised logits for gfx950.
+//
+// Reference arithmetic: alkinun/helion tritium/ops/cross_entropy.py:36-68
+// (forward: per row lse = log(sum(exp(x - max))) + max in fp32, nll = lse -
+// x[target], loss = mean(nll)) and 71-100 (backward: dlogits = (exp(x - lse) -
+// onehot(target)) * grad_out / n_rows, stored in the logits dtype).
+//
+// Both kernels stream the logits once with 16-byte nontemporal accesses.
+// Forward: each lane keeps a running (max, sum of exp) over its vectors,
+// rescaling the sum once per vector when the max grows; the lanes of a row
+// then merge their pairs with cross-lane shuffles (and LDS across the
+// wavefronts of a block when a whole block shares one row).  Rows shorter
+// than kWideRow get one wavefront each, longer ones a 256-lane block, so both
+// small vocabularies with many rows and one long row fill the machine.  The
+// per-row nll values are summed by one block in a fixed order (the reference
+// accumulates them with atomics), so the loss is deterministic.
+#include "common.h"
+#include "../../include/tritium_hip.h"
+
+namespace tri {
+namespace {
+
+constexpr int kBlock = 256;
+constexpr int64_t kWideRow = 8192;        // rows at least this long get a whole block
+constexpr int64_t kBwdChunk = 256 * 8 * 4;  // elements of one row per backward block
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+
+// exp(x - m) in base 2 on pre-scaled values: a = x * log2(e), mb = m * log2(e)
+__device__ __forceinline__ float exp_shift(float a, float mb) { return fast_exp2(a - mb); }
+
+// Merge (m2, s2) into (m, s): both sums are relative to their own max (in
+// log2 units); an all -inf side contributes nothing.
+__device__ __forceinline__ void merge_ms(float& m, float& s, float m2, float s2) {
+  const float mx = fmaxf(m, m2);
+  if (mx == -INFINITY) return;
+  s = (m == -INFINITY ? 0.0f : s * fast_exp2(m - mx)) + (m2 == -INFINITY ? 0.0f : s2 * fast_exp2(m2 - mx));
+  m = mx;
+}
+
+template <typename TT>
+__device__ __forceinline__ int64_t target_at(const void* t, int64_t row) {
+  return (int64_t)static_cast<const TT*>(t)[row];
+}
+
+// One row's (max, sum) in log2 units for the lanes [lane, lane + LANES, ...).
+template <typename T, int LANES>
+__device__ __forceinline__ void row_ms(const T* __restrict__ x, int64_t V, bool vec_ok, int lane,
+                                       float& m, float& s) {
+  constexpr int VEC = 16 / sizeof(T);
+  m = -INFINITY;
+  s = 0.0f;
+  int64_t tail = 0;
+  if (vec_ok) {
+    const int64_t nv = V / VEC;
+    for (int64_t iv = lane; iv < nv; iv += LANES) {
+      float f[VEC];
+      unpack<T>(ld16_nt(x + iv * VEC), f);
+      float vm = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        f[i] *= kLog2e;
+        vm = fmaxf(vm, f[i]);
+      }
+      if (vm > m) {
+        s = (m == -INFINITY) ? 0.0f : s * fast_exp2(m - vm);
+        m = vm;
+      }
+      if (m != -INFINITY) {
+#pragma unroll
+        for (int i = 0; i < VEC; ++i) s += exp_shift(f[i], m);
+      }
+    }
+    tail = nv * VEC;
+  }
+  for (int64_t i = tail + lane; i < V; i += LANES) {
+    const float a = to_f32(x[i]) * kLog2e;
+    if (a > m) {
+      s = (m == -INFINITY) ? 0.0f : s * fast_exp2(m - a);
+      m = a;
+    }
+    if (m != -INFINITY) s += exp_shift(a, m);
+  }
+}
+
+__device__ __forceinline__ void wave_merge(float& m, float& s) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) {
+    const float m2 = __shfl_xor(m, off, kWave);
+    const float s2 = __shfl_xor(s, off, kWave);
+    merge_ms(m, s, m2, s2);
+  }
+}
+
+// LANES = 64: one wavefront per row, 4 rows per block; LANES = 256: one row per block.
+template <typename T, typename TT, int LANES>
+__global__ void __launch_bounds__(kBlock)
+ce_fwd_kernel(const T* __restrict__ logits, const void* __restrict__ target, float* __restrict__ lse,
+              float* __restrict__ nll, int64_t n_rows, int64_t V, int vec_ok) {
+  constexpr int kRowsPerBlock = kBlock / LANES;
+  const int lane = threadIdx.x % LANES;
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + threadIdx.x / LANES;
+  float m = -INFINITY, s = 0.0f;
+  if (row < n_rows) row_ms<T, LANES>(logits + row * V, V, vec_ok != 0, lane, m, s);
+  wave_merge(m, s);
+  if constexpr (LANES > kWave) {
+    __shared__ float sm[kBlock / kWave], ss[kBlock / kWave];
+    const int w = threadIdx.x / kWave;
+    if ((threadIdx.x & (kWave - 1)) == 0) {
+      sm[w] = m;
+      ss[w] = s;
+    }
+    __syncthreads();
+    m = sm[0];
+    s = ss[0];
+#pragma unroll
+    for (int i = 1; i < kBlock / kWave; ++i) merge_ms(m, s, sm[i], ss[i]);
+  }
+  if (lane == 0 && row < n_rows) {
+    // natural-log logsumexp: (m + log2 s) * ln 2
+    const float l = (m + __log2f(s)) * kLn2;
+    lse[row] = l;
+    const int64_t t = target_at<TT>(target, row);
+    // an out-of-range target has no logit: its nll (and so the loss) is NaN
+    nll[row] = (t >= 0 && t < V) ? l - to_f32(logits[row * V + t]) : __builtin_nanf("");
+  }
+}
+
+// loss = sum(nll) / n_rows, summed in a fixed order (fp64 partials).
+__global__ void __launch_bounds__(kBlock)
+ce_mean_kernel(const float* __restrict__ nll, int64_t n_rows, float* __restrict__ loss) {
+  __shared__ double part[kBlock];
+  double acc = 0.0;
+  for (int64_t i = threadIdx.x; i < n_rows; i += kBlock) acc += (double)nll[i];
+  part[threadIdx.x] = acc;
+  __syncthreads();
+  for (int w = kBlock / 2; w > 0; w >>= 1) {
+    if (threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) loss[0] = (float)(part[0] / (double)n_rows);
+}
+
+// dlogits for one kBwdChunk-element span of one row per block.
+template <typename T, typename TT>
+__global__ void __launch_bounds__(kBlock)
+ce_bwd_kernel(const float* __restrict__ grad_out, const T* __restrict__ logits,
+              const void* __restrict__ target, const float* __restrict__ lse, T* __restrict__ dlogits,
+              int64_t V, int64_t chunks_per_row, float inv_den, int vec_ok) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int64_t row = blockIdx.x / chunks_per_row;
+  const int64_t c0 = (blockIdx.x - row * chunks_per_row) * kBwdChunk;
+  const int64_t c1 = min(c0 + kBwdChunk, V);
+  const float scale = grad_out[0] * inv_den;
+  const float lb = lse[row] * kLog2e;
+  const int64_t t = target_at<TT>(target, row);
+  const T* x = logits + row * V;
+  T* d = dlogits + row * V;
+  int64_t tail = c0;
+  if (vec_ok) {
+    const int64_t v_end = c0 + ((c1 - c0) / VEC) * VEC;
+    for (int64_t e = c0 + (int64_t)threadIdx.x * VEC; e < v_end; e += (int64_t)kBlock * VEC) {
+      float f[VEC];
+      unpack<T>(ld16_nt(x + e), f);
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const float p = fast_exp2(f[i] * kLog2e - lb);
+        f[i] = (p - (e + i == t ? 1.0f : 0.0f)) * scale;
+      }
+      st16_nt(d + e, pack<T>(f));
+    }
+    tail = v_end;
+  }
+  for (int64_t e = tail + threadIdx.x; e < c1; e += kBlock) {
+    const float p = fast_exp2(to_f32(x[e]) * kLog2e - lb);
+    d[e] = from_f32<T>((p - (e == t ? 1.0f : 0.0f)) * scale);
+  }
+}
+
+#define TRI_DISPATCH_INDEX(kind, TT, ...)                                           \
+  do {                                                                              \
+    if ((kind) == 1) { typedef int32_t TT; __VA_ARGS__; }                           \
+    else if ((kind) == 2) { typedef int64_t TT; __VA_ARGS__; }                      \
+    else return fail(TRI_EINVAL, "cross_entropy: bad target kind %d", (int)(kind)); \
+  } while (0)
+
+bool rows_vec_ok(const void* p, int64_t V, int dtype) {
+  return aligned16(p) && ((V * dtype_size(dtype)) % 16) == 0;
+}
+
+}  // namespace
+}  // namespace tri
+
+using namespace tri;
+
+extern "C" int tritium_cross_entropy_fwd(const void* logits, const void* target, int target_kind,
+                                         float* loss, float* lse, float* nll, int64_t n_rows,
+                                         int64_t vocab, int dtype, void* stream) {
+  if (n_rows < 0 || vocab <= 0) return fail(TRI_EINVAL, "cross_entropy: bad sizes");
+  hipStream_t st = (hipStream_t)stream;
+  if (n_rows == 0) return TRI_OK;
+  const int vec_ok = rows_vec_ok(logits, vocab, dtype);
+  TRI_DISPATCH_INDEX(target_kind, TT,
+    TRI_DISPATCH_FLOAT(dtype, T, {
+      if (vocab >= kWideRow) {
+        ce_fwd_kernel<T, TT, kBlock><<<(unsigned)n_rows, kBlock, 0, st>>>(
+            (const T*)logits, target, lse, nll, n_rows, vocab, vec_ok);
+      } else {
+        ce_fwd_kernel<T, TT, kWave><<<(unsigned)cdiv(n_rows, kBlock / kWave), kBlock, 0, st>>>(
+            (const T*)logits, target, lse, nll, n_rows, vocab, vec_ok);
+      }
+    }));
+  if (int e = check_launch("cross_entropy_fwd")) return e;
+  ce_mean_kernel<<<1, kBlock, 0, st>>>(nll, n_rows, loss);
+  return check_launch("cross_entropy_mean");
+}
+
+extern "C" int tritium_cross_entropy_bwd(const float* grad_out, const void* logits,
+                                         const void* target, int target_kind, const float* lse,
+                                         void* dlogits, int64_t n_rows, int64_t vocab,
+                                         double grad_denominator, int dtype, void* stream) {
+  if (n_rows < 0 || vocab <= 0) return fail(TRI_EINVAL, "cross_entropy: bad sizes");
+  if (n_rows == 0) return TRI_OK;
+  const int64_t chunks = cdiv(vocab, kBwdChunk);
+  if (n_rows * chunks > 0x7fffffffLL) return fail(TRI_EINVAL, "cross_entropy: grid too large");
+  const int vec_ok = rows_vec_ok(logits, vocab, dtype) && rows_vec_ok(dlogits, vocab, dtype);
+  const float inv_den = (float)(1.0 / grad_denominator);
+  hipStream_t st = (hipStream_t)stream;
+  TRI_DISPATCH_INDEX(target_kind, TT,
+    TRI_DISPATCH_FLOAT(dtype, T,
+      ce_bwd_kernel<T, TT><<<(unsigned)(n_rows * chunks), kBlock, 0, st>>>(
+          grad_out, (const T*)logits, target, lse, (T*)dlogits, vocab, chunks, inv_den, vec_ok)));
+  return check_launch("cross_entropy_bwd");
+}

@@ -179,6 +179,26 @@ int tritium_linear_ce_grad_logits(const float* grad_out, const float* n_valid, c
                                   int64_t n_rows, int64_t hidden_size, int64_t vocab, int64_t v0,
                                   int64_t vc, int dtype, void* stream);
 
+/* ---- Cross-entropy on materialised logits ----------------------------------
+ * tritium.cross_entropy forward (tritium/ops/cross_entropy.py:36-68
+ * `_cross_entropy_forward_kernel`, host 534-561): for logits [n_rows, vocab]
+ * in `dtype` (row-major, contiguous) and int32 (target_kind 1) or int64 (2)
+ * targets, lse[row] = logsumexp(logits[row]) in fp32, nll[row] = lse[row] -
+ * logits[row, target[row]] (NaN for a target outside [0, vocab)), and
+ * loss[0] = mean(nll) summed in a fixed order.  `nll` is caller-provided
+ * scratch of n_rows floats. */
+int tritium_cross_entropy_fwd(const void* logits, const void* target, int target_kind,
+                              float* loss, float* lse, float* nll, int64_t n_rows, int64_t vocab,
+                              int dtype, void* stream);
+
+/* tritium.cross_entropy_backward (cross_entropy.py:71-100
+ * `_cross_entropy_backward_kernel`, host 728-799): dlogits = (exp(logits -
+ * lse) - onehot(target)) * grad_out[0] / grad_denominator in `dtype`
+ * (grad_out a device float; the reference's denominator is n_rows). */
+int tritium_cross_entropy_bwd(const float* grad_out, const void* logits, const void* target,
+                              int target_kind, const float* lse, void* dlogits, int64_t n_rows,
+                              int64_t vocab, double grad_denominator, int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
