@@ -140,7 +140,10 @@ def _linear_cross_entropy_forward(hidden, weight, target, ignore_index: int = IG
     return loss, lse
 
 
-_G_CHUNK_BYTES = 1 << 30  # gradient-of-logits tile per chunk
+# gradient-of-logits tile per chunk: one chunk at both benchmark shapes (2.1 GB
+# at N = 8192, V = 128256), so dH is a single GEMM with a 16-bit output and no
+# fp32 accumulation pass (measured 22.3 -> 21.9 ms against 1 GiB chunks)
+_G_CHUNK_BYTES = 4 << 30
 _mm_out_dtype: bool | None = None  # torch.mm(..., out_dtype=float32) available on this device
 
 
