@@ -55,6 +55,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _P, _P, _P, _P, _I32, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I32,
          _I32, _P],
     ),
+    "tritium_rope_strided": (
+        _I32,
+        [_P, _P, _P, _P, _P, _I32, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _I32, _I64, _I64,
+         _I32, _I32, _P],
+    ),
     "tritium_swiglu_fwd": (_I32, [_P, _P, _P, _I64, _I32, _P]),
     "tritium_swiglu_bwd": (_I32, [_P, _P, _P, _P, _P, _I64, _I32, _P]),
     "tritium_adamw_step": (

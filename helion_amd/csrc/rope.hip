@@ -14,6 +14,11 @@
 //
 // A position outside [0, max_position) has no table row; the kernel then
 // writes NaN for that token instead of reading out of bounds.
+//
+// Token rows of the inputs and of the outputs each have their own stride
+// (elements; heads are adjacent inside a row), so q and k can be read in
+// place from a fused [tokens, 3, heads, head_dim] projection and the inverse
+// rotation written back into the matching gradient rows.
 #include "common.h"
 #include "../../include/tritium_hip.h"
 
@@ -27,7 +32,8 @@ __global__ void __launch_bounds__(kBlock)
 rope_kernel(const T* q, const T* k, const CT* __restrict__ cos_t,
             const CT* __restrict__ sin_t, const void* __restrict__ pos_ids, int pos_kind,
             T* q_out, T* k_out, uint32_t n_items, uint32_t items_per_head, uint32_t n_heads,
-            int head_dim, int64_t max_pos, int64_t offset, int interleaved, int inverse) {
+            int head_dim, int64_t max_pos, int64_t offset, int interleaved, int inverse,
+            int64_t in_ts, int64_t out_ts) {
   const uint32_t item = blockIdx.x * kBlock + threadIdx.x;
   if (item >= n_items) return;
   const uint32_t th = item / items_per_head;
@@ -43,7 +49,9 @@ rope_kernel(const T* q, const T* k, const CT* __restrict__ cos_t,
   } else {
     pos = (int64_t)token + offset;
   }
-  const int64_t base = (int64_t)th * head_dim;
+  const int64_t hoff = (int64_t)(th - token * n_heads) * head_dim;
+  const int64_t base = (int64_t)token * in_ts + hoff;   // q, k
+  const int64_t obase = (int64_t)token * out_ts + hoff;  // q_out, k_out
   const bool valid = pos >= 0 && pos < max_pos;
 
   // The P pairs this lane owns start at pair index p0 (cos/sin column p0).
@@ -73,10 +81,10 @@ rope_kernel(const T* q, const T* k, const CT* __restrict__ cos_t,
       oka[i] = valid ? ka[i] * c[i] - kb[i] * s[i] : nan;
       okb[i] = valid ? kb[i] * c[i] + ka[i] * s[i] : nan;
     }
-    store_stream<T, P>(q_out + base + p0, oqa);
-    store_stream<T, P>(q_out + base + half + p0, oqb);
-    store_stream<T, P>(k_out + base + p0, oka);
-    store_stream<T, P>(k_out + base + half + p0, okb);
+    store_stream<T, P>(q_out + obase + p0, oqa);
+    store_stream<T, P>(q_out + obase + half + p0, oqb);
+    store_stream<T, P>(k_out + obase + p0, oka);
+    store_stream<T, P>(k_out + obase + half + p0, okb);
   } else {
     // elements [2*p0, 2*p0 + 2P) hold P adjacent (a, b) pairs
     float qv[2 * P], kv[2 * P];
@@ -94,17 +102,18 @@ rope_kernel(const T* q, const T* k, const CT* __restrict__ cos_t,
       ok[2 * i] = valid ? ka * c[i] - kb * s[i] : nan;
       ok[2 * i + 1] = valid ? kb * c[i] + ka * s[i] : nan;
     }
-    store_stream<T, P>(q_out + base + 2 * p0, *reinterpret_cast<float(*)[P]>(oq));
-    store_stream<T, P>(q_out + base + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(oq + P));
-    store_stream<T, P>(k_out + base + 2 * p0, *reinterpret_cast<float(*)[P]>(ok));
-    store_stream<T, P>(k_out + base + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(ok + P));
+    store_stream<T, P>(q_out + obase + 2 * p0, *reinterpret_cast<float(*)[P]>(oq));
+    store_stream<T, P>(q_out + obase + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(oq + P));
+    store_stream<T, P>(k_out + obase + 2 * p0, *reinterpret_cast<float(*)[P]>(ok));
+    store_stream<T, P>(k_out + obase + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(ok + P));
   }
 }
 
 template <typename T, typename CT, int P>
 int launch(const void* q, const void* k, const void* cs, const void* sn, const void* pos,
            int pos_kind, void* qo, void* ko, int64_t n_tokens, int64_t n_heads, int64_t head_dim,
-           int64_t max_pos, int64_t offset, int interleaved, int inverse, hipStream_t stream) {
+           int64_t max_pos, int64_t offset, int interleaved, int inverse, int64_t in_ts,
+           int64_t out_ts, hipStream_t stream) {
   const int64_t items_per_head = (head_dim / 2) / P;
   const int64_t n_items = n_tokens * n_heads * items_per_head;
   if (n_items >= ((int64_t)1 << 32) - kBlock)
@@ -112,7 +121,7 @@ int launch(const void* q, const void* k, const void* cs, const void* sn, const v
   rope_kernel<T, CT, P><<<(unsigned)cdiv(n_items, kBlock), kBlock, 0, stream>>>(
       (const T*)q, (const T*)k, (const CT*)cs, (const CT*)sn, pos, pos_kind, (T*)qo, (T*)ko,
       (uint32_t)n_items, (uint32_t)items_per_head, (uint32_t)n_heads, (int)head_dim, max_pos,
-      offset, interleaved, inverse);
+      offset, interleaved, inverse, in_ts, out_ts);
   return check_launch("rope");
 }
 
@@ -120,11 +129,12 @@ template <typename T, typename CT>
 int dispatch_pairs(const void* q, const void* k, const void* cs, const void* sn, const void* pos,
                    int pos_kind, void* qo, void* ko, int64_t n_tokens, int64_t n_heads,
                    int64_t head_dim, int64_t max_pos, int64_t offset, int interleaved,
-                   int inverse, hipStream_t stream) {
+                   int inverse, int64_t in_ts, int64_t out_ts, hipStream_t stream) {
   // P pairs per lane: 16-byte q/k vectors when every access stays aligned.
   constexpr int PV = 16 / sizeof(T);
   const int64_t half = head_dim / 2;
-  const bool ptr_ok = aligned16(q) && aligned16(k) && aligned16(qo) && aligned16(ko);
+  const bool ptr_ok = aligned16(q) && aligned16(k) && aligned16(qo) && aligned16(ko) &&
+                      in_ts % PV == 0 && out_ts % PV == 0;
   // split layout: offsets p0 and half+p0 (elements) must be multiples of PV, cos/sin
   // offsets pos*half+p0 multiples of PV (CT) -> half % PV == 0 covers all of them.
   // interleaved: offsets 2*p0 and 2*p0+P must be multiples of P -> half % PV == 0.
@@ -132,10 +142,10 @@ int dispatch_pairs(const void* q, const void* k, const void* cs, const void* sn,
                       ((uintptr_t)sn % (sizeof(CT) * PV) == 0);
   if (ptr_ok && tbl_ok && half % PV == 0) {
     return launch<T, CT, PV>(q, k, cs, sn, pos, pos_kind, qo, ko, n_tokens, n_heads, head_dim,
-                             max_pos, offset, interleaved, inverse, stream);
+                             max_pos, offset, interleaved, inverse, in_ts, out_ts, stream);
   }
   return launch<T, CT, 1>(q, k, cs, sn, pos, pos_kind, qo, ko, n_tokens, n_heads, head_dim,
-                          max_pos, offset, interleaved, inverse, stream);
+                          max_pos, offset, interleaved, inverse, in_ts, out_ts, stream);
 }
 
 }  // namespace
@@ -143,15 +153,20 @@ int dispatch_pairs(const void* q, const void* k, const void* cs, const void* sn,
 
 using namespace tri;
 
-extern "C" int tritium_rope(const void* q, const void* k, const void* cos_table,
-                            const void* sin_table, const void* position_ids, int position_kind,
-                            void* q_out, void* k_out, int64_t n_tokens, int64_t n_heads,
-                            int64_t head_dim, int64_t max_position, int64_t position_offset,
-                            int interleaved, int inverse, int dtype, int table_dtype,
-                            void* stream) {
+extern "C" int tritium_rope_strided(const void* q, const void* k, const void* cos_table,
+                                    const void* sin_table, const void* position_ids,
+                                    int position_kind, void* q_out, void* k_out, int64_t n_tokens,
+                                    int64_t n_heads, int64_t head_dim, int64_t max_position,
+                                    int64_t position_offset, int interleaved, int inverse,
+                                    int64_t in_token_stride, int64_t out_token_stride, int dtype,
+                                    int table_dtype, void* stream) {
   if (n_tokens < 0 || n_heads <= 0 || head_dim <= 0 || (head_dim & 1) || max_position < 0)
     return fail(TRI_EINVAL, "rope: bad shape tokens=%lld heads=%lld head_dim=%lld",
                 (long long)n_tokens, (long long)n_heads, (long long)head_dim);
+  if (in_token_stride < n_heads * head_dim || out_token_stride < n_heads * head_dim)
+    return fail(TRI_EINVAL, "rope: token strides %lld/%lld below heads*head_dim %lld",
+                (long long)in_token_stride, (long long)out_token_stride,
+                (long long)(n_heads * head_dim));
   if (position_kind < 0 || position_kind > 2 || (position_kind != 0 && position_ids == nullptr))
     return fail(TRI_EINVAL, "rope: bad position_ids kind %d", position_kind);
   if (n_tokens == 0) return TRI_OK;
@@ -160,6 +175,19 @@ extern "C" int tritium_rope(const void* q, const void* k, const void* cos_table,
     TRI_DISPATCH_FLOAT(table_dtype, CT,
       return dispatch_pairs<T, CT>(q, k, cos_table, sin_table, position_ids, position_kind,
                                    q_out, k_out, n_tokens, n_heads, head_dim, max_position,
-                                   position_offset, interleaved, inverse, s)));
+                                   position_offset, interleaved, inverse, in_token_stride,
+                                   out_token_stride, s)));
   return TRI_OK;
+}
+
+extern "C" int tritium_rope(const void* q, const void* k, const void* cos_table,
+                            const void* sin_table, const void* position_ids, int position_kind,
+                            void* q_out, void* k_out, int64_t n_tokens, int64_t n_heads,
+                            int64_t head_dim, int64_t max_position, int64_t position_offset,
+                            int interleaved, int inverse, int dtype, int table_dtype,
+                            void* stream) {
+  return tritium_rope_strided(q, k, cos_table, sin_table, position_ids, position_kind, q_out,
+                              k_out, n_tokens, n_heads, head_dim, max_position, position_offset,
+                              interleaved, inverse, n_heads * head_dim, n_heads * head_dim, dtype,
+                              table_dtype, stream);
 }

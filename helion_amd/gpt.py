@@ -57,7 +57,7 @@ from .adamw import adamw_step
 from .attention import attention
 from .linear_ce import linear_cross_entropy
 from .rmsnorm import residual_rmsnorm
-from .rope import rope
+from .rope import rope_rows
 from .swiglu import swiglu
 
 
@@ -215,12 +215,7 @@ class HipGPT:
             p = f"blocks.{i}."
             normed, residual = residual_rmsnorm(delta, residual, self._w(p + "attn_norm"), cfg.eps)
             qkv = torch.matmul(normed, self._w(p + "wqkv").t()).view(b, s, 3, nh, hd)
-            # unbind, not three slices: its backward stacks the three gradients in
-            # one kernel, where slices would zero-fill and add full-size qkv grads
-            qv, kv, vv = qkv.unbind(2)
-            q = qv.reshape(b * s, nh, hd).contiguous()
-            k = kv.reshape(b * s, nh, hd).contiguous()
-            q, k = rope(q, k, cos, sin, position_ids=pos)
+            q, k, vv = _QKVRope.apply(qkv, cos, sin, pos)
             o = attention(q.view(b, s, nh, hd).transpose(1, 2), k.view(b, s, nh, hd).transpose(1, 2),
                           vv.transpose(1, 2), is_causal=True)
             o = o.transpose(1, 2).reshape(b, s, nh * hd)
@@ -310,6 +305,38 @@ class TorchTwin:
         self.last_grad_norm = float(torch.norm(torch.stack([
             work[k].grad.float().norm() for k in self.master])))
         return loss.detach()
+
+
+class _QKVRope(torch.autograd.Function):
+    """Split of the fused q/k/v projection ``[b, s, 3, heads, head_dim]`` with
+    RoPE on q and k: one kernel reads q and k in place and writes the rotated
+    rows contiguously (what ``rope`` computes on contiguous copies); v is
+    returned as a view.  The backward writes the inverse rotation of dq, dk
+    and a copy of dv straight into one fused gradient, instead of a stack of
+    three gradients after two contiguous copies and a separate rope pass."""
+
+    @staticmethod
+    def forward(ctx, qkv, cos, sin, pos):
+        b, s, _, nh, hd = qkv.shape
+        flat = qkv.view(b * s, 3, nh, hd)
+        q = torch.empty((b * s, nh, hd), device=qkv.device, dtype=qkv.dtype)
+        k = torch.empty_like(q)
+        rope_rows(flat[:, 0], flat[:, 1], cos, sin, pos, q, k, inverse=False,
+                  in_token_stride=3 * nh * hd, out_token_stride=nh * hd)
+        ctx.save_for_backward(cos, sin, pos)
+        ctx.shape = qkv.shape
+        return q, k, qkv[:, :, 2]
+
+    @staticmethod
+    def backward(ctx, dq, dk, dv):
+        cos, sin, pos = ctx.saved_tensors
+        b, s, _, nh, hd = ctx.shape
+        dqkv = torch.empty(ctx.shape, device=dq.device, dtype=dq.dtype)
+        flat = dqkv.view(b * s, 3, nh, hd)
+        rope_rows(dq.contiguous(), dk.contiguous(), cos, sin, pos, flat[:, 0], flat[:, 1],
+                  inverse=True, in_token_stride=nh * hd, out_token_stride=3 * nh * hd)
+        dqkv[:, :, 2].copy_(dv)
+        return dqkv, None, None, None
 
 
 GEMM_TABLE = pathlib.Path(__file__).with_name("gemm_table_gfx950.csv")

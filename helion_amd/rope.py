@@ -143,6 +143,38 @@ def _launch(q, k, cos, sin, position_ids, position_offset, interleaved, inverse,
     )
 
 
+def rope_rows(q, k, cos, sin, position_ids, q_out, k_out, *, inverse: bool,
+              in_token_stride: int, out_token_stride: int) -> None:
+    """Rotate (or, with ``inverse``, un-rotate) token rows of q and k into
+    q_out/k_out, where each operand is addressed as token * stride + head *
+    head_dim + i with its own token stride -- e.g. q and k read in place from a
+    fused [tokens, 3, heads, head_dim] projection (``tritium_rope_strided``).
+    Not part of the reference's surface (its rope takes contiguous tensors
+    only, rope.py:192-195): the training harness's fused split uses it.  q,
+    k, q_out, k_out are [tokens, heads, head_dim]-shaped views with those
+    strides and a unit head_dim stride; positions as in ``rope``."""
+    n_tokens, n_heads, head_dim = q.shape
+    for t in (k, q_out, k_out):
+        if t.shape != q.shape or t.dtype != q.dtype or t.device != q.device:
+            raise ValueError("rope_rows: q, k, q_out, k_out must share shape, dtype and device")
+    for t, ts in ((q, in_token_stride), (k, in_token_stride), (q_out, out_token_stride),
+                  (k_out, out_token_stride)):
+        if t.stride() != (ts, head_dim, 1):
+            raise ValueError(f"rope_rows: expected strides {(ts, head_dim, 1)}, got {t.stride()}")
+    if n_tokens == 0:
+        return
+    if sin.dtype != cos.dtype:
+        sin = sin.to(cos.dtype)
+    kind = 0 if position_ids is None else (1 if position_ids.dtype == torch.int32 else 2)
+    _lib.call(
+        "tritium_rope_strided", q.data_ptr(), k.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+        _lib.ptr(position_ids), kind, q_out.data_ptr(), k_out.data_ptr(), n_tokens, n_heads,
+        head_dim, cos.shape[0], 0, 0, int(bool(inverse)), int(in_token_stride),
+        int(out_token_stride), _lib.dtype_code(q.dtype), _lib.dtype_code(cos.dtype),
+        _lib.stream_of(q),
+    )
+
+
 def _rope_forward(q, k, cos, sin, position_ids, position_offset, interleaved, inverse):
     """rope.py:201-247 (out of place)."""
     q_out = torch.empty_like(q)

@@ -75,6 +75,21 @@ int tritium_rope(const void* q, const void* k, const void* cos_table, const void
                  int64_t position_offset, int interleaved, int inverse, int dtype,
                  int table_dtype, void* stream);
 
+/* tritium_rope with its own token-row strides (elements) for the inputs q, k
+ * and for the outputs q_out, k_out; heads stay adjacent inside a row
+ * (tritium_rope is this with both strides n_heads * head_dim).  No counterpart
+ * in the reference, whose rope requires contiguous q and k (rope.py:192-195):
+ * it lets a caller rotate q and k in place inside a fused
+ * [tokens, 3, heads, head_dim] q/k/v projection (token stride
+ * 3 * heads * head_dim), and write the backward's inverse rotation straight
+ * into the fused gradient. */
+int tritium_rope_strided(const void* q, const void* k, const void* cos_table,
+                         const void* sin_table, const void* position_ids, int position_kind,
+                         void* q_out, void* k_out, int64_t n_tokens, int64_t n_heads,
+                         int64_t head_dim, int64_t max_position, int64_t position_offset,
+                         int interleaved, int inverse, int64_t in_token_stride,
+                         int64_t out_token_stride, int dtype, int table_dtype, void* stream);
+
 /* ---- SwiGLU ----------------------------------------------------------------
  * tritium.swiglu forward (tritium/ops/swiglu.py:21-35 `_swiglu_forward_kernel`,
  * host 61-73): out = silu(x) * gate over n elements. */

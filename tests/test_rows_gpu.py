@@ -70,6 +70,50 @@ def test_rope_inplace_matches_out_of_place():
     assert torch.equal(q, qo) and torch.equal(k, ko)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("head_dim", [64, 6])
+def test_rope_rows_in_fused_qkv_matches_rope(dtype, head_dim):
+    # tritium_rope_strided: q, k read in place from [tokens, 3, heads, head_dim] and the
+    # inverse rotation written back into it give exactly what rope does on contiguous copies
+    from helion_amd.rope import rope_rows
+    t, h = 300, 5
+    qkv = randn((t, 3, h, head_dim), dtype, 21)
+    cos, sin = _tables(512, head_dim)
+    pos = torch.randint(0, 512, (t,), generator=torch.Generator().manual_seed(3)).cuda()
+    q, k = torch.empty((t, h, head_dim), device="cuda", dtype=dtype), torch.empty((t, h, head_dim), device="cuda", dtype=dtype)
+    rope_rows(qkv[:, 0], qkv[:, 1], cos, sin, pos, q, k, inverse=False,
+              in_token_stride=3 * h * head_dim, out_token_stride=h * head_dim)
+    eq, ek = tritium.rope(qkv[:, 0].contiguous(), qkv[:, 1].contiguous(), cos, sin, position_ids=pos)
+    assert torch.equal(q, eq) and torch.equal(k, ek)
+    back = torch.full_like(qkv, 7.0)
+    rope_rows(q, k, cos, sin, pos, back[:, 0], back[:, 1], inverse=True,
+              in_token_stride=h * head_dim, out_token_stride=3 * h * head_dim)
+    from helion_amd.rope import _rope_forward
+    iq, ik = _rope_forward(q, k, cos, sin, pos, 0, False, True)
+    assert torch.equal(back[:, 0], iq) and torch.equal(back[:, 1], ik)
+    assert torch.equal(back[:, 2], torch.full_like(back[:, 2], 7.0))  # v rows untouched
+
+
+def test_fused_qkv_split_matches_unbind_rope():
+    # the training harness's split (gpt._QKVRope) against unbind + contiguous + rope, fwd and bwd
+    from helion_amd.gpt import _QKVRope
+    b, s, h, d = 2, 96, 3, 64
+    cos, sin = _tables(128, d)
+    pos = torch.arange(s, device="cuda").repeat(b)
+    base = randn((b, s, 3, h, d), torch.bfloat16, 5)
+    gq, gk, gv = (randn((b * s, h, d), torch.bfloat16, 10 + i) for i in range(3))
+    x1 = base.clone().requires_grad_(True)
+    q1, k1, v1 = _QKVRope.apply(x1, cos, sin, pos)
+    torch.autograd.backward([q1, k1, v1], [gq, gk, gv.view(b, s, h, d)])
+    x2 = base.clone().requires_grad_(True)
+    qv, kv, vv = x2.unbind(2)
+    q2, k2 = tritium.rope(qv.reshape(b * s, h, d).contiguous(), kv.reshape(b * s, h, d).contiguous(),
+                          cos, sin, position_ids=pos)
+    torch.autograd.backward([q2, k2, vv], [gq, gk, gv.view(b, s, h, d)])
+    assert torch.equal(q1, q2) and torch.equal(k1, k2) and torch.equal(v1, vv)
+    assert torch.equal(x1.grad, x2.grad)
+
+
 def test_rope_out_of_range_position_is_nan_not_a_fault():
     q = randn((4, 2, 16), torch.float32, 1)
     cos, sin = _tables(8, 16)
