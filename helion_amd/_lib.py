@@ -62,6 +62,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     ),
     "tritium_swiglu_fwd": (_I32, [_P, _P, _P, _I64, _I32, _P]),
     "tritium_swiglu_bwd": (_I32, [_P, _P, _P, _P, _P, _I64, _I32, _P]),
+    "tritium_swiglu_rows_fwd": (_I32, [_P, _P, _P, _I64, _I64, _I64, _I64, _I32, _P]),
+    "tritium_swiglu_rows_bwd": (
+        _I32, [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I32, _P],
+    ),
     "tritium_adamw_step": (
         _I32,
         [_P, _P, _P, _P, _I64, _F32, _F32, _F32, _F32, _F32, _F64, _F64, _I32, _P],

@@ -82,6 +82,14 @@ def _unit_last(t: torch.Tensor) -> torch.Tensor:
     return t if t.stride(-1) == 1 else t.contiguous()
 
 
+def _rows_aligned(t: torch.Tensor) -> bool:
+    """Unit head_dim stride, 16-byte aligned base and row strides (what the MFMA
+    kernels need of every operand to take it in place)."""
+    es = t.element_size()
+    return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
+            and all((st * es) % 16 == 0 for st in t.stride()[:-1]))
+
+
 def _strides(*ts: torch.Tensor) -> torch.Tensor:
     vals: list[int] = []
     for t in ts:
@@ -172,7 +180,11 @@ class _AttentionAutograd(torch.autograd.Function):
     def backward(ctx: Any, *grad_outputs: torch.Tensor):
         do = grad_outputs[0]
         q, k, v, o, lse = ctx.saved_tensors
-        if not do.is_contiguous():
+        # attention.py:726-727 copies a non-contiguous upstream gradient; the kernels read
+        # dO through its own (batch, head, seq) strides, so a copy is needed only when
+        # those strides would break 16-byte row alignment (e.g. not the transposed
+        # [batch, seq, heads, head_dim] view a module passes)
+        if not do.is_contiguous() and not _rows_aligned(do):
             do = do.contiguous()
         dq, dk, dv = _attention_backward_impl(do, q, k, v, o, lse, ctx.is_causal)
         return (

@@ -11,6 +11,8 @@
 #include "common.h"
 #include "../../include/tritium_hip.h"
 
+#include <initializer_list>
+
 namespace tri {
 namespace {
 
@@ -95,6 +97,112 @@ swiglu_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x, const T* __
   }
 }
 
+// Row-strided variants: n_rows rows of n_cols elements; x and gate rows at
+// stride ld_in, dy rows at ld_dy, outputs at ld_out (elements) -- e.g. x and
+// gate as the two halves of each row of a fused [tokens, 2 * d_ff]
+// projection, and the gradients written back into the same layout.  A
+// workgroup covers up to kBlock * kRowU vectors of one row (the row index is
+// one scalar division per workgroup).
+constexpr int kRowU = 2;
+
+template <typename T, int VEC>
+__global__ void __launch_bounds__(kBlock)
+swiglu_rows_fwd_kernel(const T* __restrict__ x, const T* __restrict__ g, T* __restrict__ out,
+                       int64_t n_cols, int64_t ld_in, int64_t ld_out, int64_t chunks) {
+  const int64_t row = blockIdx.x / chunks;
+  const int64_t c0 = (blockIdx.x - row * chunks) * (int64_t)kBlock * kRowU * VEC;
+  const T* xr = x + row * ld_in;
+  const T* gr = g + row * ld_in;
+  T* orow = out + row * ld_out;
+  float xv[kRowU][VEC], gv[kRowU][VEC];
+#pragma unroll
+  for (int u = 0; u < kRowU; ++u) {
+    const int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * VEC;
+    if (c < n_cols) {
+      load_stream<T, VEC>(xr + c, xv[u]);
+      load_stream<T, VEC>(gr + c, gv[u]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kRowU; ++u) {
+    const int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * VEC;
+    if (c < n_cols) {
+      float o[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) o[i] = xv[u][i] * sigmoid_f32(xv[u][i]) * gv[u][i];
+      store_stream<T, VEC>(orow + c, o);
+    }
+  }
+}
+
+template <typename T, int VEC>
+__global__ void __launch_bounds__(kBlock)
+swiglu_rows_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x, const T* __restrict__ g,
+                       T* __restrict__ dx, T* __restrict__ dg, int64_t n_cols, int64_t ld_dy,
+                       int64_t ld_in, int64_t ld_out, int64_t chunks) {
+  const int64_t row = blockIdx.x / chunks;
+  const int64_t c0 = (blockIdx.x - row * chunks) * (int64_t)kBlock * kRowU * VEC;
+  const T* dyr = dy + row * ld_dy;
+  const T* xr = x + row * ld_in;
+  const T* gr = g + row * ld_in;
+  float dv[kRowU][VEC], xv[kRowU][VEC], gv[kRowU][VEC];
+#pragma unroll
+  for (int u = 0; u < kRowU; ++u) {
+    const int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * VEC;
+    if (c < n_cols) {
+      load_stream<T, VEC>(dyr + c, dv[u]);
+      load_stream<T, VEC>(xr + c, xv[u]);
+      load_stream<T, VEC>(gr + c, gv[u]);
+    }
+  }
+#pragma unroll
+  for (int u = 0; u < kRowU; ++u) {
+    const int64_t c = c0 + ((int64_t)u * kBlock + threadIdx.x) * VEC;
+    if (c < n_cols) {
+      float ox[VEC], og[VEC];
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) {
+        const float s = sigmoid_f32(xv[u][i]);
+        const float silu = xv[u][i] * s;
+        const float dsilu = s * (1.0f + xv[u][i] * (1.0f - s));
+        ox[i] = dv[u][i] * gv[u][i] * dsilu;
+        og[i] = dv[u][i] * silu;
+      }
+      store_stream<T, VEC>(dx + row * ld_out + c, ox);
+      store_stream<T, VEC>(dg + row * ld_out + c, og);
+    }
+  }
+}
+
+// VEC-element vectors when every row start stays 16-byte aligned and no
+// vector straddles a row end.
+template <typename T>
+bool rows_vec_ok(std::initializer_list<const void*> ptrs, std::initializer_list<int64_t> lds,
+                 int64_t n_cols) {
+  constexpr int VEC = 16 / sizeof(T);
+  for (const void* p : ptrs)
+    if (!aligned16(p)) return false;
+  for (int64_t ld : lds)
+    if (ld % VEC) return false;
+  return n_cols % VEC == 0;
+}
+
+template <int VEC>
+int64_t row_chunks(int64_t n_cols) { return cdiv(n_cols, (int64_t)kBlock * kRowU * VEC); }
+
+int check_rows(int64_t n_rows, int64_t n_cols, std::initializer_list<int64_t> lds) {
+  if (n_rows < 0 || n_cols < 0)
+    return fail(TRI_EINVAL, "swiglu_rows: bad shape %lld x %lld", (long long)n_rows,
+                (long long)n_cols);
+  for (int64_t ld : lds)
+    if (ld < n_cols)
+      return fail(TRI_EINVAL, "swiglu_rows: row stride %lld below %lld columns", (long long)ld,
+                  (long long)n_cols);
+  if (n_rows * cdiv(std::max<int64_t>(n_cols, 1), kBlock * kRowU) >= ((int64_t)1 << 31))
+    return fail(TRI_EINVAL, "swiglu_rows: grid too large");
+  return TRI_OK;
+}
+
 template <int VEC>
 unsigned grid_for(int64_t n) {
   const int64_t nvec = n / VEC;
@@ -154,4 +262,48 @@ extern "C" int tritium_swiglu_bwd(const void* dy, const void* x, const void* gat
   TRI_DISPATCH_FLOAT(dtype, T,
                      return bwd_impl<T>(dy, x, gate, dx, dgate, n, (hipStream_t)stream));
   return TRI_OK;
+}
+
+extern "C" int tritium_swiglu_rows_fwd(const void* x, const void* gate, void* out, int64_t n_rows,
+                                       int64_t n_cols, int64_t ld_in, int64_t ld_out, int dtype,
+                                       void* stream) {
+  if (int e = check_rows(n_rows, n_cols, {ld_in, ld_out})) return e;
+  if (n_rows == 0 || n_cols == 0) return TRI_OK;
+  hipStream_t st = (hipStream_t)stream;
+  TRI_DISPATCH_FLOAT(dtype, T, {
+    constexpr int VEC = 16 / sizeof(T);
+    if (rows_vec_ok<T>({x, gate, out}, {ld_in, ld_out}, n_cols)) {
+      const int64_t ch = row_chunks<VEC>(n_cols);
+      swiglu_rows_fwd_kernel<T, VEC><<<(unsigned)(n_rows * ch), kBlock, 0, st>>>(
+          (const T*)x, (const T*)gate, (T*)out, n_cols, ld_in, ld_out, ch);
+    } else {
+      const int64_t ch = row_chunks<1>(n_cols);
+      swiglu_rows_fwd_kernel<T, 1><<<(unsigned)(n_rows * ch), kBlock, 0, st>>>(
+          (const T*)x, (const T*)gate, (T*)out, n_cols, ld_in, ld_out, ch);
+    }
+  });
+  return check_launch("swiglu_rows forward");
+}
+
+extern "C" int tritium_swiglu_rows_bwd(const void* dy, const void* x, const void* gate, void* dx,
+                                       void* dgate, int64_t n_rows, int64_t n_cols, int64_t ld_dy,
+                                       int64_t ld_in, int64_t ld_out, int dtype, void* stream) {
+  if (int e = check_rows(n_rows, n_cols, {ld_dy, ld_in, ld_out})) return e;
+  if (n_rows == 0 || n_cols == 0) return TRI_OK;
+  hipStream_t st = (hipStream_t)stream;
+  TRI_DISPATCH_FLOAT(dtype, T, {
+    constexpr int VEC = 16 / sizeof(T);
+    if (rows_vec_ok<T>({dy, x, gate, dx, dgate}, {ld_dy, ld_in, ld_out}, n_cols)) {
+      const int64_t ch = row_chunks<VEC>(n_cols);
+      swiglu_rows_bwd_kernel<T, VEC><<<(unsigned)(n_rows * ch), kBlock, 0, st>>>(
+          (const T*)dy, (const T*)x, (const T*)gate, (T*)dx, (T*)dgate, n_cols, ld_dy, ld_in,
+          ld_out, ch);
+    } else {
+      const int64_t ch = row_chunks<1>(n_cols);
+      swiglu_rows_bwd_kernel<T, 1><<<(unsigned)(n_rows * ch), kBlock, 0, st>>>(
+          (const T*)dy, (const T*)x, (const T*)gate, (T*)dx, (T*)dgate, n_cols, ld_dy, ld_in,
+          ld_out, ch);
+    }
+  });
+  return check_launch("swiglu_rows backward");
 }

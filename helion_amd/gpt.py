@@ -18,11 +18,11 @@ launch, and one pass rounds it back into the working copy.  Activations are bf16
 internally (the kernels' own rule), the residual stream is stored in bf16
 as the reference's residual-RMSNorm does (rmsnorm.py:72-83).
 
-Plain projections (q/k/v fused into one, o, gate/up/down) are library GEMMs
-(``torch.matmul``, hipBLASLt); everything on the kernel layer's hot path is a
-HIP kernel:
-residual-RMSNorm, RoPE, causal attention, SwiGLU, fused linear-cross-entropy
-and AdamW.
+Plain projections (q/k/v fused into one, o, gate/up fused into one, down)
+are library GEMMs (``torch.matmul``, hipBLASLt); everything on the kernel
+layer's hot path is a HIP kernel: residual-RMSNorm, RoPE (applied in place
+to the fused q/k/v output), causal attention, SwiGLU (on the fused gate/up
+output), fused linear-cross-entropy and AdamW.
 
 ``TorchTwin`` computes the same step with PyTorch only (F.rms_norm,
 F.scaled_dot_product_attention, F.silu, F.cross_entropy on materialised
@@ -58,7 +58,7 @@ from .attention import attention
 from .linear_ce import linear_cross_entropy
 from .rmsnorm import residual_rmsnorm
 from .rope import rope_rows
-from .swiglu import swiglu
+from .swiglu import swiglu_rows, swiglu_rows_backward
 
 
 @dataclasses.dataclass(frozen=True)
@@ -149,8 +149,9 @@ def lm_batch(cfg: GPTConfig, tc: TrainConfig, gen: torch.Generator, device,
 
 class _Flat:
     """Views of ``param_shapes`` into one flat tensor, plus each layer's fused
-    q/k/v projection ``blocks.i.wqkv`` [3 * n_heads * head_dim, d_model]
-    (wq, wk, wv are adjacent in the layout, so it is a view too)."""
+    q/k/v projection ``blocks.i.wqkv`` [3 * n_heads * head_dim, d_model] and
+    fused gate/up projection ``blocks.i.w_gu`` [2 * d_ff, d_model] (wq, wk, wv
+    and w_gate, w_up are adjacent in the layout, so these are views too)."""
 
     def __init__(self, cfg: GPTConfig, flat: torch.Tensor):
         self.flat = flat
@@ -167,12 +168,15 @@ class _Flat:
         for i in range(cfg.n_layers):
             o = offsets[f"blocks.{i}.wq"]
             self.views[f"blocks.{i}.wqkv"] = flat[o:o + 3 * qd * cfg.d_model].view(3 * qd, cfg.d_model)
+            o = offsets[f"blocks.{i}.w_gate"]
+            self.views[f"blocks.{i}.w_gu"] = flat[o:o + 2 * cfg.d_ff * cfg.d_model].view(
+                2 * cfg.d_ff, cfg.d_model)
 
     def leaves(self) -> dict[str, torch.Tensor]:
         """The tensors the model differentiates: every parameter except the
-        separate q/k/v views, which the fused wqkv covers."""
+        separate q/k/v and gate/up views, which the fused wqkv and w_gu cover."""
         return {k: v for k, v in self.views.items()
-                if not k.endswith((".wq", ".wk", ".wv"))}
+                if not k.endswith((".wq", ".wk", ".wv", ".w_gate", ".w_up"))}
 
 
 def n_params(cfg: GPTConfig) -> int:
@@ -221,8 +225,8 @@ class HipGPT:
             o = o.transpose(1, 2).reshape(b, s, nh * hd)
             delta = torch.matmul(o, self._w(p + "wo").t())
             normed, residual = residual_rmsnorm(delta, residual, self._w(p + "ffn_norm"), cfg.eps)
-            h = swiglu(torch.matmul(normed, self._w(p + "w_gate").t()),
-                       torch.matmul(normed, self._w(p + "w_up").t()))
+            gu = torch.matmul(normed, self._w(p + "w_gu").t()).view(b * s, 2 * cfg.d_ff)
+            h = _GateUpSwiGLU.apply(gu).view(b, s, cfg.d_ff)
             delta = torch.matmul(h, self._w(p + "w_down").t())
         hidden, _ = residual_rmsnorm(delta, residual, self._w("final_norm"), cfg.eps)
         return linear_cross_entropy(hidden, self._w("embed"), targets)
@@ -337,6 +341,30 @@ class _QKVRope(torch.autograd.Function):
                   inverse=True, in_token_stride=nh * hd, out_token_stride=3 * nh * hd)
         dqkv[:, :, 2].copy_(dv)
         return dqkv, None, None, None
+
+
+class _GateUpSwiGLU(torch.autograd.Function):
+    """SwiGLU of a fused gate/up projection ``[tokens, 2 * d_ff]`` (gate in the
+    first half of each row, up in the second): silu(gate) * up, with the
+    gradients written back into one fused ``[tokens, 2 * d_ff]`` tensor.  The
+    projection is then one GEMM forward and two backward instead of two and
+    four plus the sum of the two input gradients."""
+
+    @staticmethod
+    def forward(ctx, gu):
+        f = gu.shape[1] // 2
+        out = torch.empty((gu.shape[0], f), device=gu.device, dtype=gu.dtype)
+        swiglu_rows(gu[:, :f], gu[:, f:], out)
+        ctx.save_for_backward(gu)
+        return out
+
+    @staticmethod
+    def backward(ctx, dy):
+        (gu,) = ctx.saved_tensors
+        f = gu.shape[1] // 2
+        dgu = torch.empty_like(gu)
+        swiglu_rows_backward(dy.contiguous(), gu[:, :f], gu[:, f:], dgu[:, :f], dgu[:, f:])
+        return dgu
 
 
 GEMM_TABLE = pathlib.Path(__file__).with_name("gemm_table_gfx950.csv")

@@ -93,3 +93,37 @@ def swiglu(x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
     if not requires_autograd(x, gate):
         return _swiglu_forward(x, gate)
     return _SwiGLUAutograd.apply(x, gate)
+
+
+def _check_rows(ts, name):
+    ref = ts[0]
+    for t in ts:
+        if t.dim() != 2 or t.shape != ref.shape or t.dtype != ref.dtype or t.device != ref.device:
+            raise ValueError(f"{name}: operands must be 2-D views of one shape, dtype and device")
+        if t.stride(1) != 1:
+            raise ValueError(f"{name}: rows must have unit column stride")
+
+
+def swiglu_rows(x: torch.Tensor, gate: torch.Tensor, out: torch.Tensor) -> None:
+    """``out = silu(x) * gate`` on 2-D row-strided views (``x`` and ``gate``
+    sharing one row stride), e.g. the two halves of each row of a fused
+    gate/up projection (``tritium_swiglu_rows_fwd``).  Not part of the
+    reference's surface, whose swiglu takes separate tensors; the training
+    harness's fused MLP uses it."""
+    _check_rows((x, gate, out), "swiglu_rows")
+    if x.stride(0) != gate.stride(0):
+        raise ValueError("swiglu_rows: x and gate must share a row stride")
+    _lib.call("tritium_swiglu_rows_fwd", x.data_ptr(), gate.data_ptr(), out.data_ptr(),
+              x.shape[0], x.shape[1], x.stride(0), out.stride(0), _lib.dtype_code(x.dtype),
+              _lib.stream_of(x))
+
+
+def swiglu_rows_backward(dy, x, gate, dx, dgate) -> None:
+    """Gradients of ``swiglu_rows`` into row-strided ``dx`` and ``dgate`` (which
+    share a row stride, as ``x`` and ``gate`` do) -- ``tritium_swiglu_rows_bwd``."""
+    _check_rows((dy, x, gate, dx, dgate), "swiglu_rows_backward")
+    if x.stride(0) != gate.stride(0) or dx.stride(0) != dgate.stride(0):
+        raise ValueError("swiglu_rows_backward: paired operands must share a row stride")
+    _lib.call("tritium_swiglu_rows_bwd", dy.data_ptr(), x.data_ptr(), gate.data_ptr(),
+              dx.data_ptr(), dgate.data_ptr(), x.shape[0], x.shape[1], dy.stride(0),
+              x.stride(0), dx.stride(0), _lib.dtype_code(x.dtype), _lib.stream_of(x))

@@ -101,6 +101,20 @@ int tritium_swiglu_fwd(const void* x, const void* gate, void* out, int64_t n, in
 int tritium_swiglu_bwd(const void* dy, const void* x, const void* gate, void* dx, void* dgate,
                        int64_t n, int dtype, void* stream);
 
+/* SwiGLU over n_rows rows of n_cols elements with row strides (elements): x
+ * and gate rows at ld_in, out rows at ld_out; the backward reads dy rows at
+ * ld_dy and writes dx, dgate rows at ld_out.  Same arithmetic as
+ * tritium_swiglu_fwd/_bwd.  No counterpart in the reference (its swiglu takes
+ * two separate tensors, swiglu.py:61-100): it lets a caller keep the gate and
+ * up projections as the two halves of one fused [tokens, 2 * d_ff] GEMM
+ * output and receive their gradients in the same layout. */
+int tritium_swiglu_rows_fwd(const void* x, const void* gate, void* out, int64_t n_rows,
+                            int64_t n_cols, int64_t ld_in, int64_t ld_out, int dtype,
+                            void* stream);
+int tritium_swiglu_rows_bwd(const void* dy, const void* x, const void* gate, void* dx,
+                            void* dgate, int64_t n_rows, int64_t n_cols, int64_t ld_dy,
+                            int64_t ld_in, int64_t ld_out, int dtype, void* stream);
+
 /* ---- AdamW -----------------------------------------------------------------
  * tritium.adamw_step (tritium/ops/adamw.py:20-54 `_adamw_step_kernel`, host
  * 113-151): in-place update of one parameter tensor (param/grad in `dtype`,

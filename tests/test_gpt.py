@@ -38,8 +38,9 @@ def test_gemm_table_covers_every_projection():
     sigs = {r[1].split("_ld_")[0] for r in rows if r[0].startswith("GemmTunableOp_BFloat16")}
     cfg, tc = gpt.GPTConfig(), gpt.TrainConfig()
     t, d = tc.batch * tc.seq_len, cfg.d_model
+    # fused q/k/v, o, fused gate/up, down
     for out, inp in [(3 * cfg.n_heads * cfg.head_dim, d), (d, cfg.n_heads * cfg.head_dim),
-                     (cfg.d_ff, d), (d, cfg.d_ff)]:
+                     (2 * cfg.d_ff, d), (d, cfg.d_ff)]:
         assert {f"tn_{out}_{t}_{inp}", f"nn_{inp}_{t}_{out}", f"nt_{inp}_{out}_{t}"} <= sigs
 
 

@@ -126,6 +126,43 @@ def test_rope_out_of_range_position_is_nan_not_a_fault():
 
 # ----------------------------------------------------------------- SwiGLU --
 @pytest.mark.parametrize("dtype", DTYPES)
+@pytest.mark.parametrize(("rows", "cols"), [(37, 3072), (5, 4100), (3, 7), (1, 300000)])
+def test_swiglu_rows_matches_swiglu(dtype, rows, cols):
+    # tritium_swiglu_rows_*: x and gate as the two halves of each row of a fused projection,
+    # gradients written back into that layout -- exactly what swiglu does on copies
+    from helion_amd.swiglu import swiglu_rows, swiglu_rows_backward
+    gu = randn((rows, 2 * cols), dtype, 31)
+    dy = randn((rows, cols), dtype, 32)
+    out = torch.empty((rows, cols), device="cuda", dtype=dtype)
+    swiglu_rows(gu[:, :cols], gu[:, cols:], out)
+    x, g = gu[:, :cols].contiguous(), gu[:, cols:].contiguous()
+    dgu = torch.full_like(gu, 3.0)
+    swiglu_rows_backward(dy, gu[:, :cols], gu[:, cols:], dgu[:, :cols], dgu[:, cols:])
+    ex, eg = tritium.swiglu_backward(dy, x, g)
+    pairs = [(out, tritium.swiglu(x, g)), (dgu[:, :cols], ex), (dgu[:, cols:], eg)]
+    if cols % (16 // x.element_size()) == 0:
+        # both sides run the 16-byte-vector path: identical arithmetic
+        assert all(torch.equal(a, e) for a, e in pairs)
+    else:
+        # element-wise rows against the vector path on the copy: same formula, compiled apart
+        rtol, atol = TOL[dtype]
+        for a, e in pairs:
+            assert_close(a, np32(e), rtol, atol)
+
+
+def test_fused_gate_up_matches_two_projections():
+    # the training harness's fused MLP input (gpt._GateUpSwiGLU) against swiglu on two halves
+    from helion_amd.gpt import _GateUpSwiGLU
+    gu = randn((96, 2 * 512), torch.bfloat16, 33)
+    dy = randn((96, 512), torch.bfloat16, 34)
+    a = gu.clone().requires_grad_(True)
+    _GateUpSwiGLU.apply(a).backward(dy)
+    b = gu.clone().requires_grad_(True)
+    tritium.swiglu(b[:, :512], b[:, 512:]).backward(dy)
+    assert torch.equal(a.grad, b.grad)
+
+
+@pytest.mark.parametrize("dtype", DTYPES)
 @pytest.mark.parametrize("n", [1, 7, 16, 1024, 8193, 1 << 20])
 def test_swiglu_forward_backward(dtype, n):
     x = randn((n,), dtype, 1).requires_grad_(True)
