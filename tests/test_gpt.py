@@ -48,6 +48,32 @@ def test_use_gemm_table_without_file_keeps_defaults(tmp_path):
     assert gpt.use_gemm_table(tmp_path / "missing.csv") is False
 
 
+def test_split_k_choice():
+    # the measured split counts at the config-5 shapes (16384 tokens); slices stay >= 512 tokens
+    assert [gpt._split_k(o, i, 16384) for o, i in [(768, 768), (2304, 768), (768, 3072), (6144, 768)]] \
+        == [16, 4, 4, 2]
+    assert gpt._split_k(768, 768, 1024) == 2 and gpt._split_k(768, 768, 1000) == 1
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize(("n_out", "n_in"), [(768, 768), (2304, 768), (96, 40)])
+def test_projection_split_k_gradients(n_out, n_in):
+    # _Proj: the split-K weight gradient is the fp32-accumulated product rounded once
+    g = torch.Generator().manual_seed(n_out)
+    x = torch.randn(4096, n_in, generator=g).bfloat16().cuda().requires_grad_(True)
+    w = (torch.randn(n_out, n_in, generator=g) * 0.02).bfloat16().cuda().requires_grad_(True)
+    dy = torch.randn(4096, n_out, generator=g).bfloat16().cuda()
+    y = gpt._Proj.apply(x, w)
+    y.backward(dy)
+    x32, w32, dy32 = x.detach().double().cpu(), w.detach().double().cpu(), dy.double().cpu()
+    torch.testing.assert_close(y.float().cpu(), (x32 @ w32.t()).to(torch.bfloat16).float(), rtol=2e-2, atol=2e-2)
+    dw_ref = (dy32.t() @ x32)
+    scale = dw_ref.abs().max()
+    assert float((w.grad.double().cpu() - dw_ref).abs().max() / scale) < 8e-3
+    dx_ref = dy32 @ w32
+    assert float((x.grad.double().cpu() - dx_ref).abs().max() / dx_ref.abs().max()) < 8e-3
+
+
 @pytest.mark.gpu
 def test_train_step_matches_torch_twin():
     cfg = gpt.GPTConfig(vocab_size=1024, d_model=256, n_layers=2, n_heads=4, head_dim=64,
