@@ -288,23 +288,16 @@ def lce_leg(torch, tritium, iters: int = 3, warmup: int = 1, n=8192, d=4096, v=1
 def gpt_leg(torch, steps: int = 10, warmup: int = 3):
     """Config 5: the 151.9M-parameter GPT (12 x 768, SwiGLU 3072, vocab 50304, tied
     embeddings) training step at B=16 x T=1024 on the kernel layer: bf16 compute,
-    fp32 master weights, fused AdamW; random-init weights, uniform random tokens.
-    Timed first with the GEMM library's default solutions for the projections,
-    then with the committed solution table (``gpt.use_gemm_table``); the
-    headline figure is the latter.  Runs last: the table stays loaded for the
-    rest of the process."""
+    fp32 master weights, fused AdamW; random-init weights, uniform random tokens."""
     from helion_amd import gpt
 
     cfg, tc = gpt.GPTConfig(), gpt.TrainConfig()
     model = gpt.HipGPT(cfg, tc, gpt.init_params(cfg, tc.seed), torch.device("cuda"))
-    base = gpt.time_steps(model, cfg, tc, steps, warmup)
-    table = gpt.use_gemm_table()
-    res = gpt.time_steps(model, cfg, tc, steps, warmup) if table else base
+    res = gpt.time_steps(model, cfg, tc, steps, warmup)
     del model
     torch.cuda.empty_cache()
     return {"tokens_per_s": round(res["tokens_per_s"], 1), "ms_per_step": round(res["ms_per_step"], 3),
             "mfu_vs_2.5PF": round(res["mfu"], 4), "loss": round(res["loss"], 4),
-            "gemm_table": table, "tokens_per_s_default_gemms": round(base["tokens_per_s"], 1),
             "params": gpt.n_params(cfg), "tokens_per_step": tc.batch * tc.seq_len}
 
 

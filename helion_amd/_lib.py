@@ -98,6 +98,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "tritium_cross_entropy_bwd": (
         _I32, [_P, _P, _P, _I32, _P, _P, _I64, _I64, _F64, _I32, _P],
     ),
+    "tritium_adamw_step_mixed": (
+        _I32,
+        [_P, _I32, _I64, _F32, _F32, _F32, _F32, _F32, _F64, _F64, _I32, _P],
+    ),
     "tritium_linear_ce_grad_logits": (
         _I32,
         [_P, _P, _P, _P, _P, _I32, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P],

@@ -9,6 +9,9 @@ bias corrections 133-134).
 builds a small int64 descriptor table (pointers, sizes, dtype, chunk offsets),
 copies it to the device through pinned memory without a host sync, and caches
 it while the tensors' storage stays the same.
+
+``adamw_step_mixed`` is new too: fp32 params and moments, 16-bit gradients
+read as they are, and the 16-bit working weights written in the same pass.
 """
 
 from __future__ import annotations
@@ -208,4 +211,75 @@ def adamw_step_multi(
         bc1,
         bc2,
         _lib.stream_of(params[0]),
+    )
+
+
+def adamw_step_mixed(
+    params: Sequence[torch.Tensor],
+    grads: Sequence[torch.Tensor],
+    exp_avgs: Sequence[torch.Tensor],
+    exp_avg_sqs: Sequence[torch.Tensor],
+    shadows: Sequence[torch.Tensor] | None = None,
+    *,
+    lr: float,
+    beta1: float = 0.9,
+    beta2: float = 0.999,
+    eps: float = 1e-8,
+    weight_decay: float = 0.01,
+    step: int = 1,
+) -> None:
+    """Mixed-precision AdamW over a parameter list in one launch
+    (``tritium_adamw_step_mixed``): fp32 ``params`` and moments updated from
+    16-bit ``grads`` read as they are, and, when ``shadows`` is given, each
+    updated parameter rounded into the matching 16-bit tensor in the same
+    pass.  The arithmetic is :func:`adamw_step`'s on the widened gradient.
+    Not part of the reference's surface (its ``adamw_step`` wants grad and
+    param of one dtype, adamw.py:86-90): a training step with 16-bit working
+    weights over fp32 masters uses it instead of widening every gradient and
+    re-rounding every weight in two extra passes."""
+    n = len(params)
+    lists = [grads, exp_avgs, exp_avg_sqs] + ([shadows] if shadows is not None else [])
+    if any(len(x) != n for x in lists):
+        raise ValueError("params, grads, exp_avgs, exp_avg_sqs (and shadows) must have the same length.")
+    if n == 0:
+        return
+    gdt = grads[0].dtype
+    if gdt not in (torch.float16, torch.bfloat16):
+        raise ValueError(f"grads must be float16 or bfloat16, got {gdt}.")
+    device = params[0].device
+    chunk = int(_lib.lib().tritium_adamw_chunk_elements())
+    rows: list[int] = []
+    first = 0
+    for i in range(n):
+        p, g, m, v = params[i], grads[i], exp_avgs[i], exp_avg_sqs[i]
+        sh = shadows[i] if shadows is not None else None
+        for name, t, dt in (("param", p, torch.float32), ("grad", g, gdt), ("exp_avg", m, torch.float32),
+                            ("exp_avg_sq", v, torch.float32)) + ((("shadow", sh, gdt),) if sh is not None else ()):
+            check_cuda_tensor(name, t)
+            if t.dtype != dt:
+                raise ValueError(f"{name} must have dtype {dt}, got {t.dtype}.")
+            if t.shape != p.shape:
+                raise ValueError(f"Shape mismatch: {name} has shape {tuple(t.shape)}, "
+                                 f"param has shape {tuple(p.shape)}.")
+            if t.device != device:
+                raise ValueError(f"Device mismatch: {name} is on {t.device}, expected {device}.")
+            check_contiguous(name, t, "for tritium.adamw_step_mixed")
+        numel = p.numel()
+        if numel == 0:
+            continue
+        ptrs = [p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr()]
+        sp = sh.data_ptr() if sh is not None else 0
+        aligned = all(x % 16 == 0 for x in ptrs + ([sp] if sp else []))
+        rows.extend(ptrs)
+        rows.extend((numel, int(aligned), first, sp))
+        first += -(-numel // chunk)
+    if not rows:
+        return
+    host = torch.tensor(rows, dtype=torch.int64).pin_memory()
+    table = host.to(device, non_blocking=True)
+    bc1, bc2 = _bias_corrections(beta1, beta2, step)
+    _lib.call(
+        "tritium_adamw_step_mixed", table.data_ptr(), len(rows) // 8, first, float(lr),
+        float(beta1), float(beta2), float(eps), float(weight_decay), bc1, bc2,
+        _lib.dtype_code(gdt), _lib.stream_of(params[0]),
     )

@@ -137,6 +137,88 @@ adamw_multi_kernel(const int64_t* __restrict__ table, int n_tensors, Hyper h) {
   }
 }
 
+// Mixed precision: fp32 parameters and moments, 16-bit gradients (read as
+// they are), and optionally a 16-bit copy of each updated parameter (the
+// working weights of a mixed-precision model) written in the same pass --
+// 28 bytes per parameter, where widening the gradients first and rounding
+// the weights afterwards would add 12.  Eight elements per lane step: two
+// 16-byte vectors of each fp32 stream, one of each 16-bit stream.
+template <typename TG>
+__device__ __forceinline__ void adam_chunk_mixed(float* __restrict__ p, const TG* __restrict__ g,
+                                                 float* __restrict__ m, float* __restrict__ v,
+                                                 TG* __restrict__ shadow, int64_t n, int64_t start,
+                                                 bool vec_ok, const Hyper& h) {
+  static_assert(sizeof(TG) == 2, "16-bit gradients");
+  const float lr_wd = h.lr * h.weight_decay;
+  const float step_size = h.lr / h.bc1;
+  const int64_t end = min(start + kChunk, n);
+  int64_t tail = start;
+  if (vec_ok) {
+    constexpr int NV = (int)(kChunk / 8 / kBlock);
+    const int64_t vec_end = start + ((end - start) / 8) * 8;
+    typedef float F4[4];
+    float pv[NV][8], gv[NV][8], mv[NV][8], vv[NV][8];
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * 8;
+      if (e < vec_end) {
+        unpack<float>(ld16_nt(p + e), *reinterpret_cast<F4*>(&pv[u][0]));
+        unpack<float>(ld16_nt(p + e + 4), *reinterpret_cast<F4*>(&pv[u][4]));
+        unpack<TG>(ld16_nt(g + e), gv[u]);
+        unpack<float>(ld16_nt(m + e), *reinterpret_cast<F4*>(&mv[u][0]));
+        unpack<float>(ld16_nt(m + e + 4), *reinterpret_cast<F4*>(&mv[u][4]));
+        unpack<float>(ld16_nt(v + e), *reinterpret_cast<F4*>(&vv[u][0]));
+        unpack<float>(ld16_nt(v + e + 4), *reinterpret_cast<F4*>(&vv[u][4]));
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * 8;
+      if (e < vec_end) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) adam_update(pv[u][i], gv[u][i], mv[u][i], vv[u][i], h, lr_wd, step_size);
+        st16_nt(m + e, pack<float>(*reinterpret_cast<F4*>(&mv[u][0])));
+        st16_nt(m + e + 4, pack<float>(*reinterpret_cast<F4*>(&mv[u][4])));
+        st16_nt(v + e, pack<float>(*reinterpret_cast<F4*>(&vv[u][0])));
+        st16_nt(v + e + 4, pack<float>(*reinterpret_cast<F4*>(&vv[u][4])));
+        st16_nt(p + e, pack<float>(*reinterpret_cast<F4*>(&pv[u][0])));
+        st16_nt(p + e + 4, pack<float>(*reinterpret_cast<F4*>(&pv[u][4])));
+        if (shadow != nullptr) st16_nt(shadow + e, pack<TG>(pv[u]));
+      }
+    }
+    tail = vec_end;
+  }
+  for (int64_t e = tail + threadIdx.x; e < end; e += kBlock) {
+    float pp = p[e], mm = m[e], vv2 = v[e];
+    adam_update(pp, to_f32(g[e]), mm, vv2, h, lr_wd, step_size);
+    m[e] = mm;
+    v[e] = vv2;
+    p[e] = pp;
+    if (shadow != nullptr) shadow[e] = from_f32<TG>(pp);
+  }
+}
+
+// Table rows of kMixedWords int64: [param, grad, exp_avg, exp_avg_sq, numel,
+// flags (bit 0: every pointer 16-byte aligned), first_chunk, shadow or 0].
+constexpr int kMixedWords = 8;
+
+template <typename TG>
+__global__ void __launch_bounds__(kBlock)
+adamw_mixed_kernel(const int64_t* __restrict__ table, int n_tensors, Hyper h) {
+  const int64_t b = blockIdx.x;
+  int lo = 0, hi = n_tensors - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (table[mid * kMixedWords + 6] <= b) lo = mid; else hi = mid - 1;
+  }
+  const int64_t* d = table + lo * kMixedWords;
+  const int64_t n = d[4];
+  const int64_t start = (b - d[6]) * kChunk;
+  if (start >= n) return;
+  adam_chunk_mixed<TG>((float*)d[0], (const TG*)d[1], (float*)d[2], (float*)d[3], (TG*)d[7], n,
+                       start, (d[5] & 1) != 0, h);
+}
+
 Hyper make_hyper(float lr, float beta1, float beta2, float eps, float wd, double bc1, double bc2) {
   return Hyper{lr, beta1, beta2, eps, wd, (float)bc1, (float)bc2};
 }
@@ -174,4 +256,23 @@ extern "C" int tritium_adamw_step_multi(const int64_t* table, int n_tensors, int
   const Hyper h = make_hyper(lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2);
   adamw_multi_kernel<<<(unsigned)total_chunks, kBlock, 0, (hipStream_t)stream>>>(table, n_tensors, h);
   return check_launch("adamw multi-tensor step");
+}
+
+extern "C" int tritium_adamw_step_mixed(const int64_t* table, int n_tensors, int64_t total_chunks,
+                                        float lr, float beta1, float beta2, float eps,
+                                        float weight_decay, double bias_correction1,
+                                        double bias_correction2, int grad_dtype, void* stream) {
+  if (n_tensors < 0 || total_chunks < 0) return fail(TRI_EINVAL, "adamw mixed: bad table size");
+  if (n_tensors == 0 || total_chunks == 0) return TRI_OK;
+  if (total_chunks >= ((int64_t)1 << 31)) return fail(TRI_EINVAL, "adamw mixed: too many chunks");
+  const Hyper h = make_hyper(lr, beta1, beta2, eps, weight_decay, bias_correction1, bias_correction2);
+  hipStream_t st = (hipStream_t)stream;
+  if (grad_dtype == kBF16) {
+    adamw_mixed_kernel<bf16_t><<<(unsigned)total_chunks, kBlock, 0, st>>>(table, n_tensors, h);
+  } else if (grad_dtype == kF16) {
+    adamw_mixed_kernel<f16_t><<<(unsigned)total_chunks, kBlock, 0, st>>>(table, n_tensors, h);
+  } else {
+    return fail(TRI_EINVAL, "adamw mixed: gradients must be 16-bit (dtype code %d)", grad_dtype);
+  }
+  return check_launch("adamw mixed-precision step");
 }

@@ -11,10 +11,10 @@ d_model 768, 12 heads x 64, MLP 3072, vocab 50304, tied embeddings
 Precision boundary.  The optimizer owns fp32 master weights in one flat
 buffer; each step runs on a bf16 working copy (one flat buffer, the model's
 parameters are views into it).  The bf16 gradients come back from
-``torch.autograd.grad`` (nothing accumulated, so no gradient zeroing) and are
-widened straight into the matching views of one flat fp32 buffer by a
-multi-tensor copy; ``adamw_step`` updates the whole flat master buffer in one
-launch, and one pass rounds it back into the working copy.  Activations are bf16 throughout; every op computes in fp32
+``torch.autograd.grad`` (nothing accumulated, so no gradient zeroing) and
+``adamw_step_mixed`` consumes them as they are: one launch updates the fp32
+masters and moments and rounds each updated master into its bf16 working
+weight.  Activations are bf16 throughout; every op computes in fp32
 internally (the kernels' own rule), the residual stream is stored in bf16
 as the reference's residual-RMSNorm does (rmsnorm.py:72-83).
 
@@ -31,14 +31,6 @@ logits, torch.optim.AdamW) from identical initial weights and data, for the
 loss-curve parity check; its attention and norms run in fp32.
 
 Run ``python -m helion_amd.gpt --steps 200`` on a GPU for the parity report.
-
-GEMM solutions.  The library's default solution for the weight-gradient
-projections (K = 16384 tokens, few output tiles) is a poor fit;
-``gemm_table_gfx950.csv`` beside this file records, per projection shape of
-this model at the benchmark batch, the fastest hipBLASLt/rocBLAS solution
-PyTorch's TunableOp measured on an MI355X.  ``use_gemm_table`` loads it with
-tuning switched off, so no search runs at training time;
-``python -m helion_amd.gpt --tune-gemm-table PATH`` regenerates it.
 """
 
 from __future__ import annotations
@@ -47,14 +39,12 @@ import argparse
 import dataclasses
 import json
 import math
-import os
-import pathlib
 import time
 
 import torch
 import torch.nn.functional as F
 
-from .adamw import adamw_step
+from .adamw import adamw_step_mixed
 from .attention import attention
 from .linear_ce import linear_cross_entropy
 from .rmsnorm import residual_rmsnorm
@@ -194,14 +184,18 @@ class HipGPT:
         for name, t in init.items():
             self.master.views[name].copy_(t)
         self.work = _Flat(cfg, self.master.flat.to(torch.bfloat16))
-        self.grad32 = _Flat(cfg, torch.zeros(n, device=device, dtype=torch.float32))
         self.exp_avg = torch.zeros(n, device=device, dtype=torch.float32)
         self.exp_avg_sq = torch.zeros(n, device=device, dtype=torch.float32)
         leaves = self.work.leaves()
         for p in leaves.values():
             p.requires_grad_(True)
         self._params = list(leaves.values())
-        self._grad32 = [self.grad32.views[name] for name in leaves]
+        m, v = _Flat(cfg, self.exp_avg), _Flat(cfg, self.exp_avg_sq)
+        self._master = [self.master.views[name] for name in leaves]
+        self._m = [m.views[name] for name in leaves]
+        self._v = [v.views[name] for name in leaves]
+        self._shadow = [p.detach() for p in self._params]
+        self._last_grads: tuple[torch.Tensor, ...] = ()
         self.cos, self.sin = rope_tables(cfg, device)
         self.step_count = 0
 
@@ -237,17 +231,19 @@ class HipGPT:
         tc = self.tc
         loss = self.loss(tokens, targets)
         grads = torch.autograd.grad(loss, self._params)
-        torch._foreach_copy_(self._grad32, grads)  # bf16 -> fp32, grouped launches
         self.step_count += 1
-        adamw_step(self.master.flat, self.grad32.flat, self.exp_avg, self.exp_avg_sq, lr=tc.lr,
-                   beta1=tc.beta1, beta2=tc.beta2, eps=tc.eps, weight_decay=tc.weight_decay,
-                   step=self.step_count)
-        with torch.no_grad():
-            self.work.flat.copy_(self.master.flat)
+        # fp32 masters from the bf16 gradients, and the bf16 working weights rounded
+        # from the updated masters, in one pass
+        adamw_step_mixed(self._master, grads, self._m, self._v, self._shadow, lr=tc.lr,
+                         beta1=tc.beta1, beta2=tc.beta2, eps=tc.eps,
+                         weight_decay=tc.weight_decay, step=self.step_count)
+        self._last_grads = grads
         return loss.detach()
 
     def grad_norm(self) -> float:
-        return float(self.grad32.flat.norm())
+        """L2 norm of the last step's gradients (fp32 accumulation)."""
+        norms = torch.stack([torch.linalg.vector_norm(g.float()) for g in self._last_grads])
+        return float(torch.linalg.vector_norm(norms))
 
 
 class TorchTwin:
@@ -420,43 +416,6 @@ class _GateUpSwiGLU(torch.autograd.Function):
         return dgu
 
 
-GEMM_TABLE = pathlib.Path(__file__).with_name("gemm_table_gfx950.csv")
-
-
-def use_gemm_table(path: str | os.PathLike = GEMM_TABLE) -> bool:
-    """Make torch's GEMMs use the solutions recorded in ``path`` (PyTorch
-    TunableOp with tuning off; shapes not in the table keep the library's
-    default choice).  Process-wide: it changes which library kernel computes
-    every later ``torch.mm`` of a recorded shape.  Returns False, leaving the
-    default choices in force, when TunableOp rejects the file (its validators
-    -- torch, HIP, hipBLASLt and rocBLAS versions, GPU arch -- differ from the
-    running ones) or the file is missing."""
-    from torch.cuda import tunable
-
-    if not pathlib.Path(path).is_file():
-        return False
-    tunable.enable(True)
-    tunable.tuning_enable(False)
-    tunable.set_filename(str(path))
-    ok = bool(tunable.read_file(str(path)))
-    if not ok:
-        tunable.enable(False)
-    return ok
-
-
-def tune_gemm_table(path: str | os.PathLike, cfg: GPTConfig, tc: TrainConfig, device) -> None:
-    """Search the GEMM solutions of one training step of this model and have
-    TunableOp record them in ``path`` (it writes the file when the process
-    exits, since tuning stays enabled)."""
-    from torch.cuda import tunable
-
-    tunable.enable(True)
-    tunable.tuning_enable(True)
-    tunable.set_filename(str(path))
-    model = HipGPT(cfg, tc, init_params(cfg, tc.seed), device)
-    time_steps(model, cfg, tc, steps=1, warmup=1)
-
-
 def time_steps(model: HipGPT, cfg: GPTConfig, tc: TrainConfig, steps: int, warmup: int,
                seed: int = 0) -> dict:
     """Tokens per second of ``model.train_step`` (batches pre-generated)."""
@@ -501,15 +460,10 @@ def main(argv=None) -> int:
     ap.add_argument("--out", default="")
     ap.add_argument("--layers", type=int, default=12)
     ap.add_argument("--batch", type=int, default=16)
-    ap.add_argument("--tune-gemm-table", default="", metavar="PATH",
-                    help="search the projections' GEMM solutions and write them to PATH")
     args = ap.parse_args(argv)
     cfg = GPTConfig(n_layers=args.layers)
     tc = TrainConfig(batch=args.batch)
     dev = torch.device("cuda")
-    if args.tune_gemm_table:
-        tune_gemm_table(args.tune_gemm_table, cfg, tc, dev)
-        return 0
     res = parity(args.steps, cfg, tc, dev)
     summary = {k: v for k, v in res.items() if not isinstance(v, list)}
     summary["loss_first_last_hip"] = [res["loss_hip"][0], res["loss_hip"][-1]]

@@ -138,6 +138,22 @@ int tritium_adamw_step_multi(const int64_t* table, int n_tensors, int64_t total_
                              float lr, float beta1, float beta2, float eps, float weight_decay,
                              double bias_correction1, double bias_correction2, void* stream);
 
+/* Mixed-precision multi-tensor AdamW, one launch: fp32 params and moments,
+ * 16-bit gradients (grad_dtype 1 = fp16, 2 = bf16) read as they are, and an
+ * optional 16-bit copy of each updated parameter written in the same pass.
+ * Arithmetic per element as tritium_adamw_step on the widened gradient.
+ * table: device int64 rows of 8 words [param, grad, exp_avg, exp_avg_sq,
+ * numel, flags (bit 0: all pointers 16-byte aligned), first_chunk, shadow or
+ * 0], first_chunk the prefix sum of ceil(numel / tritium_adamw_chunk_elements()).
+ * No counterpart in the reference (whose adamw_step requires grad and param
+ * of one dtype, adamw.py:86-90): it serves a training step whose weights are
+ * 16-bit copies of fp32 masters, which would otherwise widen every gradient
+ * and re-round every weight in two extra passes. */
+int tritium_adamw_step_mixed(const int64_t* table, int n_tensors, int64_t total_chunks, float lr,
+                             float beta1, float beta2, float eps, float weight_decay,
+                             double bias_correction1, double bias_correction2, int grad_dtype,
+                             void* stream);
+
 /* ---- attention -------------------------------------------------------------
  * Forward of tritium.attention (tritium/ops/attention.py:31-141
  * `_attention_forward_kernel`, 144-217 decode kernel, host 284-396).

@@ -27,27 +27,6 @@ def test_init_is_seeded_and_shaped():
     assert abs(float(a["embed"].std()) - 0.02) < 0.005
 
 
-def test_gemm_table_covers_every_projection():
-    # TunableOp rows: op signature, "<ta><tb>_<m>_<n>_<k>_ld_...", solution, ms.  Column-major
-    # naming: y = x W^T is tn_<out>_<tokens>_<in>, dX = dY W is nn_<in>_<tokens>_<out>,
-    # dW = dY^T X is nt_<in>_<out>_<tokens>
-    rows = [line.strip().split(",") for line in gpt.GEMM_TABLE.read_text().splitlines() if line.strip()]
-    validators = {r[1]: r[2] for r in rows if r[0] == "Validator"}
-    assert validators["GCN_ARCH_NAME"].startswith("gfx950")
-    assert {"PT_VERSION", "HIPBLASLT_VERSION", "ROCBLAS_VERSION"} <= set(validators)
-    sigs = {r[1].split("_ld_")[0] for r in rows if r[0].startswith("GemmTunableOp_BFloat16")}
-    cfg, tc = gpt.GPTConfig(), gpt.TrainConfig()
-    t, d = tc.batch * tc.seq_len, cfg.d_model
-    # fused q/k/v, o, fused gate/up, down
-    for out, inp in [(3 * cfg.n_heads * cfg.head_dim, d), (d, cfg.n_heads * cfg.head_dim),
-                     (2 * cfg.d_ff, d), (d, cfg.d_ff)]:
-        assert {f"tn_{out}_{t}_{inp}", f"nn_{inp}_{t}_{out}", f"nt_{inp}_{out}_{t}"} <= sigs
-
-
-def test_use_gemm_table_without_file_keeps_defaults(tmp_path):
-    assert gpt.use_gemm_table(tmp_path / "missing.csv") is False
-
-
 def test_split_k_choice():
     # the measured split counts at the config-5 shapes (16384 tokens); slices stay >= 512 tokens
     assert [gpt._split_k(o, i, 16384) for o, i in [(768, 768), (2304, 768), (768, 3072), (6144, 768)]] \

@@ -232,6 +232,27 @@ def test_adamw_multi_matches_single_and_oracle():
     assert_close(params[1], ep, 1e-5, 1e-5)
 
 
+@pytest.mark.parametrize("gdtype", [torch.bfloat16, torch.float16])
+def test_adamw_mixed_matches_fp32_step(gdtype):
+    # tritium_adamw_step_mixed: same update as adamw_step on the widened gradient; the
+    # shadow is the updated fp32 param rounded once; ragged sizes take the element path
+    from helion_amd.adamw import adamw_step_mixed
+    shapes = [(4096,), (33, 7), (1,), (768, 768), (5000,)]
+    ps = [randn(s, torch.float32, 40 + i, scale=0.02) for i, s in enumerate(shapes)]
+    gs = [randn(s, gdtype, 50 + i, scale=1e-2) for i, s in enumerate(shapes)]
+    ms = [randn(s, torch.float32, 60 + i, scale=1e-3) for i, s in enumerate(shapes)]
+    vs = [randn(s, torch.float32, 70 + i, scale=1e-3).abs() for i, s in enumerate(shapes)]
+    sh = [torch.zeros(s, device="cuda", dtype=gdtype) for s in shapes]
+    ref = [(p.clone(), g.float(), m.clone(), v.clone()) for p, g, m, v in zip(ps, gs, ms, vs)]
+    kw = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, step=10)
+    adamw_step_mixed(ps, gs, ms, vs, sh, **kw)
+    for (rp, rg, rm, rv), p, m, v, s_ in zip(ref, ps, ms, vs, sh):
+        tritium.adamw_step(rp, rg, rm, rv, **kw)
+        for a, e in ((p, rp), (m, rm), (v, rv)):
+            torch.testing.assert_close(a, e, rtol=1e-6, atol=1e-9)
+        assert torch.equal(s_, p.to(gdtype))
+
+
 def test_adamw_step1_closed_form():
     # from zero moments, step 1: p1 = p*(1 - lr*wd) - lr * g / (|g| + eps)
     n = 4096
