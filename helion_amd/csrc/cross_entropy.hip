@@ -197,6 +197,7 @@ extern "C" int tritium_cross_entropy_fwd(const void* logits, const void* target,
                                          float* loss, float* lse, float* nll, int64_t n_rows,
                                          int64_t vocab, int dtype, void* stream) {
   if (n_rows < 0 || vocab <= 0) return fail(TRI_EINVAL, "cross_entropy: bad sizes");
+  if (n_rows >= ((int64_t)1 << 31)) return fail(TRI_EINVAL, "cross_entropy: too many rows");
   hipStream_t st = (hipStream_t)stream;
   if (n_rows == 0) return TRI_OK;
   const int vec_ok = rows_vec_ok(logits, vocab, dtype);
