@@ -21,6 +21,7 @@ Differences:
 
 from __future__ import annotations
 
+import ctypes
 from typing import Any
 
 import torch
@@ -90,11 +91,13 @@ def _rows_aligned(t: torch.Tensor) -> bool:
             and all((st * es) % 16 == 0 for st in t.stride()[:-1]))
 
 
-def _strides(*ts: torch.Tensor) -> torch.Tensor:
+def _strides(*ts: torch.Tensor):
+    """(batch, head, seq) strides of each tensor as a host int64 array (read by
+    the entry point before it returns)."""
     vals: list[int] = []
     for t in ts:
         vals.extend(t.stride()[:3])
-    return torch.tensor(vals, dtype=torch.int64)
+    return (ctypes.c_int64 * len(vals))(*vals)
 
 
 def _attention_forward(q, k, v, is_causal: bool):
@@ -108,6 +111,19 @@ def _attention_forward(q, k, v, is_causal: bool):
     if q_len == 0 or batch == 0:
         return o, lse
     strides = _strides(q, k, v, o)
+    if (q_len == 1 and not is_causal and kv_len > 0 and q.dtype != torch.float32
+            and head_dim in (64, 128) and n_heads // n_kv_heads <= 8
+            and all(_rows_aligned(t) for t in (q, k, v))):
+        # decode: one query row per head against a K/V cache, split over the keys
+        ws_bytes = _lib.lib().tritium_attention_decode_workspace_size(
+            batch, n_heads, n_kv_heads, kv_len, head_dim)
+        ws = torch.empty((max(ws_bytes, 4) // 4,), device=q.device, dtype=torch.float32)
+        _lib.call(
+            "tritium_attention_decode", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+            lse.data_ptr(), ws.data_ptr(), ws_bytes, batch, n_heads, n_kv_heads, kv_len,
+            head_dim, strides, _lib.dtype_code(q.dtype), _lib.stream_of(q),
+        )
+        return o, lse
     _lib.call(
         "tritium_attention_fwd",
         q.data_ptr(),
@@ -121,7 +137,7 @@ def _attention_forward(q, k, v, is_causal: bool):
         q_len,
         kv_len,
         head_dim,
-        strides.data_ptr(),
+        strides,
         int(bool(is_causal)),
         _lib.dtype_code(q.dtype),
         _lib.stream_of(q),
@@ -158,7 +174,7 @@ def _attention_backward_impl(do, q, k, v, o, lse, is_causal: bool):
         q_len,
         kv_len,
         head_dim,
-        strides.data_ptr(),
+        strides,
         int(bool(is_causal)),
         _lib.dtype_code(q.dtype),
         _lib.stream_of(q),

@@ -1816,6 +1816,230 @@ attn_bwd_dq_v2(BwdArgs a) {
   }
 }
 
+// ------------------------------------------------------ decode (q_len 1) --
+// One query row per (batch, head) against a K/V cache: memory-bound, and a
+// grid of B * H one-row tiles leaves most of the GPU idle.  A workgroup owns
+// one (batch, kv head) and one chunk of the key sequence and serves every
+// query head of the GQA group from the same K/V reads; D / 8 lanes hold one
+// 16-byte slice each of a key row, so a wavefront walks 64 / (D / 8) keys
+// per step.  Each lane group keeps an online softmax state (m, l, o over its
+// slice of dims, log2 units, rescaled only when a score exceeds m by more
+// than 8) per query head; the groups of a wavefront merge through cross-lane
+// shuffles, the wavefronts through LDS, and each workgroup writes its chunk's
+// unnormalised (m, l, o) per head to a workspace that attn_decode_combine
+// merges over the chunks (o = sum o_c 2^(m_c - M) / sum l_c 2^(m_c - M)).
+constexpr int kDecWaves = 4;
+constexpr int kDecMinChunk = 256;        // keys per chunk at least
+constexpr int kDecTargetBlocks = 2048;   // workgroups to aim for
+constexpr int kDecUnroll = 4;            // key rows in flight per lane
+constexpr int kDecMaxSplits = 256;       // chunks per (batch, head) at most
+
+struct DecArgs {
+  const void* q; const void* k; const void* v; void* o; float* lse; float* part;
+  int64_t sq_b, sq_h, sk_b, sk_h, sk_s, sv_b, sv_h, sv_s, so_b, so_h;
+  int B, H, Hkv, Tkv, n_splits, chunk;
+  float sl2;  // scale * log2(e)
+};
+
+int dec_splits(int64_t B, int64_t Hkv, int64_t Tkv) {
+  const int64_t want = cdiv(kDecTargetBlocks, std::max<int64_t>(1, B * Hkv));
+  const int64_t most = std::min<int64_t>(kDecMaxSplits, std::max<int64_t>(1, cdiv(Tkv, kDecMinChunk)));
+  return (int)std::max<int64_t>(1, std::min(want, most));
+}
+
+// Sum over each aligned group of N lanes (N = 8 or 16, inside one 16-lane
+// DPP row) with DPP moves: two quad permutations (xor 1, xor 2), then the
+// half-row and row mirrors -- four VALU adds, where __shfl_xor would make
+// four dependent LDS permute round trips.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                               0xF, 0xF, false));
+}
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+  static_assert(N == 8 || N == 16, "lane group of 8 or 16");
+  v += dpp_mov<0xB1>(v);   // quad_perm [1, 0, 3, 2]
+  v += dpp_mov<0x4E>(v);   // quad_perm [2, 3, 0, 1]
+  v += dpp_mov<0x141>(v);  // row_half_mirror: lane i of 8 <- lane 7 - i
+  if constexpr (N == 16) v += dpp_mov<0x140>(v);  // row_mirror: lane i of 16 <- lane 15 - i
+  return v;
+}
+
+// (m, l, o) <- merge of two online-softmax states over disjoint keys
+template <int N>
+__device__ __forceinline__ void dec_merge(float& m, float& l, float (&o)[N], float m2, float l2,
+                                          const float (&o2)[N]) {
+  const float mx = fmaxf(m, m2);
+  if (mx == -INFINITY) return;  // both empty
+  const float c1 = fast_exp2(m - mx), c2 = fast_exp2(m2 - mx);
+  l = l * c1 + l2 * c2;
+#pragma unroll
+  for (int i = 0; i < N; ++i) o[i] = o[i] * c1 + o2[i] * c2;
+  m = mx;
+}
+
+template <typename T, int D, int G>
+__global__ void __launch_bounds__(64 * kDecWaves)
+attn_decode_kernel(DecArgs a) {
+  constexpr int LPK = D / 8;     // lanes per key row
+  constexpr int KPW = 64 / LPK;  // keys per wavefront step
+  __shared__ float sm[kDecWaves][G], sl[kDecWaves][G], so[kDecWaves][G][D];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int sub = lane / LPK, part = lane % LPK;
+  int bid = blockIdx.x;
+  const int split = bid % a.n_splits;
+  bid /= a.n_splits;
+  const int hk = bid % a.Hkv, b = bid / a.Hkv;
+  const int group = a.H / a.Hkv;
+  const int kv0 = split * a.chunk;
+  const int kv1 = min(a.Tkv, kv0 + a.chunk);
+
+  float qv[G][8], m[G], l[G], o[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = -INFINITY;
+    l[g] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[g][i] = 0.f;
+    if (g < group) {
+      float f[8];
+      unpack<T>(ld16((const T*)a.q + b * a.sq_b + (int64_t)(hk * group + g) * a.sq_h + part * 8), f);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qv[g][i] = f[i] * a.sl2;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 8; ++i) qv[g][i] = 0.f;
+    }
+  }
+  const T* kb = (const T*)a.k + b * a.sk_b + hk * a.sk_h + part * 8;
+  const T* vb = (const T*)a.v + b * a.sv_b + hk * a.sv_h + part * 8;
+  // kDecUnroll key rows per lane are loaded before any is used (memory-level
+  // parallelism for a latency-bound stream); the LPK lanes of a key row share
+  // its bounds, so the shuffles below only combine lanes active together
+  constexpr int kStride = kDecWaves * KPW;
+  for (int kv = kv0 + wave * KPW + sub; kv < kv1; kv += kDecUnroll * kStride) {
+    u32x4 kr[kDecUnroll], vr[kDecUnroll];
+#pragma unroll
+    for (int u = 0; u < kDecUnroll; ++u) {
+      const int ku = kv + u * kStride;
+      if (ku < kv1) {
+        kr[u] = ld16_nt(kb + (int64_t)ku * a.sk_s);
+        vr[u] = ld16_nt(vb + (int64_t)ku * a.sv_s);
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kDecUnroll; ++u) {
+      if (kv + u * kStride >= kv1) break;
+      float kf[8], vf[8];
+      unpack<T>(kr[u], kf);
+      unpack<T>(vr[u], vf);
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) s = fmaf(qv[g][i], kf[i], s);
+        s = group_sum<LPK>(s);
+        if (s > m[g] + 8.f) {
+          const float c = fast_exp2(m[g] - s);
+          l[g] *= c;
+#pragma unroll
+          for (int i = 0; i < 8; ++i) o[g][i] *= c;
+          m[g] = s;
+        }
+        const float p = fast_exp2(s - m[g]);
+        l[g] += p;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) o[g][i] = fmaf(p, vf[i], o[g][i]);
+      }
+    }
+  }
+  // merge the KPW key slots of the wavefront (lanes part, part + LPK, ...)
+#pragma unroll
+  for (int off = LPK; off < kWave; off <<= 1) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float o2[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) o2[i] = __shfl_xor(o[g][i], off, kWave);
+      const float m2 = __shfl_xor(m[g], off, kWave), l2 = __shfl_xor(l[g], off, kWave);
+      dec_merge<8>(m[g], l[g], o[g], m2, l2, o2);
+    }
+  }
+  if (sub == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (part == 0) {
+        sm[wave][g] = m[g];
+        sl[wave][g] = l[g];
+      }
+#pragma unroll
+      for (int i = 0; i < 8; ++i) so[wave][g][part * 8 + i] = o[g][i];
+    }
+  }
+  __syncthreads();
+  // merge the wavefronts; thread d < D owns dimension d of every head
+  for (int g = 0; g < group && g < G; ++g) {
+    if (threadIdx.x < D) {
+      float mm = sm[0][g], ll = sl[0][g], oo[1] = {so[0][g][threadIdx.x]};
+#pragma unroll
+      for (int w = 1; w < kDecWaves; ++w) {
+        const float o2[1] = {so[w][g][threadIdx.x]};
+        dec_merge<1>(mm, ll, oo, sm[w][g], sl[w][g], o2);
+      }
+      float* dst = a.part + (((int64_t)b * a.H + hk * group + g) * a.n_splits + split) * (D + 2);
+      dst[2 + threadIdx.x] = oo[0];
+      if (threadIdx.x == 0) {
+        dst[0] = mm;
+        dst[1] = ll;
+      }
+    }
+  }
+}
+
+// o[b, h] and lse[b, h] from the chunks' (m, l, o): the chunk maxima and
+// weights 2^(m_c - M) are formed by strided threads and reduced through LDS
+// (independent loads, not a serial walk over the chunks); thread d then sums
+// dimension d of every chunk's o with the weights, loads unrolled.
+template <typename T, int D>
+__global__ void __launch_bounds__(D)
+attn_decode_combine(DecArgs a) {
+  constexpr int NW = D / kWave;
+  __shared__ float wgt[kDecMaxSplits];
+  __shared__ float red[2][NW];
+  const int bh = blockIdx.x;
+  const int b = bh / a.H, h = bh % a.H;
+  const int lane = threadIdx.x & (kWave - 1), wave = threadIdx.x / kWave;
+  const float* src = a.part + (int64_t)bh * a.n_splits * (D + 2);
+  float mx = -INFINITY;
+  for (int c = threadIdx.x; c < a.n_splits; c += D) mx = fmaxf(mx, src[c * (D + 2)]);
+  mx = wave_max(mx);
+  if (lane == 0) red[0][wave] = mx;
+  __syncthreads();
+  mx = red[0][0];
+#pragma unroll
+  for (int w = 1; w < NW; ++w) mx = fmaxf(mx, red[0][w]);
+  float ls = 0.f;
+  for (int c = threadIdx.x; c < a.n_splits; c += D) {
+    const float mc = src[c * (D + 2)];
+    const float w = mc == -INFINITY ? 0.f : fast_exp2(mc - mx);  // a chunk without keys
+    wgt[c] = w;
+    ls += src[c * (D + 2) + 1] * w;
+  }
+  ls = wave_sum(ls);
+  if (lane == 0) red[1][wave] = ls;
+  __syncthreads();
+  float l = 0.f;
+#pragma unroll
+  for (int w = 0; w < NW; ++w) l += red[1][w];
+  float od = 0.f;
+#pragma unroll 8
+  for (int c = 0; c < a.n_splits; ++c) od += src[c * (D + 2) + 2 + threadIdx.x] * wgt[c];
+  T* orow = (T*)a.o + b * a.so_b + h * a.so_h;
+  orow[threadIdx.x] = from_f32<T>(l > 0.f ? od / l : 0.f);
+  if (threadIdx.x == 0) a.lse[bh] = (mx + log2f(l)) * kLn2;
+}
+
 // --------------------------------------------------------------- SIMT path --
 // One wavefront per row; lane i owns head-dim entries i, i+64, ...
 constexpr int kSimtMaxPerLane = 16;  // head_dim <= 1024
@@ -2220,4 +2444,68 @@ extern "C" int tritium_attention_bwd(const void* dout, const void* q, const void
   hipStream_t st = (hipStream_t)stream;
   TRI_DISPATCH_FLOAT(dtype, T, return bwd_impl<T>(a, D, mfma, st));
   return TRI_OK;
+}
+
+extern "C" size_t tritium_attention_decode_workspace_size(int64_t B, int64_t H, int64_t Hkv,
+                                                          int64_t Tkv, int64_t D) {
+  if (B <= 0 || H <= 0 || Hkv <= 0 || Tkv <= 0 || D <= 0) return 0;
+  return (size_t)B * H * dec_splits(B, Hkv, Tkv) * (D + 2) * sizeof(float);
+}
+
+extern "C" int tritium_attention_decode(const void* q, const void* k, const void* v, void* o,
+                                        float* lse, void* workspace, size_t workspace_bytes,
+                                        int64_t B, int64_t H, int64_t Hkv, int64_t Tkv, int64_t D,
+                                        const int64_t* strides, int dtype, void* stream) {
+  if (int e = check_dims(B, H, Hkv, 1, Tkv, D)) return e;
+  if (B == 0) return TRI_OK;
+  if (Tkv < 1) return fail(TRI_EINVAL, "attention decode: needs at least one key");
+  if (dtype == kF32 || (D != 64 && D != 128))
+    return fail(TRI_EINVAL, "attention decode: 16-bit inputs with head_dim 64 or 128 only");
+  const int64_t group = H / Hkv;
+  if (group > 8) return fail(TRI_EINVAL, "attention decode: at most 8 query heads per kv head");
+  DecArgs a;
+  a.q = q; a.k = k; a.v = v; a.o = o; a.lse = lse; a.part = (float*)workspace;
+  a.sq_b = strides[0]; a.sq_h = strides[1];
+  a.sk_b = strides[3]; a.sk_h = strides[4]; a.sk_s = strides[5];
+  a.sv_b = strides[6]; a.sv_h = strides[7]; a.sv_s = strides[8];
+  a.so_b = strides[9]; a.so_h = strides[10];
+  if (!aligned16(q) || a.sq_b % 8 || a.sq_h % 8 || !rows_aligned(k, a.sk_b, a.sk_h, a.sk_s) ||
+      !rows_aligned(v, a.sv_b, a.sv_h, a.sv_s))
+    return fail(TRI_EINVAL, "attention decode: q, k, v rows must be 16-byte aligned");
+  a.B = (int)B; a.H = (int)H; a.Hkv = (int)Hkv; a.Tkv = (int)Tkv;
+  a.n_splits = dec_splits(B, Hkv, Tkv);
+  const int step = kDecWaves * (64 / (int)(D / 8));
+  a.chunk = (int)(cdiv(cdiv(Tkv, a.n_splits), step) * step);
+  a.sl2 = (float)(1.0 / sqrt((double)D)) * kLog2e;
+  const size_t need = (size_t)B * H * a.n_splits * (D + 2) * sizeof(float);
+  if (workspace == nullptr || workspace_bytes < need)
+    return fail(TRI_EINVAL, "attention decode: workspace of %zu bytes needed", need);
+  const int64_t blocks = B * Hkv * a.n_splits;
+  if (blocks >= ((int64_t)1 << 31)) return fail(TRI_EINVAL, "attention decode: grid too large");
+  hipStream_t st = (hipStream_t)stream;
+#define TRI_DEC_LAUNCH(TT, DD, GG) \
+  attn_decode_kernel<TT, DD, GG><<<(unsigned)blocks, 64 * kDecWaves, 0, st>>>(a)
+#define TRI_DEC_GROUPS(TT, DD)                        \
+  do {                                                \
+    if (group == 1) TRI_DEC_LAUNCH(TT, DD, 1);        \
+    else if (group == 2) TRI_DEC_LAUNCH(TT, DD, 2);   \
+    else if (group <= 4) TRI_DEC_LAUNCH(TT, DD, 4);   \
+    else TRI_DEC_LAUNCH(TT, DD, 8);                   \
+  } while (0)
+  if (dtype == kBF16) {
+    if (D == 64) TRI_DEC_GROUPS(bf16_t, 64); else TRI_DEC_GROUPS(bf16_t, 128);
+  } else {
+    if (D == 64) TRI_DEC_GROUPS(f16_t, 64); else TRI_DEC_GROUPS(f16_t, 128);
+  }
+#undef TRI_DEC_GROUPS
+#undef TRI_DEC_LAUNCH
+  if (int e = check_launch("attention decode")) return e;
+  if (dtype == kBF16) {
+    if (D == 64) attn_decode_combine<bf16_t, 64><<<(unsigned)(B * H), 64, 0, st>>>(a);
+    else attn_decode_combine<bf16_t, 128><<<(unsigned)(B * H), 128, 0, st>>>(a);
+  } else {
+    if (D == 64) attn_decode_combine<f16_t, 64><<<(unsigned)(B * H), 64, 0, st>>>(a);
+    else attn_decode_combine<f16_t, 128><<<(unsigned)(B * H), 128, 0, st>>>(a);
+  }
+  return check_launch("attention decode combine");
 }

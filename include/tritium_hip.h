@@ -178,6 +178,22 @@ int tritium_attention_bwd(const void* dout, const void* q, const void* k, const 
                           int64_t Tkv, int64_t D, const int64_t* strides, int causal, int dtype,
                           void* stream);
 
+/* The attention forward for one query row per (batch, head) against a K/V
+ * cache (the reference's decode branch, attention.py:144-217, 354-396:
+ * q_len = 1, no causal mask, strided cache slices): same outputs as
+ * tritium_attention_fwd (o in q's layout, natural-log lse [B, H]) for 16-bit
+ * inputs with head_dim 64 or 128 and at most 8 query heads per kv head.
+ * The key sequence is split into chunks over extra workgroups whose partial
+ * (m, l, o) go to `workspace` (tritium_attention_decode_workspace_size bytes)
+ * and are merged by a second kernel.  strides as for tritium_attention_fwd
+ * (the query and output sequence strides are unused). */
+size_t tritium_attention_decode_workspace_size(int64_t B, int64_t H, int64_t Hkv, int64_t Tkv,
+                                               int64_t D);
+int tritium_attention_decode(const void* q, const void* k, const void* v, void* o, float* lse,
+                             void* workspace, size_t workspace_bytes, int64_t B, int64_t H,
+                             int64_t Hkv, int64_t Tkv, int64_t D, const int64_t* strides,
+                             int dtype, void* stream);
+
 /* ---- fused linear + cross-entropy ---------------------------------------------
  * Forward of tritium.linear_cross_entropy (tritium/ops/cross_entropy.py:134-293
  * kernels, host `_linear_cross_entropy_forward` 563-640, autograd 663-705),

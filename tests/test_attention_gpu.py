@@ -86,6 +86,42 @@ def test_attention_kv_cache_single_query(dtype):
     assert_close(o, eo, tol, tol)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("head_dim", [64, 128])
+@pytest.mark.parametrize(("b", "h", "hkv", "kv_len"),
+                         [(1, 4, 4, 1), (2, 8, 4, 7), (1, 6, 2, 300), (2, 16, 4, 5000),
+                          (1, 8, 1, 2500), (3, 32, 32, 1030)])
+def test_attention_decode_split_kv(dtype, head_dim, b, h, hkv, kv_len):
+    # q_len 1 against strided cache slices takes the split-KV decode kernels (groups of 1,
+    # 2, 3 (padded to 4), 4 and 8 query heads per kv head); o and lse against the oracle
+    print(f"[decode] {dtype} d={head_dim} b={b} h={h} hkv={hkv} L={kv_len}", flush=True)
+    cache_k = randn((b, hkv, kv_len + 40, head_dim), dtype, 3)
+    cache_v = randn((b, hkv, kv_len + 40, head_dim), dtype, 4)
+    k, v = cache_k[:, :, :kv_len], cache_v[:, :, :kv_len]
+    q = randn((b, 1, h, head_dim), dtype, 5).transpose(1, 2)  # the module's layout
+    o = tritium.attention(q, k, v, is_causal=False)
+    eo, e_lse = oracle.attention.forward(np32(q), np32(k), np32(v), False)
+    assert_close(o, eo, 2e-2, 2e-2, "o")
+    from helion_amd.attention import _attention_forward
+    _, lse = _attention_forward(q, k, v, False)
+    assert_close(lse, e_lse, 1e-4, 1e-4, "lse")
+
+
+def test_attention_decode_grads_through_general_backward():
+    # the decode forward's (o, lse) feed the general backward kernels
+    b, h, hkv, kv_len, d = 2, 8, 2, 333, 128
+    q = randn((b, h, 1, d), torch.bfloat16, 7).requires_grad_(True)
+    k = randn((b, hkv, kv_len, d), torch.bfloat16, 8).requires_grad_(True)
+    v = randn((b, hkv, kv_len, d), torch.bfloat16, 9).requires_grad_(True)
+    do = randn((b, h, 1, d), torch.bfloat16, 10)
+    tritium.attention(q, k, v, is_causal=False).backward(do)
+    eo, lse = oracle.attention.forward(np32(q), np32(k), np32(v), False)
+    edq, edk, edv = oracle.attention.backward(np32(do), np32(q), np32(k), np32(v), lse, False)
+    assert_close(q.grad, edq, 2e-2, 2e-2, "dq")
+    assert_close(k.grad, edk, 2e-2, 2e-2, "dk")
+    assert_close(v.grad, edv, 2e-2, 2e-2, "dv")
+
+
 def test_attention_large_head_bf16_t1024():
     _check(torch.bfloat16, 1, 2, 2, 1024, 1024, 128, True, seed=13)
 
