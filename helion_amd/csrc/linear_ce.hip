@@ -24,6 +24,14 @@
 //   dH (+)= G W_c      NT GEMM with B = W^T (made once per backward);
 //   dW_c = G^T H       NT GEMM with B = H^T, the full token reduction inside
 //                      one GEMM, stored once in the weight dtype.
+// Backward from kept probabilities (16-bit inputs, when the caller can hold an
+// [N, V] 16-bit buffer from the forward to the backward): the forward epilogue
+// also stores p~ = exp(logit - m_b) in fp16 (the terms of its sum, m_b the
+// max over the logit's 256-row vocab tile, so p~ is in [0, 1]); the backward
+// turns that buffer into G in place with one streaming pass
+// (lce_g_from_probs) instead of recomputing the logits GEMM, and dH, dW are
+// the same two GEMMs.  The target entry, where p - 1 would cancel, is taken
+// from the fp32 target logit instead of p~.
 // All reductions are in a fixed order: results are bitwise reproducible.
 #include <math.h>
 
@@ -64,6 +72,54 @@ __device__ __forceinline__ T from_bits16(uint16_t b) {
   return __builtin_bit_cast(T, b);
 }
 
+// Four values rounded to the 16-bit type S, packed in 8 bytes.
+template <typename S>
+__device__ __forceinline__ uint2 pack4(const float* v) {
+  uint2 pk;
+  pk.x = (uint32_t)bits16(from_f32<S>(v[0])) | ((uint32_t)bits16(from_f32<S>(v[1])) << 16);
+  pk.y = (uint32_t)bits16(from_f32<S>(v[2])) | ((uint32_t)bits16(from_f32<S>(v[3])) << 16);
+  return pk;
+}
+
+// A 16-bit tile of 256 vocab rows x BN tokens, held by the lanes as 4
+// consecutive vocab rows of one token, leaves for a token-major [N, ld]
+// buffer through the (idle) LDS as whole 512-byte token rows; stored
+// directly, every store instruction would touch 32 token rows.  Staging
+// layout: the 8-byte slot s of token row r sits at slot s ^ (r & 63), so the
+// 32 tokens of a half-wavefront write distinct banks.
+__device__ __forceinline__ void stage_put4(char* tile, int tok, int vl, uint2 pk) {
+  *reinterpret_cast<uint2*>(tile + tok * 512 + (((vl >> 2) ^ (tok & 63)) << 3)) = pk;
+}
+
+// Copy the staged tile out: 32 lanes per token row, 16 bytes (8 vocab
+// entries) each; rows at or past N and vocab entries at or past Vc are not
+// written.  The caller has passed a barrier since the last stage_put4.
+template <int THREADS, int BN>
+__device__ __forceinline__ void stage_out(const char* tile, uint16_t* out, int64_t ld, int64_t n0,
+                                          int64_t v0, int64_t N, int64_t Vc) {
+  constexpr int ITER = BN * 32 / THREADS;
+#pragma unroll
+  for (int it = 0; it < ITER; ++it) {
+    const int idx = it * THREADS + threadIdx.x;
+    const int row = idx >> 5, c = idx & 31;
+    const int64_t n = n0 + row;
+    const int64_t vb = v0 + 8 * c;
+    // slots 2c and 2c + 1 sit in one 16-byte chunk, swapped for odd rows
+    u32x4 v = *reinterpret_cast<const u32x4*>(tile + row * 512 + ((((2 * c) ^ (row & 63)) & ~1) << 3));
+    if (row & 1) v = __builtin_shufflevector(v, v, 2, 3, 0, 1);
+    if (n >= N || vb >= Vc) continue;
+    uint16_t* dst = out + n * ld + vb;
+    if (vb + 8 <= Vc) {
+      st16(dst, v);
+    } else {
+      const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (vb + e < Vc) dst[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+    }
+  }
+}
+
 // ------------------------------------------------------------- forward ----
 struct FwdArgs {
   const void* hidden;  // [N, D]
@@ -72,7 +128,8 @@ struct FwdArgs {
   float* pmax;         // [tiles_v, N]
   float* psum;         // [tiles_v, N]
   float* tlogit;       // [N]
-  int64_t N, D, V, ld;
+  uint16_t* probs;     // [N, ld_p] fp16 p~, or null
+  int64_t N, D, V, ld, ld_p;
   int tiles_v, tiles_n;
 };
 
@@ -93,6 +150,8 @@ lce_fwd_kernel(FwdArgs a) {
   const int wm = wave / C::WN, wn = wave % C::WN;
   const int64_t v0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
   const TT* target = (const TT*)a.target;
+  constexpr bool kKeep = sizeof(T) == 2 && C::BM * 2 == 512 && C::BM * C::BN * 2 <= C::SMEM_BYTES;
+  const bool keep = kKeep && a.probs != nullptr;
 
   float mx[C::NT];
 #pragma unroll
@@ -125,8 +184,18 @@ lce_fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int i = 0; i < C::MT; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (v0 + acc_row<C>(wm, i, r, g) < a.V) s += fast_exp2(acc.t[i][j][r] * kLog2e - ms);
+      for (int rr = 0; rr < 4; ++rr) {
+        float e4[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * rr + e;
+          e4[e] = v0 + acc_row<C>(wm, i, r, g) < a.V ? fast_exp2(acc.t[i][j][r] * kLog2e - ms) : 0.f;
+          s += e4[e];
+        }
+        if constexpr (kKeep) {
+          if (keep) stage_put4(smem, col, acc_row<C>(wm, i, 4 * rr, g), pack4<f16_t>(e4));
+        }
+      }
     s += __shfl_xor(s, 32, 64);
     if (g == 0) red[wm][col] = s;
     // the target logit: written by the single lane that holds its row
@@ -156,6 +225,10 @@ lce_fwd_kernel(FwdArgs a) {
         a.psum[(int64_t)tm * a.N + n] = s;
       }
     }
+  }
+  // the staged p~ tile is complete since the barrier above
+  if constexpr (kKeep) {
+    if (keep) stage_out<C::THREADS, C::BN>(smem, a.probs, a.ld_p, n0, v0, a.N, a.V);
   }
 }
 
@@ -334,12 +407,7 @@ lce_g_kernel(GArgs a) {
             if (vb + e < a.Vc) gt[(vb + e) * a.ld_gt + n] = from_f32<T>(gv[e]);
         }
         if constexpr (kStage) {
-          if (gm != nullptr) {
-            uint2 pk;
-            pk.x = (uint32_t)bits16(from_f32<T>(gv[0])) | ((uint32_t)bits16(from_f32<T>(gv[1])) << 16);
-            pk.y = (uint32_t)bits16(from_f32<T>(gv[2])) | ((uint32_t)bits16(from_f32<T>(gv[3])) << 16);
-            *reinterpret_cast<uint2*>(tile + tok * 512 + (((vl >> 2) ^ (tok & 63)) << 3)) = pk;
-          }
+          if (gm != nullptr) stage_put4(tile, tok, vl, pack4<T>(gv));
         } else if (gm != nullptr && nvalid) {
           T* dst = gm + n * a.ld_g + vb;
           if (vb + 4 <= a.Vc) {
@@ -356,28 +424,43 @@ lce_g_kernel(GArgs a) {
   if constexpr (kStage) {
     if (gm == nullptr) return;
     __syncthreads();
-    // 32 lanes per 512-byte token row, 16 bytes (8 vocab entries) each
-    constexpr int ITER = C::BN * 32 / C::THREADS;
+    stage_out<C::THREADS, C::BN>(tile, (uint16_t*)gm, a.ld_g, n0, v0, a.N, a.Vc);
+  }
+}
+
+// G in place over the fp16 p~ buffer the forward kept (see the top of this
+// file): G[n, v] = (p~[n, v] * exp(m_b - lse[n]) - [v == target[n]]) * coef,
+// coef = grad_out / n_valid (0 for ignored rows), stored in T over the same
+// 2-byte entries; the target entry uses exp(target logit - lse) instead of p~.
+// Entries past V in the row padding are rewritten with values nobody reads.
+constexpr int64_t kProbsChunk = 256 * 8 * 2;  // entries of one row per block
+
+template <typename T, typename TT>
+__global__ void __launch_bounds__(256)
+lce_g_from_probs(const float* __restrict__ grad_out, const float* __restrict__ n_valid,
+                 const TT* __restrict__ target, int64_t ignore_index, const float* __restrict__ lse,
+                 const float* __restrict__ pmax, const float* __restrict__ tlogit,
+                 uint16_t* __restrict__ buf, int64_t ld, int64_t N, int64_t V,
+                 int64_t chunks_per_row, int tile_rows) {
+  static_assert(sizeof(T) == 2, "16-bit G");
+  const int64_t row = blockIdx.x / chunks_per_row;
+  const int64_t c0 = (blockIdx.x - row * chunks_per_row) * kProbsChunk;
+  const int64_t c1 = min(c0 + kProbsChunk, V);
+  const int64_t t = load_target(target, row);
+  const float coef = t == ignore_index ? 0.f : grad_out[0] / n_valid[0];
+  const float l2 = lse[row] * kLog2e;
+  uint16_t* p = buf + row * ld;
+  for (int64_t e = c0 + (int64_t)threadIdx.x * 8; e < c1; e += 256 * 8) {
+    // 8 entries never straddle a vocab tile (tile_rows is a multiple of 8)
+    const float f = fast_exp2(pmax[(e / tile_rows) * N + row] * kLog2e - l2);
+    float gv[8];
+    unpack<f16_t>(ld16_nt(p + e), gv);
 #pragma unroll
-    for (int it = 0; it < ITER; ++it) {
-      const int idx = it * C::THREADS + threadIdx.x;
-      const int row = idx >> 5, c = idx & 31;
-      const int64_t n = n0 + row;
-      const int64_t vb = v0 + 8 * c;
-      // slots 2c and 2c + 1 sit in one 16-byte chunk, swapped for odd rows
-      u32x4 v = *reinterpret_cast<const u32x4*>(tile + row * 512 + ((((2 * c) ^ (row & 63)) & ~1) << 3));
-      if (row & 1) v = __builtin_shufflevector(v, v, 2, 3, 0, 1);
-      if (n >= a.N || vb >= a.Vc) continue;
-      T* dst = gm + n * a.ld_g + vb;
-      if (vb + 8 <= a.Vc) {
-        st16(dst, v);
-      } else {
-        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          if (vb + e < a.Vc) dst[e] = from_bits16<T>((uint16_t)(w[e >> 1] >> (16 * (e & 1))));
-      }
+    for (int i = 0; i < 8; ++i) {
+      const float pr = e + i == t ? fast_exp2(tlogit[row] * kLog2e - l2) : gv[i] * f;
+      gv[i] = (pr - (e + i == t ? 1.f : 0.f)) * coef;
     }
+    st16_nt(p + e, pack<T>(gv));
   }
 }
 
@@ -535,7 +618,7 @@ int transpose(const void* in, int64_t ld_in, void* out, int64_t ld_out, int64_t 
 template <typename T, typename TT>
 int fwd_impl(const void* hidden, const void* weight, const void* target, int64_t ignore_index,
              float* loss, float* lse, float* n_valid, void* ws, size_t ws_bytes, int64_t N,
-             int64_t D, int64_t V, hipStream_t st) {
+             int64_t D, int64_t V, void* probs, int64_t ld_p, hipStream_t st) {
   typedef CfgT<T> C;
   const FwdLayout L = fwd_layout(N, V, C::BM, C::BN);
   if (ws_bytes < L.total) return fail(TRI_EINVAL, "linear_ce forward: workspace too small");
@@ -545,7 +628,8 @@ int fwd_impl(const void* hidden, const void* weight, const void* target, int64_t
   a.pmax = (float*)(w + L.pmax);
   a.psum = (float*)(w + L.psum);
   a.tlogit = (float*)(w + L.tlogit);
-  a.N = N; a.D = D; a.V = V; a.ld = D;
+  a.probs = (uint16_t*)probs;
+  a.N = N; a.D = D; a.V = V; a.ld = D; a.ld_p = ld_p;
   a.tiles_v = L.tiles_v; a.tiles_n = L.tiles_n;
   // a target outside [0, V) that is not ignore_index leaves NaN here (-> NaN loss);
   // a fill kernel rather than a memset node, so the call can be graph-captured
@@ -677,8 +761,60 @@ extern "C" int tritium_linear_ce_fwd(const void* hidden, const void* weight, con
   TRI_DISPATCH_TARGET(target_kind, TT,
     TRI_DISPATCH_FLOAT(dtype, T,
       return fwd_impl<T, TT>(hidden, weight, target, ignore_index, loss, lse, n_valid, workspace,
-                             workspace_bytes, n_rows, hidden_size, vocab, st)));
+                             workspace_bytes, n_rows, hidden_size, vocab, nullptr, 0, st)));
   return TRI_OK;
+}
+
+extern "C" int tritium_linear_ce_fwd_probs(const void* hidden, const void* weight,
+                                           const void* target, int target_kind,
+                                           int64_t ignore_index, float* loss, float* lse,
+                                           float* n_valid, void* probs, int64_t ld_probs,
+                                           void* workspace, size_t workspace_bytes,
+                                           int64_t n_rows, int64_t hidden_size, int64_t vocab,
+                                           int dtype, void* stream) {
+  if (int e = check_sizes(n_rows, hidden_size, vocab, dtype)) return e;
+  if (dtype == kF32) return fail(TRI_EINVAL, "linear_ce fwd_probs: 16-bit inputs only");
+  if (ld_probs < vocab || ld_probs % 8 != 0)
+    return fail(TRI_EINVAL, "linear_ce fwd_probs: ld_probs %lld must be >= vocab and a multiple of 8",
+                (long long)ld_probs);
+  if (n_rows == 0) return TRI_OK;
+  if (!aligned16(hidden) || !aligned16(weight) || !aligned16(probs))
+    return fail(TRI_EINVAL, "linear_ce: hidden, weight and probs must be 16-byte aligned");
+  hipStream_t st = (hipStream_t)stream;
+  TRI_DISPATCH_TARGET(target_kind, TT,
+    TRI_DISPATCH_FLOAT(dtype, T,
+      return fwd_impl<T, TT>(hidden, weight, target, ignore_index, loss, lse, n_valid, workspace,
+                             workspace_bytes, n_rows, hidden_size, vocab, probs, ld_probs, st)));
+  return TRI_OK;
+}
+
+extern "C" int tritium_linear_ce_grad_from_probs(const float* grad_out, const float* n_valid,
+                                                 const void* target, int target_kind,
+                                                 int64_t ignore_index, const float* lse,
+                                                 const void* fwd_workspace,
+                                                 size_t fwd_workspace_bytes, void* probs,
+                                                 int64_t ld_probs, int64_t n_rows, int64_t vocab,
+                                                 int dtype, void* stream) {
+  if (n_rows < 0 || vocab <= 0) return fail(TRI_EINVAL, "linear_ce grad_from_probs: bad sizes");
+  if (dtype == kF32) return fail(TRI_EINVAL, "linear_ce grad_from_probs: 16-bit inputs only");
+  if (ld_probs < vocab || ld_probs % 8 != 0 || !aligned16(probs))
+    return fail(TRI_EINVAL, "linear_ce grad_from_probs: probs must be 16-byte aligned, ld_probs >= vocab and a multiple of 8");
+  if (n_rows == 0) return TRI_OK;
+  typedef CfgT<bf16_t> C;
+  const FwdLayout L = fwd_layout(n_rows, vocab, C::BM, C::BN);
+  if (fwd_workspace_bytes < L.total)
+    return fail(TRI_EINVAL, "linear_ce grad_from_probs: forward workspace too small");
+  const int64_t chunks = cdiv(vocab, kProbsChunk);
+  if (n_rows * chunks > 0x7fffffffLL) return fail(TRI_EINVAL, "linear_ce grad_from_probs: grid too large");
+  const char* w = (const char*)fwd_workspace;
+  hipStream_t st = (hipStream_t)stream;
+  TRI_DISPATCH_TARGET(target_kind, TT,
+    TRI_DISPATCH_FLOAT(dtype, T, if constexpr (sizeof(T) == 2) {
+      lce_g_from_probs<T, TT><<<(unsigned)(n_rows * chunks), 256, 0, st>>>(
+          grad_out, n_valid, (const TT*)target, ignore_index, lse, (const float*)(w + L.pmax),
+          (const float*)(w + L.tlogit), (uint16_t*)probs, ld_probs, n_rows, vocab, chunks, C::BM);
+    }));
+  return check_launch("linear_ce gradient from kept probabilities");
 }
 
 extern "C" size_t tritium_linear_ce_bwd_workspace_size(int64_t n_rows, int64_t hidden_size,

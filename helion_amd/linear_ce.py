@@ -105,20 +105,42 @@ def _target_kind(target: torch.Tensor) -> int:
     return 1 if target.dtype == torch.int32 else 2
 
 
-def _linear_cross_entropy_forward(hidden, weight, target, ignore_index: int = IGNORE_INDEX):
-    """cross_entropy.py:563-640: returns ``(loss, logsumexp)``."""
+def _keep_fits(n_rows: int, vocab_size: int, dtype: torch.dtype) -> bool:
+    """Whether the autograd forward keeps the [n_rows, vocab] fp16 buffer for
+    the backward: 16-bit inputs whose buffer fits the gradient-tile budget
+    (the backward's G tiles need the same memory anyway)."""
+    ld = -(-vocab_size // 8) * 8
+    return dtype in (torch.float16, torch.bfloat16) and 0 < n_rows * ld * 2 <= _G_CHUNK_BYTES
+
+
+def _linear_cross_entropy_forward(hidden, weight, target, ignore_index: int = IGNORE_INDEX,
+                                  keep: bool = False):
+    """cross_entropy.py:563-640: returns ``(loss, logsumexp)``; with ``keep``
+    returns ``(loss, logsumexp, kept)``, ``kept`` the state
+    ``tritium_linear_ce_fwd_probs`` leaves for :func:`_backward_from_probs`."""
     n_rows, hidden_size, vocab_size = _check_linear_cross_entropy_inputs(hidden, weight, target)
     dev = hidden.device
     loss = torch.zeros((), device=dev, dtype=torch.float32)
     lse = torch.empty((n_rows,), device=dev, dtype=torch.float32)
     if n_rows == 0:
-        return loss, lse
+        return (loss, lse, None) if keep else (loss, lse)
     h2 = _kernel_operand(hidden.reshape(n_rows, hidden_size))
     w2 = _kernel_operand(weight)
     ws_bytes = _lib.lib().tritium_linear_ce_fwd_workspace_size(
         n_rows, vocab_size, _lib.dtype_code(hidden.dtype)
     )
     ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
+    if keep:
+        ld_p = -(-vocab_size // 8) * 8
+        probs = torch.empty((n_rows, ld_p), device=dev, dtype=torch.float16)
+        n_valid = torch.empty((), device=dev, dtype=torch.float32)
+        _lib.call(
+            "tritium_linear_ce_fwd_probs", h2.data_ptr(), w2.data_ptr(), target.data_ptr(),
+            _target_kind(target), int(ignore_index), loss.data_ptr(), lse.data_ptr(),
+            n_valid.data_ptr(), probs.data_ptr(), ld_p, ws.data_ptr(), ws.numel(), n_rows,
+            h2.shape[-1], vocab_size, _lib.dtype_code(hidden.dtype), _lib.stream_of(hidden),
+        )
+        return loss, lse, (probs, ws, n_valid)
     _lib.call(
         "tritium_linear_ce_fwd",
         h2.data_ptr(),
@@ -209,6 +231,35 @@ def _backward(grad_out, hidden_2d, weight, target_1d, lse, need_dh, need_dw, ign
             torch.mm(gc.t(), h2, out=dw[v0:v0 + vc])
     if dh32 is not None:
         dh = dh32.to(hidden_2d.dtype)
+    if dp != hidden_size:
+        dh = dh[:, :hidden_size].contiguous() if dh is not None else None
+        dw = dw[:, :hidden_size].contiguous() if dw is not None else None
+    return dh, dw
+
+
+def _backward_from_probs(grad_out, hidden_2d, weight, target_1d, lse, kept, need_dh, need_dw,
+                         ignore_index):
+    """Backward from the buffer the forward kept (``tritium_linear_ce_fwd_probs``):
+    ``tritium_linear_ce_grad_from_probs`` turns it into G in place with one
+    streaming pass (no logits recompute), then dH = G W and dW = G^T H are the
+    same library GEMMs as in :func:`_backward`.  Consumes ``kept``."""
+    probs, ws, n_valid = kept
+    n_rows, hidden_size = hidden_2d.shape
+    vocab_size = weight.shape[0]
+    dev = hidden_2d.device
+    g = grad_out.detach().to(device=dev, dtype=torch.float32).reshape(())
+    _lib.call(
+        "tritium_linear_ce_grad_from_probs", g.data_ptr(), n_valid.data_ptr(),
+        target_1d.data_ptr(), _target_kind(target_1d), int(ignore_index), lse.data_ptr(),
+        ws.data_ptr(), ws.numel(), probs.data_ptr(), probs.shape[1], n_rows, vocab_size,
+        _lib.dtype_code(weight.dtype), _lib.stream_of(hidden_2d),
+    )
+    gc = probs.view(weight.dtype)[:, :vocab_size]
+    h2 = _kernel_operand(hidden_2d)
+    w2 = _kernel_operand(weight)
+    dh = torch.mm(gc, w2) if need_dh else None
+    dw = torch.mm(gc.t(), h2) if need_dw else None
+    dp = h2.shape[-1]
     if dp != hidden_size:
         dh = dh[:, :hidden_size].contiguous() if dh is not None else None
         dw = dw[:, :hidden_size].contiguous() if dw is not None else None
@@ -309,10 +360,17 @@ class _LinearCrossEntropyAutograd(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx: Any, hidden, weight, target, ignore_index):
-        loss, lse = _linear_cross_entropy_forward(hidden, weight, target, ignore_index)
+        n = target.numel()
+        ctx.kept = None
+        if _keep_fits(n, weight.shape[0], hidden.dtype):
+            # one [n, vocab] fp16 buffer held until the backward, which then
+            # skips the logits recompute
+            loss, lse, ctx.kept = _linear_cross_entropy_forward(hidden, weight, target,
+                                                                ignore_index, keep=True)
+        else:
+            loss, lse = _linear_cross_entropy_forward(hidden, weight, target, ignore_index)
         ctx.hidden_shape = tuple(hidden.shape)
         ctx.ignore_index = ignore_index
-        n = target.numel()
         ctx.save_for_backward(hidden.view(n, hidden.shape[-1]), weight, target.view(n), lse)
         return loss
 
@@ -326,8 +384,15 @@ class _LinearCrossEntropyAutograd(torch.autograd.Function):
             dh = torch.zeros(ctx.hidden_shape, device=hidden_2d.device, dtype=hidden_2d.dtype)
             return (dh if need_dh else None), (torch.zeros_like(weight) if need_dw else None), \
                 None, None
-        dh, dw = _backward(grad_outputs[0], hidden_2d, weight, target_1d, lse, need_dh, need_dw,
-                           ctx.ignore_index)
+        kept, ctx.kept = ctx.kept, None
+        if kept is not None:
+            # the buffer becomes G in place: a second backward (retain_graph)
+            # takes the recompute path below
+            dh, dw = _backward_from_probs(grad_outputs[0], hidden_2d, weight, target_1d, lse,
+                                          kept, need_dh, need_dw, ctx.ignore_index)
+        else:
+            dh, dw = _backward(grad_outputs[0], hidden_2d, weight, target_1d, lse, need_dh,
+                               need_dw, ctx.ignore_index)
         if dh is not None:
             dh = dh.view(ctx.hidden_shape)
         return dh, dw, None, None
@@ -341,7 +406,11 @@ def linear_cross_entropy(
     ignore_index: int = IGNORE_INDEX,
 ) -> torch.Tensor:
     """Mean cross-entropy of ``hidden @ weight.T`` against ``target`` without
-    materialising the logits (cross_entropy.py:716-725)."""
+    materialising the logits (cross_entropy.py:716-725).  Under autograd with
+    16-bit inputs, when an [n_rows, vocab] 16-bit buffer fits the 4 GiB
+    gradient-tile budget, the forward keeps the fp16 terms exp(logit - tile
+    max) for the backward (the backward's gradient of the logits needs that
+    much memory anyway), so the backward skips the logits recompute."""
     if not requires_autograd(hidden, weight):
         loss, _ = _linear_cross_entropy_forward(hidden, weight, target, ignore_index)
         return loss

@@ -167,3 +167,77 @@ def test_linear_ce_empty_rows():
     w = torch.randn((10, 64), device="cuda").bfloat16()
     t = torch.empty((0,), device="cuda", dtype=torch.int64)
     assert float(tritium.linear_cross_entropy(h, w, t)) == 0.0
+
+
+# ---------------------------------------------------------------- kept probabilities
+# The autograd forward of 16-bit inputs keeps fp16 exp(logit - tile max) and the backward
+# forms G from it in place (tritium_linear_ce_fwd_probs / _grad_from_probs) instead of
+# recomputing the logits GEMM.  Same bar as the recompute path: the float64 oracle.
+def _kept_backward(g, h, w, t, lse, need_dh, need_dw, ignore_index, chunk_rows=0):
+    loss2, lse2, kept = tritium.linear_ce._linear_cross_entropy_forward(h, w, t, ignore_index,
+                                                                        keep=True)
+    # the keeping forward sums the same terms in the same order: bitwise the same lse
+    assert torch.equal(lse2, lse)
+    return tritium.linear_ce._backward_from_probs(g, h, w, t, lse2, kept, need_dh, need_dw,
+                                                  ignore_index)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n,d,v,ignore_frac,tdtype", [
+    (1, 32, 128, 0.0, torch.int64),
+    (130, 64, 1001, 0.1, torch.int32),      # vocab not a multiple of 8: padded rows
+    (257, 128, 2049, 0.05, torch.int64),    # past the 256-token and 256-vocab tile edges
+    (64, 40, 300, 0.0, torch.int64),        # hidden_size padded to 48
+])
+def test_linear_ce_kept_probs_against_oracle(dtype, n, d, v, ignore_frac, tdtype):
+    _run(n, d, v, dtype, seed=20, ignore_frac=ignore_frac, tdtype=tdtype, backward=_kept_backward)
+
+
+def test_linear_ce_kept_probs_confident_targets():
+    # targets at each row's arg-max with large logits: p(target) is close to 1 and the
+    # target entry of G is a small difference p - 1 (taken from the fp32 target logit)
+    n, d, v = 128, 64, 777
+    h, w, _ = _inputs(n, d, v, torch.bfloat16, seed=21, wscale=1.5)
+    t = (h.float() @ w.float().t()).argmax(dim=1)
+    loss, lse = tritium.linear_ce._linear_cross_entropy_forward(h, w, t)
+    ref_loss, ref_lse = oracle.linear_ce.forward(np32(h), np32(w), np32(t))
+    assert float(loss) < 0.5  # most rows have p(target) near 1
+    dh, dw = _kept_backward(torch.tensor(1.0, device="cuda"), h, w, t, lse, True, True, -100)
+    edh, edw = oracle.linear_ce.backward(1.0, np32(h), np32(w), np32(t), ref_lse)
+    for got, want, name in ((dh, edh, "dhidden"), (dw, edw, "dweight")):
+        ref = np.asarray(want, dtype=np.float64)
+        rel = np.linalg.norm(np32(got).astype(np.float64) - ref) / max(np.linalg.norm(ref), 1e-30)
+        assert rel < 2e-2, f"{name}: relative L2 {rel:.3e}"
+
+
+def test_linear_ce_kept_probs_matches_recompute_path():
+    h, w, t = _inputs(512, 256, 5000, torch.bfloat16, seed=22, ignore_frac=0.03)
+    loss, lse = tritium.linear_ce._linear_cross_entropy_forward(h, w, t)
+    g = torch.tensor(0.75, device="cuda")
+    a = tritium.linear_ce._backward(g, h, w, t, lse, True, True, -100)
+    b = _kept_backward(g, h, w, t, lse, True, True, -100)
+    for x, y in zip(a, b):
+        x, y = x.double(), y.double()
+        # the two differ only by the fp16 rounding of exp(logit - tile max)
+        assert float((x - y).norm() / y.norm()) < 5e-3
+
+
+def test_linear_ce_autograd_keeps_probs_and_retain_graph():
+    h, w, t = _inputs(200, 64, 900, torch.bfloat16, seed=23, ignore_frac=0.1)
+    hs, ws = h.clone().requires_grad_(True), w.clone().requires_grad_(True)
+    loss = tritium.linear_cross_entropy(hs, ws, t) * 3.0
+    assert loss.grad_fn.next_functions[0][0].kept is not None
+    loss.backward(retain_graph=True)
+    g1 = (hs.grad.clone(), ws.grad.clone())
+    # the kept buffer was consumed: the second backward recomputes the logits
+    loss.backward()
+    def rel(a, b):
+        a, b = a.double(), b.double()
+        return float((a - b).norm() / b.norm())
+
+    for first, total in zip(g1, (hs.grad, ws.grad)):
+        assert rel(total, 2 * first) < 1e-2
+    import torch.nn.functional as F
+    hr, wr = h.float().requires_grad_(True), w.float().requires_grad_(True)
+    (F.cross_entropy(hr @ wr.t(), t, ignore_index=-100) * 3.0).backward()
+    assert rel(g1[0], hr.grad) < 2e-2 and rel(g1[1], wr.grad) < 2e-2
