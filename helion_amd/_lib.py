@@ -107,6 +107,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I32,
         [_P, _I32, _I64, _F32, _F32, _F32, _F32, _F32, _F64, _F64, _I32, _P],
     ),
+    "tritium_sum_splits": (_I32, [_P, _P, _I64, _I64, _I32, _P]),
     "tritium_linear_ce_fwd_probs": (
         _I32,
         [_P, _P, _P, _I32, _I64, _P, _P, _P, _P, _I64, _P, _SZ, _I64, _I64, _I64, _I32, _P],

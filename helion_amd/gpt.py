@@ -44,6 +44,7 @@ import time
 import torch
 import torch.nn.functional as F
 
+from . import _lib
 from .adamw import adamw_step_mixed
 from .attention import attention
 from .linear_ce import linear_cross_entropy
@@ -358,6 +359,16 @@ def _split_k(n_out: int, n_in: int, k: int) -> int:
 _bmm_out_dtype: bool | None = None  # torch.bmm(..., out_dtype=float32) available
 
 
+def _sum_splits(part: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """part.sum(0) rounded once into ``dtype``, in one pass (``tritium_sum_splits``:
+    fp32 sum in split order)."""
+    part = part.contiguous()
+    out = torch.empty(part.shape[1:], device=part.device, dtype=dtype)
+    _lib.call("tritium_sum_splits", part.data_ptr(), out.data_ptr(), part.shape[0], out.numel(),
+              _lib.dtype_code(dtype), _lib.stream_of(part))
+    return out
+
+
 class _Proj(torch.autograd.Function):
     """y = x W^T for a projection of the token rows x [tokens, in]; the weight
     gradient is reduced over token slices by one batched GEMM with fp32 outputs
@@ -383,7 +394,7 @@ class _Proj(torch.autograd.Function):
                 try:
                     part = torch.bmm(dy.view(s, k // s, n_out).transpose(1, 2),
                                      x.view(s, k // s, x.shape[1]), out_dtype=torch.float32)
-                    dw = part.sum(0).to(dy.dtype)
+                    dw = _sum_splits(part, dy.dtype)
                     _bmm_out_dtype = True
                 except (RuntimeError, TypeError, NotImplementedError):
                     _bmm_out_dtype = False

@@ -266,6 +266,16 @@ int tritium_linear_ce_grad_from_probs(const float* grad_out, const float* n_vali
                                       size_t fwd_workspace_bytes, void* probs, int64_t ld_probs,
                                       int64_t n_rows, int64_t vocab, int dtype, void* stream);
 
+/* ---- Split-K finish -------------------------------------------------------
+ * dst[i] = (dtype)(src[0 * n + i] + src[1 * n + i] + ... + src[(n_splits - 1) * n + i]),
+ * summed in fp32 in split order, for src [n_splits, n] float32 (the fp32
+ * outputs of a GEMM split over its reduction dimension) and dst [n] in
+ * `dtype`.  No reference counterpart: the training harness's weight
+ * gradients use it (the reference computes them with one matmul per weight,
+ * tritium/ops/matmul.py:311-333). */
+int tritium_sum_splits(const float* src, void* dst, int64_t n_splits, int64_t n, int dtype,
+                       void* stream);
+
 /* ---- Cross-entropy on materialised logits ----------------------------------
  * tritium.cross_entropy forward (tritium/ops/cross_entropy.py:36-68
  * `_cross_entropy_forward_kernel`, host 534-561): for logits [n_rows, vocab]

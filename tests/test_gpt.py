@@ -66,3 +66,29 @@ def test_train_step_matches_torch_twin():
     assert abs(ga - gb) / gb < 0.02, (ga, gb)
     # training moves the loss
     assert res["loss_hip"][-1] < res["loss_hip"][0]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("s,n", [(1, 8), (4, 768 * 768), (16, 2304 * 768), (3, 1001), (2, 6)])
+def test_sum_splits_bitwise_against_ordered_fp32_sum(dtype, s, n):
+    # tritium_sum_splits sums the split partials in fp32 in split order and rounds once:
+    # bit-equal to the same ordered sum in torch (odd n takes the scalar path)
+    g = torch.Generator().manual_seed(s * 1000 + n % 997)
+    part = torch.randn((s, n), generator=g).cuda()
+    want = part[0].clone()
+    for j in range(1, s):
+        want += part[j]
+    got = gpt._sum_splits(part, dtype)
+    assert torch.equal(got, want.to(dtype))
+    # a misaligned source (offset by one element) takes the scalar path
+    buf = torch.randn((s * n + 1,), generator=g).cuda()
+    part2 = buf[1:].view(s, n)
+    want2 = part2[0].clone()
+    for j in range(1, s):
+        want2 += part2[j]
+    out = torch.empty(n, device="cuda", dtype=dtype)
+    from helion_amd import _lib
+    _lib.call("tritium_sum_splits", part2.data_ptr(), out.data_ptr(), s, n,
+              _lib.dtype_code(dtype), _lib.stream_of(part2))
+    assert torch.equal(out, want2.to(dtype))
