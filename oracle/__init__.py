@@ -18,7 +18,7 @@ Conventions shared by every function here:
 * Each function cites the reference ``file:line`` whose arithmetic it follows.
 
 Pinning status (what independent check fixes each function) is written in the
-docstring of every module; the CPU test-suite (``tests/test_oracle_*.py``)
+docstring of every module; the CPU test-suite (``tests/test_oracle.py``)
 runs those checks.
 """
 

@@ -6,7 +6,7 @@ before the Adam term (adamw.py:50), ``denom = sqrt(v / bc2) + eps`` and
 ``step_size = lr / bc1`` (adamw.py:51-53) with the bias corrections computed on
 the host in float64 (adamw.py:133-134).
 
-Pinned by (tests/test_oracle_adamw.py): ``torch.optim.AdamW(foreach=False)``
+Pinned by (tests/test_oracle.py, test_adamw_*): ``torch.optim.AdamW(foreach=False)``
 over several steps (tests/tritium/test_adamw.py:19-27 compares against it), and
 the step-1 closed form from zero moments
 ``p1 = p*(1 - lr*wd) - lr * g / (|g| + eps)``.

@@ -18,7 +18,7 @@ Arithmetic is float64 by default (``acc=np.float64``), the "fp32 reference" the
 north-star tolerance (max-abs 2e-2 for bf16) is quoted against; ``acc=np.float32``
 gives the reference kernels' own accumulation width.
 
-Pinned by (tests/test_oracle_attention.py): torch
+Pinned by (tests/test_oracle.py, test_attention_*): torch
 ``F.scaled_dot_product_attention`` with ``repeat_interleave`` for GQA and its
 autograd (tests/tritium/test_attention.py:9-21, 100-107), ``T = 1`` gives
 ``o = v``, causal row 0 gives ``o[0] = v[0]``, uniform v rows give ``o = v``,

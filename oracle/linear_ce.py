@@ -19,7 +19,7 @@ no ignored target the result is the reference's.
 Arithmetic is float64 by default (the fp32-or-better reference the north-star
 tolerance is quoted against).
 
-Pinned by (tests/test_oracle_linear_ce.py): torch
+Pinned by (tests/test_oracle.py, test_linear_ce_*): torch
 ``F.cross_entropy(F.linear(h, W).float(), t, ignore_index=-100)`` and its
 autograd (tests/tritium/test_cross_entropy.py:72, 93), the closed form for
 ``W = 0`` (``loss = ln V``, ``dH = 0``, ``dW = (1/V - onehot)^T h / N_valid``),

@@ -16,7 +16,7 @@ Follows alkinun/helion ``tritium/ops/rmsnorm.py``:
 * residual backward ``dz = rmsnorm_bwd(dy) + dresidual_out``, returned for both
   x and residual (rmsnorm.py:720-734).
 
-Pinned by (tests/test_oracle_rmsnorm.py): torch's ``F.rms_norm`` library
+Pinned by (tests/test_oracle.py, test_rmsnorm_*): torch's ``F.rms_norm`` library
 routine, the closed form for a constant row ``y = w*c/sqrt(c^2+eps)``, torch
 autograd of the forward (an independent derivation of dx and dw), a float64
 finite-difference gradient check, and the reference's own test formulas

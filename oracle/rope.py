@@ -11,7 +11,7 @@ Follows alkinun/helion ``tritium/ops/rope.py``:
   ``(a*c + b*s, b*c - a*s)`` (rope.py:76-85), computed in fp32 and stored in
   the input dtype.
 
-Pinned by (tests/test_oracle_rope.py): the complex-multiplication restatement
+Pinned by (tests/test_oracle.py, test_rope_*): the complex-multiplication restatement
 ``(a + i b) * exp(+-i theta)``, identity at position 0, conservation of every
 pair's norm, ``inverse(forward(x)) == x`` in float64, torch autograd of the
 forward (which must equal the inverse rotation: the reference never checks

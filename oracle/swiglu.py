@@ -4,7 +4,7 @@ Follows alkinun/helion ``tritium/ops/swiglu.py``: ``silu(x) * gate`` in fp32
 (swiglu.py:32-35); backward ``dx = dy * gate * sig * (1 + x * (1 - sig))``,
 ``dgate = dy * silu(x)`` (swiglu.py:51-58); the first argument gets the silu.
 
-Pinned by (tests/test_oracle_swiglu.py): torch ``F.silu(x) * gate`` and its
+Pinned by (tests/test_oracle.py, test_swiglu_*): torch ``F.silu(x) * gate`` and its
 autograd (tests/tritium/test_swiglu.py:9-10, 25-36), the special case x = 0
 (``out = 0``, ``dgate = 0``, ``dx = dy * gate / 2``), a float64
 finite-difference check, and the golden fixtures.
