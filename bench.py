@@ -306,6 +306,8 @@ REF_ROWS = [
     ("linear_ce_bwd 512x4096x128256", 25.50, "ms", 160),
     ("linear_ce_fwd 1024x4096x32000", 4.05, "ms", 170),
     ("linear_ce_bwd 1024x4096x32000", 11.78, "ms", 161),
+    ("cross_entropy_fwd 128x1024", 41.367951, "GB/s", 68),
+    ("cross_entropy_fwd 16x32768", 112.024969, "GB/s", 70),
 ]
 
 
@@ -384,6 +386,11 @@ def ref_bench_leg(torch, tritium, reps: int = 20):
         out[f"linear_ce_bwd {nr}x{dh}x{vv}"] = (None, ms_of(
             lambda: tritium.linear_cross_entropy_backward(go, hid, wt, tgt, lse)))
         del hid, wt, lse
+    # bench_cross_entropy.py:42-51: fp16 logits, effective GB/s on the logits bytes
+    for nr, vv in ((128, 1024), (16, 32768)):
+        lg = rnd(nr, vv)
+        tg = torch.randint(vv, (nr,), generator=g, device=dev)
+        out[f"cross_entropy_fwd {nr}x{vv}"] = (lg.numel() * 2, ms_of(lambda: tritium.cross_entropy(lg, tg)))
     del flush
     torch.cuda.empty_cache()
     rows = []
@@ -400,6 +407,74 @@ def ref_bench_leg(torch, tritium, reps: int = 20):
 
 
 # ------------------------------------------------------------ CPU leg --
+DECODE_SHAPES = ((1, 32, 32, 4096, 128), (8, 32, 32, 4096, 128), (8, 32, 8, 8192, 128),
+                 (16, 12, 12, 1024, 64))
+
+
+def decode_leg(torch, tritium, calls: int = 50):
+    """KV-cache decode: ``attention`` with one query row per head against a
+    bf16 cache slice (B, H, H_kv, L, D) in ``DECODE_SHAPES``.  Per shape the
+    eager time per call (host path included: back-to-back calls) and the time
+    per call of the same calls replayed from one captured graph (the kernels
+    alone), with GB/s on the K + V bytes the call must read (HBM-bound)."""
+    dev = torch.device("cuda")
+    g = torch.Generator(device=dev).manual_seed(0)
+    out = []
+    for b, h, hkv, L, d in DECODE_SHAPES:
+        kc = torch.randn((b, hkv, L + 512, d), generator=g, device=dev).to(torch.bfloat16)
+        vc = torch.randn((b, hkv, L + 512, d), generator=g, device=dev).to(torch.bfloat16)
+        q = torch.randn((b, h, 1, d), generator=g, device=dev).to(torch.bfloat16)
+        k, v = kc[:, :, :L], vc[:, :, :L]
+
+        def fn():
+            return tritium.attention(q, k, v, is_causal=False)
+
+        for _ in range(5):
+            ref = fn()
+        torch.cuda.synchronize()
+        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s.record()
+        for _ in range(calls):
+            fn()
+        e.record()
+        torch.cuda.synchronize()
+        eager_us = s.elapsed_time(e) / calls * 1e3
+        nbytes = 2 * b * hkv * L * d * 2
+        row = {"shape": [b, h, hkv, L, d], "kv_bytes": nbytes, "eager_us": round(eager_us, 1)}
+        try:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(3):
+                    fn()
+            torch.cuda.current_stream().wait_stream(side)
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for _ in range(calls):
+                    got = fn()
+            for _ in range(2):
+                graph.replay()
+            torch.cuda.synchronize()
+            row["graph_matches_eager"] = bool(torch.equal(got, ref))
+            reps = 5
+            s.record()
+            for _ in range(reps):
+                graph.replay()
+            e.record()
+            torch.cuda.synchronize()
+            us = s.elapsed_time(e) / (reps * calls) * 1e3
+            row.update({"graph_us": round(us, 1), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
+                        "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
+            del graph
+        except RuntimeError as exc:  # capture refused: report the eager figure only
+            row["graph_error"] = str(exc)[:200]
+        out.append(row)
+        del kc, vc
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
+
+
 def gpt_leg(torch, steps: int = 10, warmup: int = 3):
     """Config 5: the 151.9M-parameter GPT (12 x 768, SwiGLU 3072, vocab 50304, tied
     embeddings) training step at B=16 x T=1024 on the kernel layer: bf16 compute,
@@ -499,7 +574,7 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--legs", default="rows,attention,lce,gpt,refbench",
+    ap.add_argument("--legs", default="rows,attention,lce,gpt,refbench,decode",
                     help="comma list of rows,attention,lce,gpt,refbench (rows is the headline; "
                          "refbench reruns the reference's published benchmark rows)")
     ap.add_argument("--copy-probe", action="store_true",
@@ -543,6 +618,8 @@ def main(argv=None) -> int:
             ops["gpt_train_step"] = gpt_leg(torch, steps=args.steps, warmup=args.warmup)
         if "refbench" in legs:
             ops["reference_benchmarks"] = ref_bench_leg(torch, tritium)
+        if "decode" in legs:
+            ops["attention_decode"] = decode_leg(torch, tritium)
         print(json.dumps({"metric": METRIC, "partial": True, "ops": ops}), flush=True)
         return 0
     rows = row_leg(torch, tritium, args.steps, args.warmup)
@@ -563,6 +640,11 @@ def main(argv=None) -> int:
         ops["reference_benchmarks"] = ref_bench_leg(torch, tritium)
         print(f"[bench] reference benchmarks: {ops['reference_benchmarks']}", file=sys.stderr,
               flush=True)
+    # after the reference rows: its captured graphs' memory pools would change
+    # what the allocator holds for them
+    if "decode" in legs:
+        ops["attention_decode"] = decode_leg(torch, tritium)
+        print(f"[bench] decode: {ops['attention_decode']}", file=sys.stderr, flush=True)
 
     adamw_gbs = rows["adamw_bytes"] / (rows["adamw_ms"] * 1e-3) / 1e9
     traffic = None

@@ -23,6 +23,7 @@ namespace {
 constexpr int kBlock = 256;
 constexpr int64_t kWideRow = 8192;        // rows at least this long get a whole block
 constexpr int64_t kBwdChunk = 256 * 8 * 4;  // elements of one row per backward block
+constexpr int kInFlight = 8;              // 16-byte loads in flight per lane (forward)
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
 
@@ -51,25 +52,37 @@ __device__ __forceinline__ void row_ms(const T* __restrict__ x, int64_t V, bool 
   m = -INFINITY;
   s = 0.0f;
   int64_t tail = 0;
+  // fold one raw 16-byte vector into (m, s)
+  auto fold = [&](u32x4 raw) {
+    float f[VEC];
+    unpack<T>(raw, f);
+    float vm = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < VEC; ++i) {
+      f[i] *= kLog2e;
+      vm = fmaxf(vm, f[i]);
+    }
+    if (vm > m) {
+      s = (m == -INFINITY) ? 0.0f : s * fast_exp2(m - vm);
+      m = vm;
+    }
+    if (m != -INFINITY) {
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) s += exp_shift(f[i], m);
+    }
+  };
   if (vec_ok) {
     const int64_t nv = V / VEC;
-    for (int64_t iv = lane; iv < nv; iv += LANES) {
-      float f[VEC];
-      unpack<T>(ld16_nt(x + iv * VEC), f);
-      float vm = -INFINITY;
+    // up to kInFlight loads issued together: the fold's branch on the running
+    // max would otherwise serialise one memory round trip per vector
+    for (int64_t iv = lane; iv < nv; iv += kInFlight * LANES) {
+      u32x4 raw[kInFlight];
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        f[i] *= kLog2e;
-        vm = fmaxf(vm, f[i]);
-      }
-      if (vm > m) {
-        s = (m == -INFINITY) ? 0.0f : s * fast_exp2(m - vm);
-        m = vm;
-      }
-      if (m != -INFINITY) {
+      for (int u = 0; u < kInFlight; ++u)
+        if (iv + u * LANES < nv) raw[u] = ld16_nt(x + (iv + u * LANES) * VEC);
 #pragma unroll
-        for (int i = 0; i < VEC; ++i) s += exp_shift(f[i], m);
-      }
+      for (int u = 0; u < kInFlight; ++u)
+        if (iv + u * LANES < nv) fold(raw[u]);
     }
     tail = nv * VEC;
   }
