@@ -131,23 +131,28 @@ class _TableCache:
 _tables = _TableCache()
 
 
-def _table_for(params, grads, exp_avgs, exp_avg_sqs, validate: bool):
+def _signature(t: torch.Tensor) -> tuple:
+    """Everything the checks of :func:`_check_adamw_inputs` and the kernel's
+    addressing depend on: a cache hit then means the same checks would pass."""
+    return (t.data_ptr(), t.dtype, t.device, tuple(t.shape), t.stride())
+
+
+def _table_for(params, grads, exp_avgs, exp_avg_sqs):
     key = tuple(
-        (p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr(), p.numel(), p.dtype)
+        (_signature(p), _signature(g), _signature(m), _signature(v))
         for p, g, m, v in zip(params, grads, exp_avgs, exp_avg_sqs)
     )
     hit = _tables.get(key)
     if hit is not None:
         return hit
-    if validate:
-        for p, g, m, v in zip(params, grads, exp_avgs, exp_avg_sqs):
-            _check_adamw_inputs(p, g, m, v)
-        device = params[0].device
-        for p in params:
-            if p.device != device:
-                raise ValueError(
-                    f"Device mismatch: all params must be on {device}, got {p.device}."
-                )
+    for p, g, m, v in zip(params, grads, exp_avgs, exp_avg_sqs):
+        _check_adamw_inputs(p, g, m, v)
+    device = params[0].device
+    for p in params:
+        if p.device != device:
+            raise ValueError(
+                f"Device mismatch: all params must be on {device}, got {p.device}."
+            )
     chunk = int(_lib.lib().tritium_adamw_chunk_elements())
     rows = []
     first = 0
@@ -184,8 +189,9 @@ def adamw_step_multi(
     """AdamW on every ``params[i]`` in ONE kernel launch.
 
     Per tensor the arithmetic and checks are those of :func:`adamw_step`;
-    all tensors must be on one device.  Checks run whenever the set of
-    tensors (their storage) changes.
+    all tensors must be on one device.  The checks run whenever any tensor's
+    storage address, dtype, device, shape or strides differ from a cached
+    descriptor table's.
     """
     if not (len(params) == len(grads) == len(exp_avgs) == len(exp_avg_sqs)):
         raise ValueError(
@@ -194,7 +200,7 @@ def adamw_step_multi(
         )
     if len(params) == 0:
         return
-    table, n_tensors, total_chunks = _table_for(params, grads, exp_avgs, exp_avg_sqs, True)
+    table, n_tensors, total_chunks = _table_for(params, grads, exp_avgs, exp_avg_sqs)
     if n_tensors == 0:
         return
     bc1, bc2 = _bias_corrections(beta1, beta2, step)

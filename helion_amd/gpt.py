@@ -359,6 +359,22 @@ def _split_k(n_out: int, n_in: int, k: int) -> int:
 _bmm_out_dtype: bool | None = None  # torch.bmm(..., out_dtype=float32) available
 
 
+def _bmm_fp32_out_supported(device) -> bool:
+    """Whether this torch accepts ``torch.bmm(..., out_dtype=float32)`` for
+    16-bit operands, probed once on a tiny product; a TypeError (an unknown
+    keyword) or NotImplementedError (no kernel for the combination) means no,
+    anything else is a real failure and propagates."""
+    global _bmm_out_dtype
+    if _bmm_out_dtype is None:
+        a = torch.zeros((1, 2, 2), device=device, dtype=torch.bfloat16)
+        try:
+            torch.bmm(a, a, out_dtype=torch.float32)
+            _bmm_out_dtype = True
+        except (TypeError, NotImplementedError):
+            _bmm_out_dtype = False
+    return _bmm_out_dtype
+
+
 def _sum_splits(part: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     """part.sum(0) rounded once into ``dtype``, in one pass (``tritium_sum_splits``:
     fp32 sum in split order)."""
@@ -382,23 +398,18 @@ class _Proj(torch.autograd.Function):
 
     @staticmethod
     def backward(ctx, dy):
-        global _bmm_out_dtype
         x, w = ctx.saved_tensors
         dy = dy.contiguous()
         dx = dy @ w if ctx.needs_input_grad[0] else None
         dw = None
         if ctx.needs_input_grad[1]:
             k, n_out = dy.shape
-            s = _split_k(n_out, x.shape[1], k) if _bmm_out_dtype is not False else 1
-            if s > 1:
-                try:
-                    part = torch.bmm(dy.view(s, k // s, n_out).transpose(1, 2),
-                                     x.view(s, k // s, x.shape[1]), out_dtype=torch.float32)
-                    dw = _sum_splits(part, dy.dtype)
-                    _bmm_out_dtype = True
-                except (RuntimeError, TypeError, NotImplementedError):
-                    _bmm_out_dtype = False
-            if dw is None:
+            s = _split_k(n_out, x.shape[1], k)
+            if s > 1 and _bmm_fp32_out_supported(dy.device):
+                part = torch.bmm(dy.view(s, k // s, n_out).transpose(1, 2),
+                                 x.view(s, k // s, x.shape[1]), out_dtype=torch.float32)
+                dw = _sum_splits(part, dy.dtype)
+            else:
                 dw = dy.t() @ x
         return dx, dw
 

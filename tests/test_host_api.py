@@ -132,6 +132,27 @@ def test_swiglu_and_adamw_messages(meta_ok):
         tritium.adamw_step_multi([meta(8)], [], [], [], lr=1e-3)
 
 
+def test_adamw_table_cache_revalidates_changed_tensors(meta_ok, monkeypatch):
+    """A cached descriptor table is reused only for tensors with the same
+    address, dtype, device, shape and strides; a wrong-dtype grad, a 16-bit
+    moment or a non-contiguous view at a cached address is checked again and
+    rejected (meta tensors all share address 0, the worst case)."""
+    cache = adamw_mod._TableCache()
+    monkeypatch.setattr(adamw_mod, "_tables", cache)
+    p, g, m, v = meta(8, 4), meta(8, 4), meta(8, 4), meta(8, 4)
+    key = ((adamw_mod._signature(p), adamw_mod._signature(g), adamw_mod._signature(m),
+            adamw_mod._signature(v)),)
+    sentinel = ("table", 1, 1)
+    cache.put(key, sentinel)
+    assert adamw_mod._table_for([p], [g], [m], [v]) is sentinel
+    with pytest.raises(ValueError, match="Dtype mismatch"):
+        adamw_mod._table_for([p], [meta(8, 4, dtype=torch.float16)], [m], [v])
+    with pytest.raises(ValueError, match="exp_avg must have dtype float32"):
+        adamw_mod._table_for([p], [g], [meta(8, 4, dtype=torch.bfloat16)], [v])
+    with pytest.raises(ValueError, match="must be contiguous"):
+        adamw_mod._table_for([p], [g], [m], [meta(4, 8).t()])
+
+
 def test_linear_ce_messages(meta_ok):
     lt = torch.int64
     with pytest.raises(ValueError, match="at least 2 dimensions"):
