@@ -85,6 +85,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I32,
         [_P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P],
     ),
+    "tritium_attention_decode_noalloc_max_bytes": (_SZ, []),
+    "tritium_attention_decode_noalloc": (
+        _I32,
+        [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P],
+    ),
     "tritium_linear_ce_fwd_workspace_size": (_SZ, [_I64, _I64, _I32]),
     "tritium_linear_ce_fwd": (
         _I32,

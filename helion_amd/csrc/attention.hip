@@ -34,6 +34,8 @@
 // first.
 #include <math.h>
 
+#include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "common.h"
@@ -2452,10 +2454,11 @@ extern "C" size_t tritium_attention_decode_workspace_size(int64_t B, int64_t H, 
   return (size_t)B * H * dec_splits(B, Hkv, Tkv) * (D + 2) * sizeof(float);
 }
 
-extern "C" int tritium_attention_decode(const void* q, const void* k, const void* v, void* o,
-                                        float* lse, void* workspace, size_t workspace_bytes,
-                                        int64_t B, int64_t H, int64_t Hkv, int64_t Tkv, int64_t D,
-                                        const int64_t* strides, int dtype, void* stream) {
+namespace {
+
+int decode_launch(const void* q, const void* k, const void* v, void* o, float* lse,
+                  void* workspace, size_t workspace_bytes, int64_t B, int64_t H, int64_t Hkv,
+                  int64_t Tkv, int64_t D, const int64_t* strides, int dtype, void* stream) {
   if (int e = check_dims(B, H, Hkv, 1, Tkv, D)) return e;
   if (B == 0) return TRI_OK;
   if (Tkv < 1) return fail(TRI_EINVAL, "attention decode: needs at least one key");
@@ -2508,4 +2511,89 @@ extern "C" int tritium_attention_decode(const void* q, const void* k, const void
     else attn_decode_combine<f16_t, 128><<<(unsigned)(B * H), 128, 0, st>>>(a);
   }
   return check_launch("attention decode combine");
+}
+
+}  // namespace
+
+// Scratch of the no-allocation decode entry: the chunks' partial (m, l, o)
+// rows, one copy per GPU, resident until the process ends.  Every partial
+// row a call reads was written by the same call's first kernel, so nothing
+// has to be cleared between calls.  On the host, `scratch` names a host-side
+// stand-in; kernels get the device address from hipGetSymbolAddress.
+constexpr size_t kDecScratchBytes = size_t(32) << 20;
+static __device__ __align__(256) float scratch[kDecScratchBytes / sizeof(float)];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch_ptr[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.  `stream` must belong to the
+// current device, or the kernels would run on another GPU than the address.
+int decode_scratch(void* stream, float** out) {
+  int dev = 0;
+  hipError_t err = hipGetDevice(&dev);
+  if (err != hipSuccess)
+    return fail(TRI_ELAUNCH, "attention decode (no-alloc): hipGetDevice: %s", hipGetErrorString(err));
+  if (dev < 0 || dev >= kMaxDevices)
+    return fail(TRI_EINVAL, "attention decode (no-alloc): device %d beyond %d", dev, kMaxDevices);
+  if (stream != nullptr) {
+    int sdev = dev;
+    err = hipStreamGetDevice((hipStream_t)stream, &sdev);
+    if (err != hipSuccess)
+      return fail(TRI_ELAUNCH, "attention decode (no-alloc): hipStreamGetDevice: %s",
+                  hipGetErrorString(err));
+    if (sdev != dev)
+      return fail(TRI_EINVAL,
+                  "attention decode (no-alloc): the stream belongs to device %d but device %d is current",
+                  sdev, dev);
+  }
+  float* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    ptr = g_scratch_ptr[dev].load(std::memory_order_relaxed);
+    if (ptr == nullptr) {
+      void* p = nullptr;
+      err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+      if (err != hipSuccess || p == nullptr)
+        return fail(TRI_ELAUNCH, "attention decode (no-alloc): hipGetSymbolAddress: %s",
+                    hipGetErrorString(err));
+      ptr = (float*)p;
+      g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+    }
+  }
+  *out = ptr;
+  return TRI_OK;
+}
+
+}  // namespace
+
+extern "C" int tritium_attention_decode(const void* q, const void* k, const void* v, void* o,
+                                        float* lse, void* workspace, size_t workspace_bytes,
+                                        int64_t B, int64_t H, int64_t Hkv, int64_t Tkv, int64_t D,
+                                        const int64_t* strides, int dtype, void* stream) {
+  return decode_launch(q, k, v, o, lse, workspace, workspace_bytes, B, H, Hkv, Tkv, D, strides,
+                       dtype, stream);
+}
+
+extern "C" size_t tritium_attention_decode_noalloc_max_bytes(void) { return kDecScratchBytes; }
+
+extern "C" int tritium_attention_decode_noalloc(const void* q, const void* k, const void* v,
+                                                void* o, float* lse, int64_t B, int64_t H,
+                                                int64_t Hkv, int64_t Tkv, int64_t D,
+                                                const int64_t* strides, int dtype, void* stream) {
+  if (int e = check_dims(B, H, Hkv, 1, Tkv, D)) return e;
+  if (B == 0) return TRI_OK;
+  const size_t need = tritium_attention_decode_workspace_size(B, H, Hkv, Tkv, D);
+  if (need > kDecScratchBytes)
+    return fail(TRI_EINVAL,
+                "attention decode (no-alloc): %zu bytes of partials needed, more than its %zu-byte "
+                "scratch; use tritium_attention_decode with a workspace",
+                need, kDecScratchBytes);
+  float* part = nullptr;
+  if (int e = decode_scratch(stream, &part)) return e;
+  return decode_launch(q, k, v, o, lse, part, kDecScratchBytes, B, H, Hkv, Tkv, D, strides, dtype,
+                       stream);
 }

@@ -194,6 +194,24 @@ int tritium_attention_decode(const void* q, const void* k, const void* v, void* 
                              int64_t Hkv, int64_t Tkv, int64_t D, const int64_t* strides,
                              int dtype, void* stream);
 
+/* tritium_attention_decode without a workspace argument and without any
+ * allocation: no counterpart in the reference.  It is for callers that cannot
+ * allocate device memory -- code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc.  The partial (m, l, o) rows go to a
+ * scratch array that the library holds on each GPU it runs on until the
+ * process ends (tritium_attention_decode_noalloc_max_bytes() bytes = 32 MiB);
+ * a call whose partials would need more (the workspace size that
+ * tritium_attention_decode_workspace_size returns for the same arguments) is
+ * rejected with TRI_EINVAL.  Results are bitwise those of
+ * tritium_attention_decode.  The scratch is looked up once per device, with
+ * that device current; `stream` must belong to the current device.  Every
+ * call on one GPU shares that GPU's scratch: calls that overlap on one GPU
+ * (on different streams, or from several threads) race. */
+size_t tritium_attention_decode_noalloc_max_bytes(void);
+int tritium_attention_decode_noalloc(const void* q, const void* k, const void* v, void* o,
+                                     float* lse, int64_t B, int64_t H, int64_t Hkv, int64_t Tkv,
+                                     int64_t D, const int64_t* strides, int dtype, void* stream);
+
 /* ---- fused linear + cross-entropy ---------------------------------------------
  * Forward of tritium.linear_cross_entropy (tritium/ops/cross_entropy.py:134-293
  * kernels, host `_linear_cross_entropy_forward` 563-640, autograd 663-705),
