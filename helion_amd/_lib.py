@@ -113,14 +113,6 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _I32, _I64, _F32, _F32, _F32, _F32, _F32, _F64, _F64, _I32, _P],
     ),
     "tritium_sum_splits": (_I32, [_P, _P, _I64, _I64, _I32, _P]),
-    "tritium_linear_ce_fwd_probs": (
-        _I32,
-        [_P, _P, _P, _I32, _I64, _P, _P, _P, _P, _I64, _P, _SZ, _I64, _I64, _I64, _I32, _P],
-    ),
-    "tritium_linear_ce_grad_from_probs": (
-        _I32,
-        [_P, _P, _P, _I32, _I64, _P, _P, _SZ, _P, _I64, _I64, _I64, _I32, _P],
-    ),
     "tritium_linear_ce_grad_logits": (
         _I32,
         [_P, _P, _P, _P, _P, _I32, _I64, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I32, _P],

@@ -1,8 +1,17 @@
 // Block-tiled GEMM core C = A * B^T for gfx950 with pluggable epilogues.
 //
-// Both operands are "K-contiguous": A is [M, K] and B is [N, K], row-major
-// with leading dimensions lda / ldb (elements; rows 16-byte aligned), so every
-// MFMA fragment is one 16-byte LDS read.  A workgroup of WM x WN wavefronts
+// Each operand is "K-contiguous" (A stored [M, K], B stored [N, K], row-major
+// with leading dimension lda / ldb in elements, rows 16-byte aligned: every
+// MFMA fragment is one 16-byte LDS read) or, for 16-bit types, selected per
+// operand by the TA / TB template flags, "MN-contiguous" (A stored [K, M],
+// B stored [K, N]: C = A^T B, A B, ... without transposed copies).  An
+// MN-contiguous tile sits in LDS as BK k-rows of BM (BN) elements and its
+// fragments come from pairs of ds_read_b64_tr_b16 transposing reads, which
+// hand lane (m, g) the k values 8g .. 8g + 7 of column m, the same k order
+// as the 16-byte reads, so the two layouts mix freely in one product.  Its
+// m (n) extent is read in 8-element granules clamped to the last granule of
+// round_up(M, 8) (round_up(N, 8)), so a stored row must hold that many
+// elements.  A workgroup of WM x WN wavefronts
 // computes a BM x BN tile of C; wavefront (wm, wn) owns the (BM/WM) x (BN/WN)
 // sub-tile at (wm*BM/WM, wn*BN/WN), i.e. MT x NT tiles of 32 x 32.
 //
@@ -75,6 +84,36 @@ __device__ __forceinline__ int swz_key(int r) {
 template <class C>
 __device__ __forceinline__ int swz(int r, int c) { return r * C::RB + ((c ^ swz_key<C>(r)) << 4); }
 
+// MN-contiguous tiles: k-row r of X columns, XR = X * 2 bytes.  Granule c
+// of row r sits at slot c ^ tkey(r): the 4 rows x 4 granules one 32-lane
+// cycle of a transposing read touches (rows 4j .. 4j + 3, granules 4q ..
+// 4q + 3) land in 16 distinct 16-byte bank groups.
+__device__ __forceinline__ int tkey(int r) { return (r & 3) << 2; }
+template <int X>
+__device__ __forceinline__ int tswz(int r, int c) { return r * (2 * X) + ((c ^ tkey(r)) << 4); }
+
+// Fragment of an MN-contiguous tile of X columns: columns col0 .. col0 + 31
+// (col0 a multiple of 32) as lane & 31, k = 16 S + 8 g .. + 7 (g = lane >> 5).
+// One transposing read serves a 16-lane group: source lane s addresses k-row
+// (s >> 2) at columns 4 (s & 3) .. + 3 of the group's 16 columns, and
+// destination lane j receives the four k values of column j; two reads (k
+// rows 8g .. 8g + 3 and 8g + 4 .. 8g + 7) make the 8 k values of a lane.
+template <int X, class V>
+__device__ __forceinline__ V frag_tr(const char* tile, int col0, int S) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const int lane = threadIdx.x & 63;
+  const int ts = lane & 15, th = (lane >> 4) & 1, g = lane >> 5;
+  const int r1 = 16 * S + 8 * g + (ts >> 2);
+  const int c = (col0 >> 3) + 2 * th + ((ts & 3) >> 1);
+  const int sub = (ts & 1) * 8;
+  const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(lds_addr(tile + tswz<X>(r1, c) + sub)));
+  const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) v4s*)(lds_addr(tile + tswz<X>(r1 + 4, c) + sub)));
+  // one whole-vector cast (element-wise assembly was miscompiled into broadcasts)
+  return __builtin_bit_cast(V, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+}
+
 template <class C>
 __device__ __forceinline__ int acc_row(int wm, int i, int r, int g) {
   return wm * C::WTM + 32 * i + 8 * (r >> 2) + 4 * g + (r & 3);
@@ -100,37 +139,111 @@ struct Problem {
   int64_t M, N, K;
 };
 
-// Issue DMAs [Q0, Q1) of this wavefront's share of K tile k0 (both
-// operands) into one LDS stage; dma_tile issues all of them.
-template <class C, typename T, int Q0 = 0, int Q1 = C::DMA_PER_WAVE>
-__device__ __forceinline__ void dma_tile(char* stage, const Problem& p, int64_t m0, int64_t n0,
-                                         int64_t k0) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int rr = lane / C::GRAN;  // row inside the instruction's run of DMA_ROWS rows
+// Source of the 16 bytes that land at byte 16 * lane of 1 KiB run `run` of
+// an operand tile (K-contiguous: DMA_ROWS rows of RB bytes; MN-contiguous:
+// 1024 / (2 X) k-rows of X elements).
+template <class C, typename T, bool TR, int X>
+__device__ __forceinline__ const T* run_src(const void* base, int64_t ld, int64_t x0, int64_t xn,
+                                            int64_t k0, int run, int lane) {
   constexpr int VE = vec<T>();
-#pragma unroll
-  for (int q = Q0; q < Q1; ++q) {
-    const int grp = wave * C::DMA_PER_WAVE + q;  // wave-uniform run of rows
-    const int trow = grp * C::DMA_ROWS + rr;     // tile row (A rows, then B rows)
-    // the granule that lands in slot lane % GRAN of that row
+  if constexpr (!TR) {
+    const int trow = run * C::DMA_ROWS + lane / C::GRAN;
     const int c = (lane % C::GRAN) ^ swz_key<C>(trow);
-    const T* src;
-    if (grp * C::DMA_ROWS < C::BM) {
-      const int64_t row = imin(m0 + trow, p.M - 1);
-      src = (const T*)p.a + row * p.lda + k0 + c * VE;
-    } else {
-      const int64_t row = imin(n0 + trow - C::BM, p.N - 1);
-      src = (const T*)p.b + row * p.ldb + k0 + c * VE;
-    }
-    dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(stage + grp * C::DMA_ROWS * C::RB)));
+    return (const T*)base + imin(x0 + trow, xn - 1) * ld + k0 + c * VE;
+  } else {
+    constexpr int XG = X / 8;  // granules per k-row
+    static_assert(XG <= 64 && 64 % XG == 0, "k-rows of at most 1 KiB");
+    const int krow = run * (64 / XG) + lane / XG;
+    const int c = (lane % XG) ^ tkey(krow);
+    const int64_t last = ((xn + 7) & ~(int64_t)7) - 8;  // last granule of round_up(xn, 8)
+    return (const T*)base + (k0 + krow) * ld + imin(x0 + c * VE, last);
   }
 }
 
-// The partial last K tile [k0, K) through registers, zero-filled past K.
-template <class C, typename T>
+// DMA q of this wavefront's share of K tile k0 into one LDS stage: every
+// wavefront issues PA runs of the A tile, then PB runs of the B tile, so the
+// operand of each DMA is known at compile time (no branch, and no per-lane
+// select between the operands' pointers, which the compiler had routed
+// through a stack array).
+template <class C, typename T, int Q, bool TA, bool TB>
+__device__ __forceinline__ void dma_one(char* stage, const Problem& p, int64_t m0, int64_t n0,
+                                        int64_t k0, int lane, int wave) {
+  constexpr int W = C::WM * C::WN;
+  constexpr int RUNS_A = C::BM / C::DMA_ROWS, RUNS_B = C::BN / C::DMA_ROWS;
+  constexpr int PA = RUNS_A / W, PB = RUNS_B / W;
+  static_assert(PA * W == RUNS_A && PB * W == RUNS_B && PA + PB == C::DMA_PER_WAVE,
+                "each operand's runs split evenly over the wavefronts");
+  if constexpr (Q < PA) {
+    const int run = wave * PA + Q;
+    const T* src = run_src<C, T, TA, C::BM>(p.a, p.lda, m0, p.M, k0, run, lane);
+    dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(stage + run * 1024)));
+  } else {
+    const int run = wave * PB + (Q - PA);
+    const T* src = run_src<C, T, TB, C::BN>(p.b, p.ldb, n0, p.N, k0, run, lane);
+    dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(stage + (RUNS_A + run) * 1024)));
+  }
+}
+
+template <class C, typename T, int Q, int Q1, bool TA, bool TB>
+__device__ __forceinline__ void dma_range(char* stage, const Problem& p, int64_t m0, int64_t n0,
+                                          int64_t k0, int lane, int wave) {
+  if constexpr (Q < Q1) {
+    dma_one<C, T, Q, TA, TB>(stage, p, m0, n0, k0, lane, wave);
+    dma_range<C, T, Q + 1, Q1, TA, TB>(stage, p, m0, n0, k0, lane, wave);
+  }
+}
+
+// Issue DMAs [Q0, Q1) of this wavefront's share of K tile k0 (both
+// operands) into one LDS stage; dma_tile issues all of them.
+template <class C, typename T, int Q0 = 0, int Q1 = C::DMA_PER_WAVE, bool TA = false,
+          bool TB = false>
+__device__ __forceinline__ void dma_tile(char* stage, const Problem& p, int64_t m0, int64_t n0,
+                                         int64_t k0) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  dma_range<C, T, Q0, Q1, TA, TB>(stage, p, m0, n0, k0, lane, wave);
+}
+
+// One operand of the partial last K tile, MN-contiguous: k-rows past K are
+// zero, columns clamped like the DMA's.
+template <class C, typename T, int X>
+__device__ __forceinline__ void reg_tile_tr(char* tile, const void* base, int64_t ld, int64_t x0,
+                                            int64_t xn, int64_t k0, int64_t K) {
+  constexpr int VE = vec<T>(), XG = X / 8, BK = bk<C, T>();
+  const int64_t last = ((xn + 7) & ~(int64_t)7) - 8;
+  for (int idx = threadIdx.x; idx < BK * XG; idx += C::THREADS) {
+    const int kr = idx / XG, c = idx % XG;
+    Pack<T, VE> pk;
+    if (k0 + kr < K) {
+      pk = *reinterpret_cast<const Pack<T, VE>*>((const T*)base + (k0 + kr) * ld +
+                                                 imin(x0 + c * VE, last));
+    } else {
+#pragma unroll
+      for (int e = 0; e < VE; ++e) pk.v[e] = (T)0.f;
+    }
+    *reinterpret_cast<Pack<T, VE>*>(tile + tswz<X>(kr, c)) = pk;
+  }
+}
+
+template <class C, typename T, bool TA = false, bool TB = false>
 __device__ __forceinline__ void reg_tile(char* stage, const Problem& p, int64_t m0, int64_t n0,
                                          int64_t k0) {
   constexpr int VE = vec<T>();
+  if constexpr (TA || TB) {
+    if constexpr (TA) reg_tile_tr<C, T, C::BM>(stage, p.a, p.lda, m0, p.M, k0, p.K);
+    if constexpr (TB) reg_tile_tr<C, T, C::BN>(stage + C::BM * C::RB, p.b, p.ldb, n0, p.N, k0, p.K);
+    const int r0 = TA ? C::BM : 0, r1 = TB ? C::BM : C::BM + C::BN;  // K-contiguous rows left
+    for (int idx = r0 * C::GRAN + threadIdx.x; idx < r1 * C::GRAN; idx += C::THREADS) {
+      const int row = idx / C::GRAN, c = idx % C::GRAN;
+      const T* src = row < C::BM ? (const T*)p.a + imin(m0 + row, p.M - 1) * p.lda
+                                 : (const T*)p.b + imin(n0 + row - C::BM, p.N - 1) * p.ldb;
+      const int64_t k = k0 + c * VE;
+      Pack<T, VE> pk;
+#pragma unroll
+      for (int e = 0; e < VE; ++e) pk.v[e] = (k + e < p.K) ? src[k + e] : (T)0.f;
+      *reinterpret_cast<Pack<T, VE>*>(stage + swz<C>(row, c)) = pk;
+    }
+    return;
+  }
   for (int idx = threadIdx.x; idx < (C::BM + C::BN) * C::GRAN; idx += C::THREADS) {
     const int row = idx / C::GRAN, c = idx % C::GRAN;
     const T* src;
@@ -206,21 +319,32 @@ struct NoHook {
 // fenced against the scheduler: left alone, the compiler reuses one
 // fragment buffer and waits on every read), and hook.step<S>() runs after
 // step S's MFMAs are issued.
-template <class C, typename T, class Hook, int S, class V>
+// A fragments (rows wm * WTM + 32 i ..) and B fragments (wn * WTN + 32 j ..)
+// of 16-deep step S, from either tile layout.
+template <class C, bool TA, class V>
+__device__ __forceinline__ V frag_a(const char* As, int wm, int i, int S) {
+  const int lane = threadIdx.x & 63;
+  if constexpr (TA) return frag_tr<C::BM, V>(As, wm * C::WTM + 32 * i, S);
+  else return *reinterpret_cast<const V*>(As + swz<C>(wm * C::WTM + 32 * i + (lane & 31), 2 * S + (lane >> 5)));
+}
+template <class C, bool TB, class V>
+__device__ __forceinline__ V frag_b(const char* Bs, int wn, int j, int S) {
+  const int lane = threadIdx.x & 63;
+  if constexpr (TB) return frag_tr<C::BN, V>(Bs, wn * C::WTN + 32 * j, S);
+  else return *reinterpret_cast<const V*>(Bs + swz<C>(wn * C::WTN + 32 * j + (lane & 31), 2 * S + (lane >> 5)));
+}
+
+template <class C, typename T, class Hook, int S, bool TA, bool TB, class V>
 __device__ __forceinline__ void mma_steps(const char* As, const char* Bs, Acc<C>& acc, int wm,
                                           int wn, V (&a)[2][C::MT], V (&b)[2][C::NT],
                                           const Hook& hook) {
   constexpr int KS = C::RB / 32;
   if constexpr (S < KS) {
-    const int lane = threadIdx.x & 63;
-    const int l32 = lane & 31, g = lane >> 5;
     if constexpr (S + 1 < KS) {
 #pragma unroll
-      for (int i = 0; i < C::MT; ++i)
-        a[(S + 1) & 1][i] = *reinterpret_cast<const V*>(As + swz<C>(wm * C::WTM + 32 * i + l32, 2 * (S + 1) + g));
+      for (int i = 0; i < C::MT; ++i) a[(S + 1) & 1][i] = frag_a<C, TA, V>(As, wm, i, S + 1);
 #pragma unroll
-      for (int j = 0; j < C::NT; ++j)
-        b[(S + 1) & 1][j] = *reinterpret_cast<const V*>(Bs + swz<C>(wn * C::WTN + 32 * j + l32, 2 * (S + 1) + g));
+      for (int j = 0; j < C::NT; ++j) b[(S + 1) & 1][j] = frag_b<C, TB, V>(Bs, wn, j, S + 1);
     }
     fence();
 #pragma unroll
@@ -229,7 +353,7 @@ __device__ __forceinline__ void mma_steps(const char* As, const char* Bs, Acc<C>
       for (int j = 0; j < C::NT; ++j) acc.t[i][j] = mma(a[S & 1][i], b[S & 1][j], acc.t[i][j]);
     hook.template step<S>();
     fence();
-    mma_steps<C, T, Hook, S + 1>(As, Bs, acc, wm, wn, a, b, hook);
+    mma_steps<C, T, Hook, S + 1, TA, TB>(As, Bs, acc, wm, wn, a, b, hook);
   }
 }
 
@@ -244,24 +368,23 @@ __device__ __forceinline__ void all_steps(const Hook& hook) {
 // hook.step<s>() runs after the MFMAs of 16-deep step s are issued (the
 // 2-stage loop issues the next tile's DMAs there, spread over the tile
 // instead of in one burst while the MFMA pipe waits)
-template <class C, typename T, class Hook = NoHook>
+template <class C, typename T, class Hook = NoHook, bool TA = false, bool TB = false>
 __device__ __forceinline__ void compute_tile(const char* stage, Acc<C>& acc, int wm, int wn,
                                              const Hook& hook = Hook()) {
   const char* As = stage;
   const char* Bs = stage + C::BM * C::RB;
   const int lane = threadIdx.x & 63;
   const int l32 = lane & 31, g = lane >> 5;
+  static_assert(sizeof(T) == 2 || (!TA && !TB), "MN-contiguous operands: 16-bit types only");
   if constexpr (sizeof(T) == 2) {
     typedef typename FragOf<T>::V V;
     V a[2][C::MT], b[2][C::NT];
 #pragma unroll
-    for (int i = 0; i < C::MT; ++i)
-      a[0][i] = *reinterpret_cast<const V*>(As + swz<C>(wm * C::WTM + 32 * i + l32, g));
+    for (int i = 0; i < C::MT; ++i) a[0][i] = frag_a<C, TA, V>(As, wm, i, 0);
 #pragma unroll
-    for (int j = 0; j < C::NT; ++j)
-      b[0][j] = *reinterpret_cast<const V*>(Bs + swz<C>(wn * C::WTN + 32 * j + l32, g));
+    for (int j = 0; j < C::NT; ++j) b[0][j] = frag_b<C, TB, V>(Bs, wn, j, 0);
     fence();
-    mma_steps<C, T, Hook, 0>(As, Bs, acc, wm, wn, a, b, hook);
+    mma_steps<C, T, Hook, 0, TA, TB>(As, Bs, acc, wm, wn, a, b, hook);
   } else {
     all_steps<C>(hook);  // no MFMA steps to spread over: the hook's work up front
     // fp32: exact FMAs; one float4 (one granule) per row and per column per step
@@ -315,7 +438,7 @@ __device__ __forceinline__ void tile_of(int64_t bid, int64_t n_blocks, int tiles
 
 // compute_tile hook: DMAs of the next K tile, DMA_PER_WAVE / KS of them
 // after each 16-deep step
-template <class C, typename T>
+template <class C, typename T, bool TA = false, bool TB = false>
 struct DmaSpread {
   char* st;
   const Problem* p;
@@ -325,16 +448,17 @@ struct DmaSpread {
     constexpr int KS = C::RB / 32, PER = (C::DMA_PER_WAVE + KS - 1) / KS;
     constexpr int Q0 = S * PER < C::DMA_PER_WAVE ? S * PER : C::DMA_PER_WAVE;
     constexpr int Q1 = Q0 + PER < C::DMA_PER_WAVE ? Q0 + PER : C::DMA_PER_WAVE;
-    if constexpr (Q0 < Q1) dma_tile<C, T, Q0, Q1>(st, *p, m0, n0, k0);
+    if constexpr (Q0 < Q1) dma_tile<C, T, Q0, Q1, TA, TB>(st, *p, m0, n0, k0);
   }
 };
 
 
-// Accumulate the (tm, tn) tile of A * B^T over all of K.  `smem` holds
-// C::SMEM_BYTES of LDS (1 KiB aligned).
-template <class C, typename T>
+// Accumulate the (tm, tn) tile of A * B^T over all of K (A, B in the
+// layouts TA, TB select).  `smem` holds C::SMEM_BYTES of LDS (1 KiB aligned).
+template <class C, typename T, bool TA = false, bool TB = false>
 __device__ __forceinline__ void mainloop(const Problem& p, int tm, int tn, char* smem,
                                          Acc<C>& acc) {
+  static_assert(!(TA || TB) || C::STAGES == 2, "MN-contiguous operands: the 2-stage DMA loop");
   // the wavefront index stays a per-lane value here: it is part of every
   // fragment's LDS address, which then folds into one VGPR base plus
   // immediate offsets (a scalar index costs an add per read: -12% measured)
@@ -349,12 +473,13 @@ __device__ __forceinline__ void mainloop(const Problem& p, int tm, int tn, char*
 
   const int64_t nfull = p.K / BK;
   if (p.K % BK != 0) {
-    reg_tile<C, T>(smem, p, m0, n0, nfull * BK);
+    reg_tile<C, T, TA, TB>(smem, p, m0, n0, nfull * BK);
     __syncthreads();
-    compute_tile<C, T>(smem, acc, wm, wn);
+    compute_tile<C, T, NoHook, TA, TB>(smem, acc, wm, wn);
     __syncthreads();
   }
   if constexpr (C::STAGES == 2 && !TRI_GEMM_DMA) {
+    static_assert(!TA && !TB, "register-staged loop: K-contiguous operands only");
     // register-staged double buffer: at step kt the global loads of tile
     // kt + 1 are in flight while tile kt is multiplied, then land in the
     // buffer read at step kt - 1
@@ -376,19 +501,21 @@ __device__ __forceinline__ void mainloop(const Problem& p, int tm, int tn, char*
   } else if constexpr (C::STAGES == 2) {
     // branch-free steady state: wait for tile kt, sync, prefetch tile kt + 1
     // into the buffer read at step kt - 1, compute tile kt
-    if (nfull > 0) dma_tile<C, T>(smem, p, m0, n0, 0);
+    if (nfull > 0) dma_tile<C, T, 0, C::DMA_PER_WAVE, TA, TB>(smem, p, m0, n0, 0);
     for (int64_t kt = 0; kt + 1 < nfull; ++kt) {
       wait_vmcnt<0>();
       __syncthreads();
       // the next tile's DMAs, spread over the 16-deep steps
-      const DmaSpread<C, T> spread{smem + (int)((kt + 1) & 1) * C::STAGE_BYTES, &p, m0, n0,
-                                   (kt + 1) * BK};
-      compute_tile<C, T>(smem + (int)(kt & 1) * C::STAGE_BYTES, acc, wm, wn, spread);
+      const DmaSpread<C, T, TA, TB> spread{smem + (int)((kt + 1) & 1) * C::STAGE_BYTES, &p, m0,
+                                           n0, (kt + 1) * BK};
+      compute_tile<C, T, DmaSpread<C, T, TA, TB>, TA, TB>(smem + (int)(kt & 1) * C::STAGE_BYTES,
+                                                          acc, wm, wn, spread);
     }
     if (nfull > 0) {
       wait_vmcnt<0>();
       __syncthreads();
-      compute_tile<C, T>(smem + (int)((nfull - 1) & 1) * C::STAGE_BYTES, acc, wm, wn);
+      compute_tile<C, T, NoHook, TA, TB>(smem + (int)((nfull - 1) & 1) * C::STAGE_BYTES, acc, wm,
+                                         wn);
     }
   } else {
 #pragma unroll

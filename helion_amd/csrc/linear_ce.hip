@@ -17,21 +17,16 @@
 //   lce_fwd_rows       per token: combine the vocab-block partials online into
 //                      lse, nll; per-block partial sums of nll and counts;
 //   lce_fwd_finalize   one block: loss = sum(nll) / count in a fixed order.
-// Backward, per vocab chunk of Vc rows (bounded G memory):
-//   lce_g_kernel       recompute S^T for the chunk, epilogue
+// Backward (16-bit inputs), per vocab chunk of Vc rows (G of one chunk fits
+// a 1 GiB workspace; nothing of size N x V is kept from the forward):
+//   lce_g_kernel       recompute S^T for the chunk on the GEMM core, epilogue
 //                      G = (exp(S - lse) - onehot) * grad_out / count (0 for
-//                      ignored rows), written as G^T [Vc, N] and G [N, Vc];
-//   dH (+)= G W_c      NT GEMM with B = W^T (made once per backward);
-//   dW_c = G^T H       NT GEMM with B = H^T, the full token reduction inside
-//                      one GEMM, stored once in the weight dtype.
-// Backward from kept probabilities (16-bit inputs, when the caller can hold an
-// [N, V] 16-bit buffer from the forward to the backward): the forward epilogue
-// also stores p~ = exp(logit - m_b) in fp16 (the terms of its sum, m_b the
-// max over the logit's 256-row vocab tile, so p~ is in [0, 1]); the backward
-// turns that buffer into G in place with one streaming pass
-// (lce_g_from_probs) instead of recomputing the logits GEMM, and dH, dW are
-// the same two GEMMs.  The target entry, where p - 1 would cancel, is taken
-// from the fp32 target logit instead of p~.
+//                      ignored rows), written as G [N, Vc] in the input dtype;
+//   dW_c = G^T H       GEMM with both operands MN-contiguous (G and H read in
+//                      place through transposing LDS reads), the full token
+//                      reduction inside one product, stored once;
+//   dH (+)= G W_c      GEMM with W_c MN-contiguous, fp32 accumulation across
+//                      chunks, rounded once after the last.
 // All reductions are in a fixed order: results are bitwise reproducible.
 #include <math.h>
 
@@ -53,7 +48,7 @@ constexpr int kMaxBM = 256;  // largest row tile of any configuration
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kRowsBlock = 256;        // threads of lce_fwd_rows
 constexpr int kRowsSplit = 8;          // threads per token in lce_fwd_rows
-constexpr int64_t kGBudget = (int64_t)1 << 30;  // bytes for G and G^T of one chunk
+constexpr int64_t kGBudget = (int64_t)1 << 30;  // bytes of G for one vocabulary chunk
 
 template <typename TT>
 __device__ __forceinline__ int64_t load_target(const TT* t, int64_t n) {
@@ -128,8 +123,7 @@ struct FwdArgs {
   float* pmax;         // [tiles_v, N]
   float* psum;         // [tiles_v, N]
   float* tlogit;       // [N]
-  uint16_t* probs;     // [N, ld_p] fp16 p~, or null
-  int64_t N, D, V, ld, ld_p;
+  int64_t N, D, V, ld;
   int tiles_v, tiles_n;
 };
 
@@ -150,8 +144,6 @@ lce_fwd_kernel(FwdArgs a) {
   const int wm = wave / C::WN, wn = wave % C::WN;
   const int64_t v0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
   const TT* target = (const TT*)a.target;
-  constexpr bool kKeep = sizeof(T) == 2 && C::BM * 2 == 512 && C::BM * C::BN * 2 <= C::SMEM_BYTES;
-  const bool keep = kKeep && a.probs != nullptr;
 
   float mx[C::NT];
 #pragma unroll
@@ -184,18 +176,8 @@ lce_fwd_kernel(FwdArgs a) {
 #pragma unroll
     for (int i = 0; i < C::MT; ++i)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        float e4[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = 4 * rr + e;
-          e4[e] = v0 + acc_row<C>(wm, i, r, g) < a.V ? fast_exp2(acc.t[i][j][r] * kLog2e - ms) : 0.f;
-          s += e4[e];
-        }
-        if constexpr (kKeep) {
-          if (keep) stage_put4(smem, col, acc_row<C>(wm, i, 4 * rr, g), pack4<f16_t>(e4));
-        }
-      }
+      for (int r = 0; r < 16; ++r)
+        if (v0 + acc_row<C>(wm, i, r, g) < a.V) s += fast_exp2(acc.t[i][j][r] * kLog2e - ms);
     s += __shfl_xor(s, 32, 64);
     if (g == 0) red[wm][col] = s;
     // the target logit: written by the single lane that holds its row
@@ -225,10 +207,6 @@ lce_fwd_kernel(FwdArgs a) {
         a.psum[(int64_t)tm * a.N + n] = s;
       }
     }
-  }
-  // the staged p~ tile is complete since the barrier above
-  if constexpr (kKeep) {
-    if (keep) stage_out<C::THREADS, C::BN>(smem, a.probs, a.ld_p, n0, v0, a.N, a.V);
   }
 }
 
@@ -428,44 +406,9 @@ lce_g_kernel(GArgs a) {
   }
 }
 
-// G in place over the fp16 p~ buffer the forward kept (see the top of this
-// file): G[n, v] = (p~[n, v] * exp(m_b - lse[n]) - [v == target[n]]) * coef,
-// coef = grad_out / n_valid (0 for ignored rows), stored in T over the same
-// 2-byte entries; the target entry uses exp(target logit - lse) instead of p~.
-// Entries past V in the row padding are rewritten with values nobody reads.
-constexpr int64_t kProbsChunk = 256 * 8 * 2;  // entries of one row per block
-
-template <typename T, typename TT>
-__global__ void __launch_bounds__(256)
-lce_g_from_probs(const float* __restrict__ grad_out, const float* __restrict__ n_valid,
-                 const TT* __restrict__ target, int64_t ignore_index, const float* __restrict__ lse,
-                 const float* __restrict__ pmax, const float* __restrict__ tlogit,
-                 uint16_t* __restrict__ buf, int64_t ld, int64_t N, int64_t V,
-                 int64_t chunks_per_row, int tile_rows) {
-  static_assert(sizeof(T) == 2, "16-bit G");
-  const int64_t row = blockIdx.x / chunks_per_row;
-  const int64_t c0 = (blockIdx.x - row * chunks_per_row) * kProbsChunk;
-  const int64_t c1 = min(c0 + kProbsChunk, V);
-  const int64_t t = load_target(target, row);
-  const float coef = t == ignore_index ? 0.f : grad_out[0] / n_valid[0];
-  const float l2 = lse[row] * kLog2e;
-  uint16_t* p = buf + row * ld;
-  for (int64_t e = c0 + (int64_t)threadIdx.x * 8; e < c1; e += 256 * 8) {
-    // 8 entries never straddle a vocab tile (tile_rows is a multiple of 8)
-    const float f = fast_exp2(pmax[(e / tile_rows) * N + row] * kLog2e - l2);
-    float gv[8];
-    unpack<f16_t>(ld16_nt(p + e), gv);
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const float pr = e + i == t ? fast_exp2(tlogit[row] * kLog2e - l2) : gv[i] * f;
-      gv[i] = (pr - (e + i == t ? 1.f : 0.f)) * coef;
-    }
-    st16_nt(p + e, pack<T>(gv));
-  }
-}
-
-// Plain GEMM: out[m, n] = (acc_in[m, n] if acc_in) + (A B^T)[m, n].
-template <typename T, typename OT>
+// Plain GEMM: out[m, n] = (acc_in[m, n] if acc_in) + (A B^T)[m, n], A and B
+// in the layouts TA, TB select (gemm_nt.h).
+template <typename T, typename OT, bool TA, bool TB>
 __global__ void __launch_bounds__(CfgT<T>::THREADS)
 gemm_store_kernel(gemm::Problem p, const float* acc_in, OT* out, int64_t ldc, int tiles_m,
                   int tiles_n) {
@@ -474,7 +417,7 @@ gemm_store_kernel(gemm::Problem p, const float* acc_in, OT* out, int64_t ldc, in
   int tm, tn;
   gemm::tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
   Acc<C> acc;
-  gemm::mainloop<C, T>(p, tm, tn, smem, acc);
+  gemm::mainloop<C, T, TA, TB>(p, tm, tn, smem, acc);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int l32 = lane & 31, g = lane >> 5;
   const int wm = wave / C::WN, wn = wave % C::WN;
@@ -494,27 +437,6 @@ gemm_store_kernel(gemm::Problem p, const float* acc_in, OT* out, int64_t ldc, in
           out[m * ldc + n] = from_f32<OT>(v);
         }
       }
-  }
-}
-
-// out[c, r] = in[r, c] for an R x C matrix (64 x 64 tiles through LDS).
-template <typename E>
-__global__ void __launch_bounds__(256)
-transpose_kernel(const E* __restrict__ in, int64_t ld_in, E* __restrict__ out, int64_t ld_out,
-                 int64_t R, int64_t C) {
-  __shared__ E tile[64][65];
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;
-  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int64_t r = r0 + ty + 4 * k, c = c0 + tx;
-    if (r < R && c < C) tile[ty + 4 * k][tx] = in[r * ld_in + c];
-  }
-  __syncthreads();
-#pragma unroll
-  for (int k = 0; k < 16; ++k) {
-    const int64_t c = c0 + ty + 4 * k, r = r0 + tx;
-    if (r < R && c < C) out[c * ld_out + r] = tile[tx][ty + 4 * k];
   }
 }
 
@@ -547,22 +469,23 @@ FwdLayout fwd_layout(int64_t N, int64_t V, int bm, int bn) {
 }
 
 struct BwdLayout {
-  int64_t chunk, n_chunks, ld_wt, ld_ht, ld_g;
-  size_t n_valid, wt, ht, gm, gt, dh_acc, total;
+  int64_t chunk, n_chunks, ld_g;
+  size_t n_valid, gm, dh_acc, total;
 };
 
-BwdLayout bwd_layout(int64_t N, int64_t D, int64_t V, int esz, bool need_dh, bool need_dw,
-                     int64_t chunk_rows) {
+// The backward's workspace: the count of valid rows, G of one vocabulary
+// chunk [N, ld_g] (chunk rows chosen so that G fits kGBudget bytes, or
+// chunk_rows rounded up to the row tile) and, with more than one chunk, the
+// fp32 dH accumulator [N, D].
+BwdLayout bwd_layout(int64_t N, int64_t D, int64_t V, int esz, bool need_dh, int64_t chunk_rows) {
   BwdLayout L;
   const int64_t vpad = round_up(V, kMaxBM);
   int64_t chunk = chunk_rows > 0 ? round_up(chunk_rows, kMaxBM)
-                                 : (kGBudget / std::max<int64_t>(1, 2 * N * esz)) / kMaxBM * kMaxBM;
+                                 : (kGBudget / std::max<int64_t>(1, N * esz)) / kMaxBM * kMaxBM;
   chunk = std::max<int64_t>(kMaxBM, std::min<int64_t>(chunk, vpad));
   L.chunk = chunk;
   L.n_chunks = cdiv(V, chunk);
-  L.ld_wt = round_up(V, 8);
-  L.ld_ht = round_up(N, 8);
-  L.ld_g = round_up(chunk, 8);
+  L.ld_g = round_up(std::min<int64_t>(chunk, V), 8);
   size_t off = 0;
   auto take = [&](size_t bytes) {
     const size_t at = off;
@@ -570,10 +493,7 @@ BwdLayout bwd_layout(int64_t N, int64_t D, int64_t V, int esz, bool need_dh, boo
     return at;
   };
   L.n_valid = take(4);
-  L.wt = need_dh ? take((size_t)D * L.ld_wt * esz) : 0;
-  L.ht = need_dw ? take((size_t)D * L.ld_ht * esz) : 0;
-  L.gm = need_dh ? take((size_t)N * L.ld_g * esz) : 0;
-  L.gt = need_dw ? take((size_t)chunk * L.ld_ht * esz) : 0;
+  L.gm = take((size_t)N * L.ld_g * esz);
   L.dh_acc = (need_dh && L.n_chunks > 1) ? take((size_t)N * D * 4) : 0;
   L.total = off;
   return L;
@@ -592,33 +512,25 @@ int check_sizes(int64_t N, int64_t D, int64_t V, int dtype) {
   return TRI_OK;
 }
 
-template <typename T>
+template <typename T, bool TA, bool TB>
 int gemm_store(const gemm::Problem& p, const float* acc_in, void* out, bool out_f32, int64_t ldc,
                hipStream_t st) {
   typedef CfgT<T> C;
   const int tiles_m = (int)cdiv(p.M, C::BM), tiles_n = (int)cdiv(p.N, C::BN);
   const unsigned blocks = (unsigned)((int64_t)tiles_m * tiles_n);
   if (out_f32)
-    gemm_store_kernel<T, float><<<blocks, C::THREADS, 0, st>>>(p, acc_in, (float*)out, ldc,
-                                                               tiles_m, tiles_n);
+    gemm_store_kernel<T, float, TA, TB><<<blocks, C::THREADS, 0, st>>>(p, acc_in, (float*)out,
+                                                                       ldc, tiles_m, tiles_n);
   else
-    gemm_store_kernel<T, T><<<blocks, C::THREADS, 0, st>>>(p, acc_in, (T*)out, ldc, tiles_m,
-                                                           tiles_n);
+    gemm_store_kernel<T, T, TA, TB><<<blocks, C::THREADS, 0, st>>>(p, acc_in, (T*)out, ldc,
+                                                                   tiles_m, tiles_n);
   return check_launch("linear_ce gemm");
-}
-
-template <typename E>
-int transpose(const void* in, int64_t ld_in, void* out, int64_t ld_out, int64_t R, int64_t C,
-              hipStream_t st) {
-  const dim3 grid((unsigned)cdiv(C, 64), (unsigned)cdiv(R, 64));
-  transpose_kernel<E><<<grid, 256, 0, st>>>((const E*)in, ld_in, (E*)out, ld_out, R, C);
-  return check_launch("linear_ce transpose");
 }
 
 template <typename T, typename TT>
 int fwd_impl(const void* hidden, const void* weight, const void* target, int64_t ignore_index,
              float* loss, float* lse, float* n_valid, void* ws, size_t ws_bytes, int64_t N,
-             int64_t D, int64_t V, void* probs, int64_t ld_p, hipStream_t st) {
+             int64_t D, int64_t V, hipStream_t st) {
   typedef CfgT<T> C;
   const FwdLayout L = fwd_layout(N, V, C::BM, C::BN);
   if (ws_bytes < L.total) return fail(TRI_EINVAL, "linear_ce forward: workspace too small");
@@ -628,8 +540,7 @@ int fwd_impl(const void* hidden, const void* weight, const void* target, int64_t
   a.pmax = (float*)(w + L.pmax);
   a.psum = (float*)(w + L.psum);
   a.tlogit = (float*)(w + L.tlogit);
-  a.probs = (uint16_t*)probs;
-  a.N = N; a.D = D; a.V = V; a.ld = D; a.ld_p = ld_p;
+  a.N = N; a.D = D; a.V = V; a.ld = D;
   a.tiles_v = L.tiles_v; a.tiles_n = L.tiles_n;
   // a target outside [0, V) that is not ignore_index leaves NaN here (-> NaN loss);
   // a fill kernel rather than a memset node, so the call can be graph-captured
@@ -651,26 +562,17 @@ int bwd_impl(const float* grad_out, const void* hidden, const void* weight, cons
              int64_t ignore_index, const float* lse, void* dhidden, void* dweight, void* ws,
              size_t ws_bytes, int64_t N, int64_t D, int64_t V, int64_t chunk_rows,
              hipStream_t st) {
+  static_assert(sizeof(T) == 2, "16-bit backward (MN-contiguous GEMM operands)");
   const bool need_dh = dhidden != nullptr, need_dw = dweight != nullptr;
   if (!need_dh && !need_dw) return TRI_OK;
-  const BwdLayout L = bwd_layout(N, D, V, (int)sizeof(T), need_dh, need_dw, chunk_rows);
+  const BwdLayout L = bwd_layout(N, D, V, (int)sizeof(T), need_dh, chunk_rows);
   if (ws_bytes < L.total) return fail(TRI_EINVAL, "linear_ce backward: workspace too small");
   char* w = (char*)ws;
   float* n_valid = (float*)(w + L.n_valid);
   lce_count_valid<TT><<<1, 1024, 0, st>>>((const TT*)target, N, ignore_index, n_valid);
   if (int e = check_launch("linear_ce count")) return e;
-  typedef typename std::conditional<sizeof(T) == 4, uint32_t, uint16_t>::type E;
-  T* wt = need_dh ? (T*)(w + L.wt) : nullptr;
-  T* ht = need_dw ? (T*)(w + L.ht) : nullptr;
-  T* gm = need_dh ? (T*)(w + L.gm) : nullptr;
-  T* gt = need_dw ? (T*)(w + L.gt) : nullptr;
+  T* gm = (T*)(w + L.gm);
   float* dh_acc = L.dh_acc ? (float*)(w + L.dh_acc) : nullptr;
-  if (need_dh) {
-    if (int e = transpose<E>(weight, D, wt, L.ld_wt, V, D, st)) return e;
-  }
-  if (need_dw) {
-    if (int e = transpose<E>(hidden, D, ht, L.ld_ht, N, D, st)) return e;
-  }
   for (int64_t c = 0; c < L.n_chunks; ++c) {
     const int64_t vc0 = c * L.chunk;
     const int64_t vc = std::min<int64_t>(L.chunk, V - vc0);
@@ -681,27 +583,30 @@ int bwd_impl(const float* grad_out, const void* hidden, const void* weight, cons
     ga.lse = lse;
     ga.grad_out = grad_out;
     ga.n_valid = n_valid;
-    ga.gt = gt;
+    ga.gt = nullptr;
     ga.gm = gm;
     ga.N = N; ga.D = D; ga.Vc = vc; ga.ld = D;
-    ga.ld_gt = L.ld_ht; ga.ld_g = L.ld_g; ga.vc0 = vc0; ga.ignore_index = ignore_index;
+    ga.ld_gt = 0; ga.ld_g = L.ld_g; ga.vc0 = vc0; ga.ignore_index = ignore_index;
     ga.tiles_v = (int)cdiv(vc, CfgT<T>::BM);
     ga.tiles_n = (int)cdiv(N, CfgT<T>::BN);
     lce_g_kernel<T, TT><<<(unsigned)((int64_t)ga.tiles_v * ga.tiles_n), CfgT<T>::THREADS, 0, st>>>(ga);
     if (int e = check_launch("linear_ce gradient tile")) return e;
-    if (need_dh) {
-      // dH[N, D] (+)= G[N, vc] * W[vc0:vc0+vc, :]  ==  A = G, B = W^T[:, vc0:]
-      gemm::Problem p{gm, wt + vc0, L.ld_g, L.ld_wt, N, D, vc};
-      const bool last = c + 1 == L.n_chunks;
-      const float* in = c > 0 ? dh_acc : nullptr;
-      if (int e = last ? gemm_store<T>(p, in, dhidden, false, D, st)
-                       : gemm_store<T>(p, in, dh_acc, true, D, st))
+    const T* wc = (const T*)weight + vc0 * D;
+    if (need_dw) {
+      // dW[vc0 : vc0 + vc, :] = G^T H: A[v][n] = G[n][v] and B[d][n] = H[n][d],
+      // both MN-contiguous; the whole token reduction in one product, rounded once
+      gemm::Problem p{gm, hidden, L.ld_g, D, vc, D, N};
+      if (int e = gemm_store<T, true, true>(p, nullptr, (T*)dweight + vc0 * D, false, D, st))
         return e;
     }
-    if (need_dw) {
-      // dW[vc0:vc0+vc, :] = G^T[vc, N] * H[N, D]  ==  A = G^T, B = H^T
-      gemm::Problem p{gt, ht, L.ld_ht, L.ld_ht, vc, D, N};
-      if (int e = gemm_store<T>(p, nullptr, (T*)dweight + vc0 * D, false, D, st)) return e;
+    if (need_dh) {
+      // dH[N, D] (+)= G W_c: A = G (K-contiguous), B[d][v] = W_c[v][d] (MN-contiguous)
+      gemm::Problem p{gm, wc, L.ld_g, D, N, D, vc};
+      const bool last = c + 1 == L.n_chunks;
+      const float* in = c > 0 ? dh_acc : nullptr;
+      if (int e = last ? gemm_store<T, false, true>(p, in, dhidden, false, D, st)
+                       : gemm_store<T, false, true>(p, in, dh_acc, true, D, st))
+        return e;
     }
   }
   return TRI_OK;
@@ -761,70 +666,17 @@ extern "C" int tritium_linear_ce_fwd(const void* hidden, const void* weight, con
   TRI_DISPATCH_TARGET(target_kind, TT,
     TRI_DISPATCH_FLOAT(dtype, T,
       return fwd_impl<T, TT>(hidden, weight, target, ignore_index, loss, lse, n_valid, workspace,
-                             workspace_bytes, n_rows, hidden_size, vocab, nullptr, 0, st)));
+                             workspace_bytes, n_rows, hidden_size, vocab, st)));
   return TRI_OK;
-}
-
-extern "C" int tritium_linear_ce_fwd_probs(const void* hidden, const void* weight,
-                                           const void* target, int target_kind,
-                                           int64_t ignore_index, float* loss, float* lse,
-                                           float* n_valid, void* probs, int64_t ld_probs,
-                                           void* workspace, size_t workspace_bytes,
-                                           int64_t n_rows, int64_t hidden_size, int64_t vocab,
-                                           int dtype, void* stream) {
-  if (int e = check_sizes(n_rows, hidden_size, vocab, dtype)) return e;
-  if (dtype == kF32) return fail(TRI_EINVAL, "linear_ce fwd_probs: 16-bit inputs only");
-  if (ld_probs < vocab || ld_probs % 8 != 0)
-    return fail(TRI_EINVAL, "linear_ce fwd_probs: ld_probs %lld must be >= vocab and a multiple of 8",
-                (long long)ld_probs);
-  if (n_rows == 0) return TRI_OK;
-  if (!aligned16(hidden) || !aligned16(weight) || !aligned16(probs))
-    return fail(TRI_EINVAL, "linear_ce: hidden, weight and probs must be 16-byte aligned");
-  hipStream_t st = (hipStream_t)stream;
-  TRI_DISPATCH_TARGET(target_kind, TT,
-    TRI_DISPATCH_FLOAT(dtype, T,
-      return fwd_impl<T, TT>(hidden, weight, target, ignore_index, loss, lse, n_valid, workspace,
-                             workspace_bytes, n_rows, hidden_size, vocab, probs, ld_probs, st)));
-  return TRI_OK;
-}
-
-extern "C" int tritium_linear_ce_grad_from_probs(const float* grad_out, const float* n_valid,
-                                                 const void* target, int target_kind,
-                                                 int64_t ignore_index, const float* lse,
-                                                 const void* fwd_workspace,
-                                                 size_t fwd_workspace_bytes, void* probs,
-                                                 int64_t ld_probs, int64_t n_rows, int64_t vocab,
-                                                 int dtype, void* stream) {
-  if (n_rows < 0 || vocab <= 0) return fail(TRI_EINVAL, "linear_ce grad_from_probs: bad sizes");
-  if (dtype == kF32) return fail(TRI_EINVAL, "linear_ce grad_from_probs: 16-bit inputs only");
-  if (ld_probs < vocab || ld_probs % 8 != 0 || !aligned16(probs))
-    return fail(TRI_EINVAL, "linear_ce grad_from_probs: probs must be 16-byte aligned, ld_probs >= vocab and a multiple of 8");
-  if (n_rows == 0) return TRI_OK;
-  typedef CfgT<bf16_t> C;
-  const FwdLayout L = fwd_layout(n_rows, vocab, C::BM, C::BN);
-  if (fwd_workspace_bytes < L.total)
-    return fail(TRI_EINVAL, "linear_ce grad_from_probs: forward workspace too small");
-  const int64_t chunks = cdiv(vocab, kProbsChunk);
-  if (n_rows * chunks > 0x7fffffffLL) return fail(TRI_EINVAL, "linear_ce grad_from_probs: grid too large");
-  const char* w = (const char*)fwd_workspace;
-  hipStream_t st = (hipStream_t)stream;
-  TRI_DISPATCH_TARGET(target_kind, TT,
-    TRI_DISPATCH_FLOAT(dtype, T, if constexpr (sizeof(T) == 2) {
-      lce_g_from_probs<T, TT><<<(unsigned)(n_rows * chunks), 256, 0, st>>>(
-          grad_out, n_valid, (const TT*)target, ignore_index, lse, (const float*)(w + L.pmax),
-          (const float*)(w + L.tlogit), (uint16_t*)probs, ld_probs, n_rows, vocab, chunks, C::BM);
-    }));
-  return check_launch("linear_ce gradient from kept probabilities");
 }
 
 extern "C" size_t tritium_linear_ce_bwd_workspace_size(int64_t n_rows, int64_t hidden_size,
                                                        int64_t vocab, int dtype,
                                                        int need_dhidden, int need_dweight,
                                                        int64_t chunk_rows) {
-  if (n_rows <= 0 || vocab <= 0 || hidden_size <= 0) return 0;
-  return bwd_layout(n_rows, hidden_size, vocab, dtype == kF32 ? 4 : 2, need_dhidden != 0,
-                    need_dweight != 0, chunk_rows)
-      .total;
+  (void)need_dweight;
+  if (n_rows <= 0 || vocab <= 0 || hidden_size <= 0 || dtype == kF32) return 0;
+  return bwd_layout(n_rows, hidden_size, vocab, 2, need_dhidden != 0, chunk_rows).total;
 }
 
 extern "C" int tritium_linear_ce_bwd(const float* grad_out, const void* hidden, const void* weight,
@@ -834,16 +686,18 @@ extern "C" int tritium_linear_ce_bwd(const float* grad_out, const void* hidden, 
                                      int64_t hidden_size, int64_t vocab, int64_t chunk_rows,
                                      int dtype, void* stream) {
   if (int e = check_sizes(n_rows, hidden_size, vocab, dtype)) return e;
+  if (dtype == kF32) return fail(TRI_EINVAL, "linear_ce backward: 16-bit inputs only");
   if (n_rows == 0) return TRI_OK;
   if (!aligned16(hidden) || !aligned16(weight) || (dhidden && !aligned16(dhidden)) ||
       (dweight && !aligned16(dweight)) || !aligned16(workspace))
     return fail(TRI_EINVAL, "linear_ce: buffers must be 16-byte aligned");
   hipStream_t st = (hipStream_t)stream;
   TRI_DISPATCH_TARGET(target_kind, TT,
-    TRI_DISPATCH_FLOAT(dtype, T,
+    TRI_DISPATCH_FLOAT(dtype, T, if constexpr (sizeof(T) == 2) {
       return bwd_impl<T, TT>(grad_out, hidden, weight, target, ignore_index, lse, dhidden,
                              dweight, workspace, workspace_bytes, n_rows, hidden_size, vocab,
-                             chunk_rows, st)));
+                             chunk_rows, st);
+    }));
   return TRI_OK;
 }
 

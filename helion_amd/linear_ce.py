@@ -14,9 +14,13 @@ Differences, each a correction the north star asks for:
   the number of the other rows, as ``F.cross_entropy`` does.  The reference
   has no such argument and yields ``inf`` for a -100 target
   (cross_entropy.py:240-244); with no ignored target both agree;
-* the logits are never written to memory in the forward, and the backward
-  accumulates ``dweight`` over all rows in fp32 before one rounding (the
-  reference accumulates it in the weight dtype chunk by chunk, 947-957);
+* the logits are never written to memory in the forward (only the fp32
+  logsumexp is kept for the backward); the 16-bit backward recomputes them
+  per vocabulary chunk on the library's MFMA GEMM core, holds only that
+  chunk's gradient of the logits (at most 1 GiB) and runs dH and dW on the
+  same core; ``dweight`` is accumulated over all rows in fp32 before one
+  rounding (the reference accumulates it in the weight dtype chunk by chunk,
+  947-957);
 * a target outside ``[0, vocab)`` that is not ``ignore_index`` gives a NaN
   loss instead of a device assert or ``inf``.
 """
@@ -105,42 +109,20 @@ def _target_kind(target: torch.Tensor) -> int:
     return 1 if target.dtype == torch.int32 else 2
 
 
-def _keep_fits(n_rows: int, vocab_size: int, dtype: torch.dtype) -> bool:
-    """Whether the autograd forward keeps the [n_rows, vocab] fp16 buffer for
-    the backward: 16-bit inputs whose buffer fits the gradient-tile budget
-    (the backward's G tiles need the same memory anyway)."""
-    ld = -(-vocab_size // 8) * 8
-    return dtype in (torch.float16, torch.bfloat16) and 0 < n_rows * ld * 2 <= _G_CHUNK_BYTES
-
-
-def _linear_cross_entropy_forward(hidden, weight, target, ignore_index: int = IGNORE_INDEX,
-                                  keep: bool = False):
-    """cross_entropy.py:563-640: returns ``(loss, logsumexp)``; with ``keep``
-    returns ``(loss, logsumexp, kept)``, ``kept`` the state
-    ``tritium_linear_ce_fwd_probs`` leaves for :func:`_backward_from_probs`."""
+def _linear_cross_entropy_forward(hidden, weight, target, ignore_index: int = IGNORE_INDEX):
+    """cross_entropy.py:563-640: returns ``(loss, logsumexp)``."""
     n_rows, hidden_size, vocab_size = _check_linear_cross_entropy_inputs(hidden, weight, target)
     dev = hidden.device
     loss = torch.zeros((), device=dev, dtype=torch.float32)
     lse = torch.empty((n_rows,), device=dev, dtype=torch.float32)
     if n_rows == 0:
-        return (loss, lse, None) if keep else (loss, lse)
+        return loss, lse
     h2 = _kernel_operand(hidden.reshape(n_rows, hidden_size))
     w2 = _kernel_operand(weight)
     ws_bytes = _lib.lib().tritium_linear_ce_fwd_workspace_size(
         n_rows, vocab_size, _lib.dtype_code(hidden.dtype)
     )
     ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
-    if keep:
-        ld_p = -(-vocab_size // 8) * 8
-        probs = torch.empty((n_rows, ld_p), device=dev, dtype=torch.float16)
-        n_valid = torch.empty((), device=dev, dtype=torch.float32)
-        _lib.call(
-            "tritium_linear_ce_fwd_probs", h2.data_ptr(), w2.data_ptr(), target.data_ptr(),
-            _target_kind(target), int(ignore_index), loss.data_ptr(), lse.data_ptr(),
-            n_valid.data_ptr(), probs.data_ptr(), ld_p, ws.data_ptr(), ws.numel(), n_rows,
-            h2.shape[-1], vocab_size, _lib.dtype_code(hidden.dtype), _lib.stream_of(hidden),
-        )
-        return loss, lse, (probs, ws, n_valid)
     _lib.call(
         "tritium_linear_ce_fwd",
         h2.data_ptr(),
@@ -162,150 +144,75 @@ def _linear_cross_entropy_forward(hidden, weight, target, ignore_index: int = IG
     return loss, lse
 
 
-# gradient-of-logits tile per chunk: one chunk at both benchmark shapes (2.1 GB
-# at N = 8192, V = 128256), so dH is a single GEMM with a 16-bit output and no
-# fp32 accumulation pass (measured 22.3 -> 21.9 ms against 1 GiB chunks)
-_G_CHUNK_BYTES = 4 << 30
-_mm_out_dtype: bool | None = None  # torch.mm(..., out_dtype=float32) available on this device
+# fp32 gradient-of-logits tile per chunk (the fp32 correctness path)
+_G_CHUNK_BYTES = 1 << 30
 
 
-def _mm_f32_into(acc: torch.Tensor, a: torch.Tensor, b: torch.Tensor) -> None:
-    """acc += a @ b with fp32 accumulation: one library GEMM with an fp32
-    output where torch offers it, else a 16-bit product added in fp32."""
-    global _mm_out_dtype
-    if _mm_out_dtype is not False:
-        try:
-            acc.add_(torch.mm(a, b, out_dtype=torch.float32))
-            _mm_out_dtype = True
-            return
-        except (RuntimeError, NotImplementedError, TypeError):
-            _mm_out_dtype = False
-    acc.add_(torch.mm(a, b))
-
-
-def _backward(grad_out, hidden_2d, weight, target_1d, lse, need_dh, need_dw, ignore_index,
-              chunk_rows: int = 0):
-    """Per vocabulary chunk: the HIP kernel recomputes the logits in registers
-    and writes only G = (softmax - onehot) * grad_out / n_valid
-    (``tritium_linear_ce_grad_logits``); dH += G W_c and dW_c = G^T H are
-    plain GEMMs on views of G, H and W (library GEMMs, no transposed copies).
-    dH accumulates over chunks in fp32; each dW chunk reduces over all rows
-    in one GEMM and is rounded once (cross_entropy.py:928-957 does the same
-    chunking with bf16 accumulation)."""
-    n_rows, hidden_size = hidden_2d.shape
-    vocab_size = weight.shape[0]
-    dev = hidden_2d.device
-    h2 = _kernel_operand(hidden_2d)
-    w2 = _kernel_operand(weight)
-    dp = h2.shape[-1]
+def _backward_f32(grad_out, h2, w2, target_1d, lse, need_dh, need_dw, ignore_index,
+                  chunk_rows: int = 0):
+    """fp32 inputs: per vocabulary chunk the HIP kernel recomputes the logits
+    (exact fp32 FMAs) and writes only G = (softmax - onehot) * grad_out /
+    n_valid (``tritium_linear_ce_grad_logits``); dH += G W_c and dW_c = G^T H
+    are fp32 library GEMMs on views (cross_entropy.py:928-957 does the same
+    chunking).  A correctness path: the MFMA contractions are 16-bit."""
+    n_rows, dp = h2.shape
+    vocab_size = w2.shape[0]
+    dev = h2.device
     g = grad_out.detach().to(device=dev, dtype=torch.float32).reshape(())
     n_valid = (target_1d != ignore_index).sum(dtype=torch.float32)
-    chunk = int(chunk_rows) if chunk_rows > 0 else max(256, (_G_CHUNK_BYTES // (2 * n_rows)) // 256 * 256)
+    chunk = int(chunk_rows) if chunk_rows > 0 else max(256, (_G_CHUNK_BYTES // (4 * n_rows)) // 256 * 256)
     chunk = min(chunk, vocab_size)
     ld_g = -(-chunk // 8) * 8
-    gbuf = torch.empty((n_rows, ld_g), device=dev, dtype=weight.dtype)
-    n_chunks = -(-vocab_size // chunk)
-    dh = dh32 = None
-    if need_dh:
-        if n_chunks == 1:
-            dh = torch.empty((n_rows, dp), device=dev, dtype=hidden_2d.dtype)
-        else:
-            dh32 = torch.zeros((n_rows, dp), device=dev, dtype=torch.float32)
-    dw = torch.empty((vocab_size, dp), device=dev, dtype=weight.dtype) if need_dw else None
-    for c in range(n_chunks):
-        v0 = c * chunk
+    gbuf = torch.empty((n_rows, ld_g), device=dev, dtype=torch.float32)
+    dh = torch.zeros((n_rows, dp), device=dev, dtype=torch.float32) if need_dh else None
+    dw = torch.empty((vocab_size, dp), device=dev, dtype=torch.float32) if need_dw else None
+    for v0 in range(0, vocab_size, chunk):
         vc = min(chunk, vocab_size - v0)
         _lib.call(
             "tritium_linear_ce_grad_logits", g.data_ptr(), n_valid.data_ptr(), h2.data_ptr(),
             w2.data_ptr(), target_1d.data_ptr(), _target_kind(target_1d), int(ignore_index),
             lse.data_ptr(), gbuf.data_ptr(), ld_g, n_rows, dp, vocab_size, v0, vc,
-            _lib.dtype_code(weight.dtype), _lib.stream_of(hidden_2d),
+            _lib.dtype_code(torch.float32), _lib.stream_of(h2),
         )
         gc = gbuf[:, :vc]
         if need_dh:
-            if dh is not None:
-                torch.mm(gc, w2[v0:v0 + vc], out=dh)
-            else:
-                _mm_f32_into(dh32, gc, w2[v0:v0 + vc])
+            dh.addmm_(gc, w2[v0:v0 + vc])
         if need_dw:
             torch.mm(gc.t(), h2, out=dw[v0:v0 + vc])
-    if dh32 is not None:
-        dh = dh32.to(hidden_2d.dtype)
-    if dp != hidden_size:
-        dh = dh[:, :hidden_size].contiguous() if dh is not None else None
-        dw = dw[:, :hidden_size].contiguous() if dw is not None else None
     return dh, dw
 
 
-def _backward_from_probs(grad_out, hidden_2d, weight, target_1d, lse, kept, need_dh, need_dw,
-                         ignore_index):
-    """Backward from the buffer the forward kept (``tritium_linear_ce_fwd_probs``):
-    ``tritium_linear_ce_grad_from_probs`` turns it into G in place with one
-    streaming pass (no logits recompute), then dH = G W and dW = G^T H are the
-    same library GEMMs as in :func:`_backward`.  Consumes ``kept``."""
-    probs, ws, n_valid = kept
-    n_rows, hidden_size = hidden_2d.shape
-    vocab_size = weight.shape[0]
-    dev = hidden_2d.device
-    g = grad_out.detach().to(device=dev, dtype=torch.float32).reshape(())
-    _lib.call(
-        "tritium_linear_ce_grad_from_probs", g.data_ptr(), n_valid.data_ptr(),
-        target_1d.data_ptr(), _target_kind(target_1d), int(ignore_index), lse.data_ptr(),
-        ws.data_ptr(), ws.numel(), probs.data_ptr(), probs.shape[1], n_rows, vocab_size,
-        _lib.dtype_code(weight.dtype), _lib.stream_of(hidden_2d),
-    )
-    gc = probs.view(weight.dtype)[:, :vocab_size]
-    h2 = _kernel_operand(hidden_2d)
-    w2 = _kernel_operand(weight)
-    dh = torch.mm(gc, w2) if need_dh else None
-    dw = torch.mm(gc.t(), h2) if need_dw else None
-    dp = h2.shape[-1]
-    if dp != hidden_size:
-        dh = dh[:, :hidden_size].contiguous() if dh is not None else None
-        dw = dw[:, :hidden_size].contiguous() if dw is not None else None
-    return dh, dw
-
-
-def _backward_capi(grad_out, hidden_2d, weight, target_1d, lse, need_dh, need_dw, ignore_index,
-                   chunk_rows: int = 0):
-    """The whole backward inside the library (``tritium_linear_ce_bwd``: the
-    same gradient tiles plus its own GEMM core for dH and dW) -- the entry a
-    C caller uses; the autograd path above hands the two plain GEMMs to the
-    GEMM library instead."""
+def _backward(grad_out, hidden_2d, weight, target_1d, lse, need_dh, need_dw, ignore_index,
+              chunk_rows: int = 0):
+    """cross_entropy.py:863-959.  16-bit inputs: the whole backward runs in the
+    library (``tritium_linear_ce_bwd``): per vocabulary chunk (its gradient of
+    the logits at most 1 GiB) the logits are recomputed on the MFMA GEMM
+    core and turned into G, then dW_c = G^T H and dH += G W_c run on the same
+    core reading G, H and W in place.  fp32 inputs: :func:`_backward_f32`."""
     n_rows, hidden_size = hidden_2d.shape
     vocab_size = weight.shape[0]
     dev = hidden_2d.device
     h2 = _kernel_operand(hidden_2d)
     w2 = _kernel_operand(weight)
     dp = h2.shape[-1]
-    dh = torch.empty((n_rows, dp), device=dev, dtype=hidden_2d.dtype) if need_dh else None
-    dw = torch.empty((vocab_size, dp), device=dev, dtype=weight.dtype) if need_dw else None
-    g = grad_out.detach().to(device=dev, dtype=torch.float32).reshape(())
-    ws_bytes = _lib.lib().tritium_linear_ce_bwd_workspace_size(
-        n_rows, dp, vocab_size, _lib.dtype_code(weight.dtype), int(need_dh), int(need_dw),
-        int(chunk_rows),
-    )
-    ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
-    _lib.call(
-        "tritium_linear_ce_bwd",
-        g.data_ptr(),
-        h2.data_ptr(),
-        w2.data_ptr(),
-        target_1d.data_ptr(),
-        _target_kind(target_1d),
-        int(ignore_index),
-        lse.data_ptr(),
-        _lib.ptr(dh),
-        _lib.ptr(dw),
-        ws.data_ptr(),
-        ws_bytes,
-        n_rows,
-        dp,
-        vocab_size,
-        int(chunk_rows),
-        _lib.dtype_code(weight.dtype),
-        _lib.stream_of(hidden_2d),
-    )
+    if weight.dtype == torch.float32:
+        dh, dw = _backward_f32(grad_out, h2, w2, target_1d, lse, need_dh, need_dw, ignore_index,
+                               chunk_rows)
+    else:
+        dh = torch.empty((n_rows, dp), device=dev, dtype=hidden_2d.dtype) if need_dh else None
+        dw = torch.empty((vocab_size, dp), device=dev, dtype=weight.dtype) if need_dw else None
+        g = grad_out.detach().to(device=dev, dtype=torch.float32).reshape(())
+        ws_bytes = _lib.lib().tritium_linear_ce_bwd_workspace_size(
+            n_rows, dp, vocab_size, _lib.dtype_code(weight.dtype), int(need_dh), int(need_dw),
+            int(chunk_rows),
+        )
+        ws = torch.empty((max(ws_bytes, 1),), device=dev, dtype=torch.uint8)
+        _lib.call(
+            "tritium_linear_ce_bwd", g.data_ptr(), h2.data_ptr(), w2.data_ptr(),
+            target_1d.data_ptr(), _target_kind(target_1d), int(ignore_index), lse.data_ptr(),
+            _lib.ptr(dh), _lib.ptr(dw), ws.data_ptr(), ws_bytes, n_rows, dp, vocab_size,
+            int(chunk_rows), _lib.dtype_code(weight.dtype), _lib.stream_of(hidden_2d),
+        )
     if dp != hidden_size:
         dh = dh[:, :hidden_size].contiguous() if dh is not None else None
         dw = dw[:, :hidden_size].contiguous() if dw is not None else None
@@ -356,19 +263,13 @@ def linear_cross_entropy_backward(
 
 
 class _LinearCrossEntropyAutograd(torch.autograd.Function):
-    """cross_entropy.py:663-705."""
+    """cross_entropy.py:663-705: saves the 2-D hidden, weight, 1-D target and
+    the fp32 logsumexp, nothing of size n_rows x vocab."""
 
     @staticmethod
     def forward(ctx: Any, hidden, weight, target, ignore_index):
         n = target.numel()
-        ctx.kept = None
-        if _keep_fits(n, weight.shape[0], hidden.dtype):
-            # one [n, vocab] fp16 buffer held until the backward, which then
-            # skips the logits recompute
-            loss, lse, ctx.kept = _linear_cross_entropy_forward(hidden, weight, target,
-                                                                ignore_index, keep=True)
-        else:
-            loss, lse = _linear_cross_entropy_forward(hidden, weight, target, ignore_index)
+        loss, lse = _linear_cross_entropy_forward(hidden, weight, target, ignore_index)
         ctx.hidden_shape = tuple(hidden.shape)
         ctx.ignore_index = ignore_index
         ctx.save_for_backward(hidden.view(n, hidden.shape[-1]), weight, target.view(n), lse)
@@ -384,15 +285,8 @@ class _LinearCrossEntropyAutograd(torch.autograd.Function):
             dh = torch.zeros(ctx.hidden_shape, device=hidden_2d.device, dtype=hidden_2d.dtype)
             return (dh if need_dh else None), (torch.zeros_like(weight) if need_dw else None), \
                 None, None
-        kept, ctx.kept = ctx.kept, None
-        if kept is not None:
-            # the buffer becomes G in place: a second backward (retain_graph)
-            # takes the recompute path below
-            dh, dw = _backward_from_probs(grad_outputs[0], hidden_2d, weight, target_1d, lse,
-                                          kept, need_dh, need_dw, ctx.ignore_index)
-        else:
-            dh, dw = _backward(grad_outputs[0], hidden_2d, weight, target_1d, lse, need_dh,
-                               need_dw, ctx.ignore_index)
+        dh, dw = _backward(grad_outputs[0], hidden_2d, weight, target_1d, lse, need_dh, need_dw,
+                           ctx.ignore_index)
         if dh is not None:
             dh = dh.view(ctx.hidden_shape)
         return dh, dw, None, None
@@ -406,11 +300,8 @@ def linear_cross_entropy(
     ignore_index: int = IGNORE_INDEX,
 ) -> torch.Tensor:
     """Mean cross-entropy of ``hidden @ weight.T`` against ``target`` without
-    materialising the logits (cross_entropy.py:716-725).  Under autograd with
-    16-bit inputs, when an [n_rows, vocab] 16-bit buffer fits the 4 GiB
-    gradient-tile budget, the forward keeps the fp16 terms exp(logit - tile
-    max) for the backward (the backward's gradient of the logits needs that
-    much memory anyway), so the backward skips the logits recompute."""
+    materialising the logits (cross_entropy.py:716-725).  Under autograd only
+    the fp32 logsumexp is kept for the backward."""
     if not requires_autograd(hidden, weight):
         loss, _ = _linear_cross_entropy_forward(hidden, weight, target, ignore_index)
         return loss

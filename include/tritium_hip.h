@@ -229,11 +229,17 @@ int tritium_linear_ce_fwd(const void* hidden, const void* weight, const void* ta
                           int64_t n_rows, int64_t hidden_size, int64_t vocab, int dtype,
                           void* stream);
 
-/* Backward: tritium.linear_cross_entropy_backward (tritium/ops/cross_entropy.py:863-959).
- * grad_out: device float32 scalar; lse from the forward.  dhidden: [n_rows,
- * hidden_size], dweight: [vocab, hidden_size], both in `dtype`; either may be
- * NULL (not computed).  The vocabulary is processed in chunks of chunk_rows
- * rows (0 = automatic, about 1 GiB of gradient tiles). */
+/* Backward: tritium.linear_cross_entropy_backward (tritium/ops/cross_entropy.py:863-959),
+ * 16-bit dtypes.  grad_out: device float32 scalar; lse from the forward.
+ * dhidden: [n_rows, hidden_size], dweight: [vocab, hidden_size], both in
+ * `dtype`; either may be NULL (not computed).  Per vocabulary chunk of
+ * chunk_rows rows (0 = automatic: the chunk's gradient of the logits fills at
+ * most 1 GiB), the logits are recomputed on the library's MFMA GEMM core and
+ * turned into that gradient G [n_rows, chunk] in the workspace; dweight's rows
+ * = G^T hidden and dhidden += G weight_chunk run on the same core, reading
+ * G, hidden and weight in place (no transposed copies).  dhidden accumulates
+ * in fp32 in the workspace when there is more than one chunk.  Workspace:
+ * tritium_linear_ce_bwd_workspace_size bytes (0 for float32, rejected). */
 size_t tritium_linear_ce_bwd_workspace_size(int64_t n_rows, int64_t hidden_size, int64_t vocab,
                                             int dtype, int need_dhidden, int need_dweight,
                                             int64_t chunk_rows);
@@ -257,32 +263,6 @@ int tritium_linear_ce_grad_logits(const float* grad_out, const float* n_valid, c
                                   int64_t ignore_index, const float* lse, void* g, int64_t ld_g,
                                   int64_t n_rows, int64_t hidden_size, int64_t vocab, int64_t v0,
                                   int64_t vc, int dtype, void* stream);
-
-/* Forward that also keeps, for a backward without the logits recompute, the
- * fp16 terms of its sums: probs[n, v] = exp(logit[n, v] - m), m the max of
- * the logits of token n over v's 256-row vocabulary tile (so every entry is in
- * [0, 1]).  No reference counterpart (the reference recomputes the logits in
- * its backward, cross_entropy.py:928-946); for callers that can hold a
- * [n_rows, ld_probs] 16-bit buffer, and the forward workspace, until the
- * backward.  16-bit dtypes only; ld_probs >= vocab and a multiple of 8,
- * probs 16-byte aligned.  Everything else is tritium_linear_ce_fwd's. */
-int tritium_linear_ce_fwd_probs(const void* hidden, const void* weight, const void* target,
-                                int target_kind, int64_t ignore_index, float* loss, float* lse,
-                                float* n_valid, void* probs, int64_t ld_probs, void* workspace,
-                                size_t workspace_bytes, int64_t n_rows, int64_t hidden_size,
-                                int64_t vocab, int dtype, void* stream);
-
-/* The gradient of the logits from the buffer tritium_linear_ce_fwd_probs
- * kept, in place: probs becomes g of tritium_linear_ce_grad_logits (same
- * formula, in `dtype`, row stride ld_probs) for the whole vocabulary.  Reads
- * the forward's workspace (unchanged since that call) and lse.  No reference
- * counterpart: it replaces the per-chunk recompute of
- * cross_entropy.py:928-946 for callers of tritium_linear_ce_fwd_probs. */
-int tritium_linear_ce_grad_from_probs(const float* grad_out, const float* n_valid,
-                                      const void* target, int target_kind, int64_t ignore_index,
-                                      const float* lse, const void* fwd_workspace,
-                                      size_t fwd_workspace_bytes, void* probs, int64_t ld_probs,
-                                      int64_t n_rows, int64_t vocab, int dtype, void* stream);
 
 /* ---- Split-K finish -------------------------------------------------------
  * dst[i] = (dtype)(src[0 * n + i] + src[1 * n + i] + ... + src[(n_splits - 1) * n + i]),

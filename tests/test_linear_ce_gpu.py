@@ -80,13 +80,21 @@ def test_linear_ce_multi_chunk_backward(dtype):
     _run(200, 128, 1200, dtype, seed=5, ignore_frac=0.05, chunk_rows=256)
 
 
-@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
-def test_linear_ce_backward_c_entry(dtype):
-    # the all-in-library backward (tritium_linear_ce_bwd, its own GEMM core and
-    # transposed operands) that a C caller uses instead of the library GEMMs
-    full = tritium.linear_ce._backward_capi
-    _run(300, 96, 777, dtype, seed=9, ignore_frac=0.1, backward=full)
-    _run(200, 128, 1200, dtype, seed=10, ignore_frac=0.05, chunk_rows=256, backward=full)
+@pytest.mark.parametrize("need", [(True, False), (False, True)])
+def test_linear_ce_backward_one_gradient(need):
+    # tritium_linear_ce_bwd with only dhidden or only dweight requested (the
+    # other pointer NULL), over several chunks
+    h, w, t = _inputs(150, 64, 700, torch.bfloat16, seed=12, ignore_frac=0.05)
+    loss, lse = tritium.linear_ce._linear_cross_entropy_forward(h, w, t)
+    ref_loss, ref_lse = oracle.linear_ce.forward(np32(h), np32(w), np32(t))
+    edh, edw = oracle.linear_ce.backward(1.0, np32(h), np32(w), np32(t), ref_lse)
+    dh, dw = tritium.linear_ce._backward(torch.tensor(1.0, device="cuda"), h, w, t, lse,
+                                         need[0], need[1], -100, 256)
+    assert (dh is None) != need[0] and (dw is None) != need[1]
+    if need[0]:
+        _close(dh, edh, 2e-2, "dhidden")
+    else:
+        _close(dw, edw, 2e-2, "dweight")
 
 
 def test_linear_ce_odd_hidden_size_is_padded():
@@ -169,40 +177,37 @@ def test_linear_ce_empty_rows():
     assert float(tritium.linear_cross_entropy(h, w, t)) == 0.0
 
 
-# ---------------------------------------------------------------- kept probabilities
-# The autograd forward of 16-bit inputs keeps fp16 exp(logit - tile max) and the backward
-# forms G from it in place (tritium_linear_ce_fwd_probs / _grad_from_probs) instead of
-# recomputing the logits GEMM.  Same bar as the recompute path: the float64 oracle.
-def _kept_backward(g, h, w, t, lse, need_dh, need_dw, ignore_index, chunk_rows=0):
-    loss2, lse2, kept = tritium.linear_ce._linear_cross_entropy_forward(h, w, t, ignore_index,
-                                                                        keep=True)
-    # the keeping forward sums the same terms in the same order: bitwise the same lse
-    assert torch.equal(lse2, lse)
-    return tritium.linear_ce._backward_from_probs(g, h, w, t, lse2, kept, need_dh, need_dw,
-                                                  ignore_index)
-
-
+# ------------------------------------------------- MFMA backward edge cases
+# The 16-bit backward (tritium_linear_ce_bwd) recomputes the logits per vocabulary
+# chunk and runs dW = G^T H and dH = G W on the GEMM core with MN-contiguous
+# operands (transposing LDS reads): tile edges in every dimension, vocab sizes
+# that are not a multiple of 8 (the last granule of a G row is padding), token
+# counts that leave a partial K tile, and one to several chunks.
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
-@pytest.mark.parametrize("n,d,v,ignore_frac,tdtype", [
-    (1, 32, 128, 0.0, torch.int64),
-    (130, 64, 1001, 0.1, torch.int32),      # vocab not a multiple of 8: padded rows
-    (257, 128, 2049, 0.05, torch.int64),    # past the 256-token and 256-vocab tile edges
-    (64, 40, 300, 0.0, torch.int64),        # hidden_size padded to 48
+@pytest.mark.parametrize("n,d,v,ignore_frac,tdtype,chunk", [
+    (1, 32, 128, 0.0, torch.int64, 0),
+    (130, 64, 1001, 0.1, torch.int32, 0),     # vocab not a multiple of 8
+    (257, 128, 2049, 0.05, torch.int64, 0),   # past the 256-token and 256-vocab tile edges
+    (64, 40, 300, 0.0, torch.int64, 0),       # hidden_size padded to 48
+    (300, 264, 1537, 0.02, torch.int64, 512), # 3 chunks, the last one 513 rows
+    (513, 96, 640, 0.0, torch.int32, 256),    # K tiles of 64 tokens plus a partial one
 ])
-def test_linear_ce_kept_probs_against_oracle(dtype, n, d, v, ignore_frac, tdtype):
-    _run(n, d, v, dtype, seed=20, ignore_frac=ignore_frac, tdtype=tdtype, backward=_kept_backward)
+def test_linear_ce_mfma_backward_edges(dtype, n, d, v, ignore_frac, tdtype, chunk):
+    print(f"[lce bwd] {dtype} n={n} d={d} v={v} chunk={chunk}", flush=True)
+    _run(n, d, v, dtype, seed=20, ignore_frac=ignore_frac, tdtype=tdtype, chunk_rows=chunk)
 
 
-def test_linear_ce_kept_probs_confident_targets():
+def test_linear_ce_confident_targets():
     # targets at each row's arg-max with large logits: p(target) is close to 1 and the
-    # target entry of G is a small difference p - 1 (taken from the fp32 target logit)
+    # target entry of G is a small difference p - 1
     n, d, v = 128, 64, 777
     h, w, _ = _inputs(n, d, v, torch.bfloat16, seed=21, wscale=1.5)
     t = (h.float() @ w.float().t()).argmax(dim=1)
     loss, lse = tritium.linear_ce._linear_cross_entropy_forward(h, w, t)
     ref_loss, ref_lse = oracle.linear_ce.forward(np32(h), np32(w), np32(t))
     assert float(loss) < 0.5  # most rows have p(target) near 1
-    dh, dw = _kept_backward(torch.tensor(1.0, device="cuda"), h, w, t, lse, True, True, -100)
+    dh, dw = tritium.linear_ce._backward(torch.tensor(1.0, device="cuda"), h, w, t, lse, True,
+                                         True, -100)
     edh, edw = oracle.linear_ce.backward(1.0, np32(h), np32(w), np32(t), ref_lse)
     for got, want, name in ((dh, edh, "dhidden"), (dw, edw, "dweight")):
         ref = np.asarray(want, dtype=np.float64)
@@ -210,34 +215,37 @@ def test_linear_ce_kept_probs_confident_targets():
         assert rel < 2e-2, f"{name}: relative L2 {rel:.3e}"
 
 
-def test_linear_ce_kept_probs_matches_recompute_path():
-    h, w, t = _inputs(512, 256, 5000, torch.bfloat16, seed=22, ignore_frac=0.03)
+def test_linear_ce_chunking_only_changes_dhidden_rounding():
+    # one chunk vs four: dweight's rows are the same products (bitwise), dhidden
+    # differs only by the fp32 accumulation across chunks before its one rounding
+    h, w, t = _inputs(512, 256, 1024, torch.bfloat16, seed=22, ignore_frac=0.03)
     loss, lse = tritium.linear_ce._linear_cross_entropy_forward(h, w, t)
     g = torch.tensor(0.75, device="cuda")
-    a = tritium.linear_ce._backward(g, h, w, t, lse, True, True, -100)
-    b = _kept_backward(g, h, w, t, lse, True, True, -100)
-    for x, y in zip(a, b):
-        x, y = x.double(), y.double()
-        # the two differ only by the fp16 rounding of exp(logit - tile max)
-        assert float((x - y).norm() / y.norm()) < 5e-3
+    dh1, dw1 = tritium.linear_ce._backward(g, h, w, t, lse, True, True, -100, 1024)
+    dh4, dw4 = tritium.linear_ce._backward(g, h, w, t, lse, True, True, -100, 256)
+    assert torch.equal(dw1, dw4)
+    x, y = dh4.double(), dh1.double()
+    assert float((x - y).norm() / y.norm()) < 5e-3
 
 
-def test_linear_ce_autograd_keeps_probs_and_retain_graph():
+def test_linear_ce_autograd_keeps_no_logit_buffer_and_retain_graph():
     h, w, t = _inputs(200, 64, 900, torch.bfloat16, seed=23, ignore_frac=0.1)
     hs, ws = h.clone().requires_grad_(True), w.clone().requires_grad_(True)
     loss = tritium.linear_cross_entropy(hs, ws, t) * 3.0
-    assert loss.grad_fn.next_functions[0][0].kept is not None
+    # what the forward keeps for the backward: the inputs and the fp32 lse only
+    saved = loss.grad_fn.next_functions[0][0].saved_tensors
+    assert [tuple(x.shape) for x in saved] == [(200, 64), (900, 64), (200,), (200,)]
     loss.backward(retain_graph=True)
     g1 = (hs.grad.clone(), ws.grad.clone())
-    # the kept buffer was consumed: the second backward recomputes the logits
     loss.backward()
+    for first, total in zip(g1, (hs.grad, ws.grad)):
+        assert torch.equal(total, 2 * first)
+    import torch.nn.functional as F
+    hr, wr = h.float().requires_grad_(True), w.float().requires_grad_(True)
+    (F.cross_entropy(hr @ wr.t(), t, ignore_index=-100) * 3.0).backward()
+
     def rel(a, b):
         a, b = a.double(), b.double()
         return float((a - b).norm() / b.norm())
 
-    for first, total in zip(g1, (hs.grad, ws.grad)):
-        assert rel(total, 2 * first) < 1e-2
-    import torch.nn.functional as F
-    hr, wr = h.float().requires_grad_(True), w.float().requires_grad_(True)
-    (F.cross_entropy(hr @ wr.t(), t, ignore_index=-100) * 3.0).backward()
     assert rel(g1[0], hr.grad) < 2e-2 and rel(g1[1], wr.grad) < 2e-2
