@@ -418,7 +418,10 @@ __device__ __forceinline__ void compute_tile(const char* stage, Acc<C>& acc, int
 // dealt round-robin to the 8 XCDs; each XCD gets a contiguous range of work
 // items, walked in groups of GROUP_M row tiles column by column so that the
 // blocks resident on one XCD share A and B tiles in its L2.
-template <int GROUP_M = 4>
+#ifndef TRI_GEMM_GROUP_M
+#define TRI_GEMM_GROUP_M 4
+#endif
+template <int GROUP_M = TRI_GEMM_GROUP_M>
 __device__ __forceinline__ void tile_of(int64_t bid, int64_t n_blocks, int tiles_m, int tiles_n,
                                         int& tm, int& tn) {
   int64_t w = bid;
@@ -438,6 +441,26 @@ __device__ __forceinline__ void tile_of(int64_t bid, int64_t n_blocks, int tiles
 
 // compute_tile hook: DMAs of the next K tile, DMA_PER_WAVE / KS of them
 // after each 16-deep step
+// How many of a wavefront's DMAs follow each 16-deep step, as decimal digits
+// of TRI_GEMM_SPREAD read from the first step; the remaining DMAs follow the
+// last step.  4400 (four after each of the first two steps) measured 3.5%
+// faster than 2222 and 1.7% faster than 8000 on config 4's linear-CE: the
+// last DMAs of the next tile then have half a tile of MFMAs to land behind.
+#ifndef TRI_GEMM_SPREAD
+#define TRI_GEMM_SPREAD 4400
+#endif
+constexpr int spread_digit(int s, int ks) {
+  int v = TRI_GEMM_SPREAD;
+  for (int i = 0; i < ks - 1 - s; ++i) v /= 10;
+  return v % 10;
+}
+template <class C>
+constexpr int spread_first(int s) {
+  int q = 0;
+  for (int i = 0; i < s; ++i) q += spread_digit(i, C::RB / 32);
+  return q < C::DMA_PER_WAVE ? q : C::DMA_PER_WAVE;
+}
+
 template <class C, typename T, bool TA = false, bool TB = false>
 struct DmaSpread {
   char* st;
@@ -445,13 +468,139 @@ struct DmaSpread {
   int64_t m0, n0, k0;
   template <int S>
   __device__ __forceinline__ void step() const {
-    constexpr int KS = C::RB / 32, PER = (C::DMA_PER_WAVE + KS - 1) / KS;
-    constexpr int Q0 = S * PER < C::DMA_PER_WAVE ? S * PER : C::DMA_PER_WAVE;
-    constexpr int Q1 = Q0 + PER < C::DMA_PER_WAVE ? Q0 + PER : C::DMA_PER_WAVE;
+    constexpr int KS = C::RB / 32;
+    constexpr int Q0 = spread_first<C>(S);
+    constexpr int Q1 = S + 1 == KS ? C::DMA_PER_WAVE : spread_first<C>(S + 1);
     if constexpr (Q0 < Q1) dma_tile<C, T, Q0, Q1, TA, TB>(st, *p, m0, n0, k0);
   }
 };
 
+
+// DMA plan of the 2-stage loop for one output tile: each of this
+// wavefront's DMA_PER_WAVE runs (PA of A, then PB of B, as in dma_one) gets
+// a per-lane byte offset computed once per tile from a wave-uniform operand
+// base that advances by a fixed stride per K tile, so issuing a DMA in the
+// loop costs scalar adds only (the per-DMA 64-bit address arithmetic and the
+// generic-to-LDS pointer check it replaces cost ~20% of the GEMM's time).
+// Offsets are 32-bit: K-contiguous operands need BM (BN) * ld * sizeof(T)
+// < 4 GiB, MN-contiguous ones BK * ld * sizeof(T) < 4 GiB (host-checked).
+template <class C, typename T, bool TR, int X>
+__device__ __forceinline__ uint32_t run_voff(int run, int lane, int64_t ld, int64_t x0,
+                                             int64_t xn) {
+  constexpr int VE = vec<T>();
+  if constexpr (!TR) {
+    const int trow = run * C::DMA_ROWS + lane / C::GRAN;
+    const int c = (lane % C::GRAN) ^ swz_key<C>(trow);
+    const int64_t row = imin(trow, xn - 1 - x0);
+    return (uint32_t)((row * ld + c * VE) * (int64_t)sizeof(T));
+  } else {
+    constexpr int XG = X / 8;
+    const int krow = run * (64 / XG) + lane / XG;
+    const int c = (lane % XG) ^ tkey(krow);
+    const int64_t last = ((xn + 7) & ~(int64_t)7) - 8;
+    const int64_t col = imin(x0 + c * VE, last) - x0;
+    return (uint32_t)((krow * ld + col) * (int64_t)sizeof(T));
+  }
+}
+
+template <class C, typename T, bool TA, bool TB>
+struct DmaPlan {
+  static constexpr int W = C::WM * C::WN;
+  static constexpr int RUNS_A = C::BM / C::DMA_ROWS;
+  static constexpr int PA = RUNS_A / W, PB = (C::BN / C::DMA_ROWS) / W;
+  uint32_t voff[PA + PB];
+  const char* base_a;
+  const char* base_b;
+  int64_t step_a, step_b;  // bytes per K tile
+  uint32_t lds_a, lds_b;   // LDS byte address of this wavefront's first A / B run, stage 0
+
+  __device__ __forceinline__ void init(const Problem& p, int64_t m0, int64_t n0, char* smem) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    constexpr int64_t BK = bk<C, T>(), ES = sizeof(T);
+#pragma unroll
+    for (int q = 0; q < PA; ++q) voff[q] = run_voff<C, T, TA, C::BM>(wave * PA + q, lane, p.lda, m0, p.M);
+#pragma unroll
+    for (int q = 0; q < PB; ++q) voff[PA + q] = run_voff<C, T, TB, C::BN>(wave * PB + q, lane, p.ldb, n0, p.N);
+    base_a = (const char*)p.a + (TA ? m0 : m0 * p.lda) * ES;
+    base_b = (const char*)p.b + (TB ? n0 : n0 * p.ldb) * ES;
+    step_a = TA ? BK * p.lda * ES : BK * ES;
+    step_b = TB ? BK * p.ldb * ES : BK * ES;
+    const int ws = __builtin_amdgcn_readfirstlane(wave);
+    const uint32_t l0 = __builtin_amdgcn_readfirstlane(lds_addr(smem));
+    lds_a = l0 + (uint32_t)(ws * PA) * 1024u;
+    lds_b = l0 + (uint32_t)(RUNS_A + ws * PB) * 1024u;
+  }
+  // A wave-uniform pointer in SGPRs: the compiler may compute base + kt *
+  // step with vector instructions, and the DMA's scalar base operand needs
+  // an SGPR pair (readfirstlane of a value already in SGPRs folds away).
+  static __device__ __forceinline__ const char* in_sgprs(const char* p) {
+    const uint64_t v = (uint64_t)p;
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return (const char*)(((uint64_t)hi << 32) | lo);
+  }
+  // DMA q of K tile kt into stage `stage`
+  template <int Q>
+  __device__ __forceinline__ void issue(int stage, int64_t kt) const {
+    const uint32_t so = (uint32_t)stage * (uint32_t)C::STAGE_BYTES;
+    if constexpr (Q < PA)
+      dma16s(in_sgprs(base_a + kt * step_a), voff[Q], lds_a + so + Q * 1024u);
+    else
+      dma16s(in_sgprs(base_b + kt * step_b), voff[Q], lds_b + so + (Q - PA) * 1024u);
+  }
+  template <int Q, int Q1>
+  __device__ __forceinline__ void issue_range(int stage, int64_t kt) const {
+    if constexpr (Q < Q1) {
+      issue<Q>(stage, kt);
+      issue_range<Q + 1, Q1>(stage, kt);
+    }
+  }
+};
+
+// compute_tile hook of the planned loop: the DMAs of K tile kt after the
+// steps TRI_GEMM_SPREAD names; with TRI_GEMM_SPREAD_HI the upper half of the
+// wavefronts (the second wavefront on each SIMD) follows its own pattern.
+#ifndef TRI_GEMM_SPREAD_HI
+#define TRI_GEMM_SPREAD_HI TRI_GEMM_SPREAD
+#endif
+constexpr int spread_digit2(int pat, int s, int ks) {
+  for (int i = 0; i < ks - 1 - s; ++i) pat /= 10;
+  return pat % 10;
+}
+template <class C>
+constexpr int spread_first2(int pat, int s) {
+  int q = 0;
+  for (int i = 0; i < s; ++i) q += spread_digit2(pat, i, C::RB / 32);
+  return q < C::DMA_PER_WAVE ? q : C::DMA_PER_WAVE;
+}
+
+template <class C, typename T, bool TA, bool TB>
+struct PlanSpread {
+  const DmaPlan<C, T, TA, TB>* plan;
+  int stage;
+  int64_t kt;
+  bool hi;
+  template <int PAT, int S>
+  __device__ __forceinline__ void run() const {
+    constexpr int KS = C::RB / 32;
+    constexpr int Q0 = spread_first2<C>(PAT, S);
+    constexpr int Q1 = S + 1 == KS ? C::DMA_PER_WAVE : spread_first2<C>(PAT, S + 1);
+    plan->template issue_range<Q0, Q1>(stage, kt);
+  }
+  template <int S>
+  __device__ __forceinline__ void step() const {
+    if constexpr (TRI_GEMM_SPREAD_HI == TRI_GEMM_SPREAD) {
+      run<TRI_GEMM_SPREAD, S>();
+    } else {
+      if (hi) run<TRI_GEMM_SPREAD_HI, S>();
+      else run<TRI_GEMM_SPREAD, S>();
+    }
+  }
+};
+
+#ifndef TRI_GEMM_PLAN
+#define TRI_GEMM_PLAN 1
+#endif
 
 // Accumulate the (tm, tn) tile of A * B^T over all of K (A, B in the
 // layouts TA, TB select).  `smem` holds C::SMEM_BYTES of LDS (1 KiB aligned).
@@ -498,9 +647,27 @@ __device__ __forceinline__ void mainloop(const Problem& p, int tm, int tn, char*
       __syncthreads();
       compute_tile<C, T>(smem + (int)((nfull - 1) & 1) * C::STAGE_BYTES, acc, wm, wn);
     }
-  } else if constexpr (C::STAGES == 2) {
+  } else if constexpr (C::STAGES == 2 && TRI_GEMM_PLAN) {
     // branch-free steady state: wait for tile kt, sync, prefetch tile kt + 1
     // into the buffer read at step kt - 1, compute tile kt
+    DmaPlan<C, T, TA, TB> plan;
+    plan.init(p, m0, n0, smem);
+    const bool hi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) >= C::WM * C::WN / 2;
+    if (nfull > 0) plan.template issue_range<0, C::DMA_PER_WAVE>(0, 0);
+    for (int64_t kt = 0; kt + 1 < nfull; ++kt) {
+      wait_vmcnt<0>();
+      __syncthreads();
+      const PlanSpread<C, T, TA, TB> spread{&plan, (int)((kt + 1) & 1), kt + 1, hi};
+      compute_tile<C, T, PlanSpread<C, T, TA, TB>, TA, TB>(smem + (int)(kt & 1) * C::STAGE_BYTES,
+                                                           acc, wm, wn, spread);
+    }
+    if (nfull > 0) {
+      wait_vmcnt<0>();
+      __syncthreads();
+      compute_tile<C, T, NoHook, TA, TB>(smem + (int)((nfull - 1) & 1) * C::STAGE_BYTES, acc, wm,
+                                         wn);
+    }
+  } else if constexpr (C::STAGES == 2) {
     if (nfull > 0) dma_tile<C, T, 0, C::DMA_PER_WAVE, TA, TB>(smem, p, m0, n0, 0);
     for (int64_t kt = 0; kt + 1 < nfull; ++kt) {
       wait_vmcnt<0>();

@@ -482,7 +482,9 @@ BwdLayout bwd_layout(int64_t N, int64_t D, int64_t V, int esz, bool need_dh, int
   const int64_t vpad = round_up(V, kMaxBM);
   int64_t chunk = chunk_rows > 0 ? round_up(chunk_rows, kMaxBM)
                                  : (kGBudget / std::max<int64_t>(1, N * esz)) / kMaxBM * kMaxBM;
-  chunk = std::max<int64_t>(kMaxBM, std::min<int64_t>(chunk, vpad));
+  // G rows are the K-contiguous A operand of dH: 256 of them must span less
+  // than 4 GiB (32-bit DMA offsets of the GEMM core)
+  chunk = std::max<int64_t>(kMaxBM, std::min<int64_t>({chunk, vpad, ((int64_t)1 << 23) - kMaxBM}));
   L.chunk = chunk;
   L.n_chunks = cdiv(V, chunk);
   L.ld_g = round_up(std::min<int64_t>(chunk, V), 8);
@@ -509,6 +511,9 @@ int check_sizes(int64_t N, int64_t D, int64_t V, int dtype) {
   if (cdiv(V, 128) * cdiv(N, 128) >= ((int64_t)1 << 31) || N >= ((int64_t)1 << 31) ||
       cdiv(V, 64) > 65535 || cdiv(N, 64) > 65535)
     return fail(TRI_EINVAL, "linear_ce: problem too large");
+  // the GEMM core's per-lane DMA offsets are 32-bit: 256 rows of hidden_size elements
+  if (D >= ((int64_t)1 << 23))
+    return fail(TRI_EINVAL, "linear_ce: hidden_size %lld must be below 2^23", (long long)D);
   return TRI_OK;
 }
 
