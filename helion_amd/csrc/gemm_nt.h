@@ -558,11 +558,9 @@ struct DmaPlan {
 };
 
 // compute_tile hook of the planned loop: the DMAs of K tile kt after the
-// steps TRI_GEMM_SPREAD names; with TRI_GEMM_SPREAD_HI the upper half of the
-// wavefronts (the second wavefront on each SIMD) follows its own pattern.
-#ifndef TRI_GEMM_SPREAD_HI
-#define TRI_GEMM_SPREAD_HI TRI_GEMM_SPREAD
-#endif
+// steps the digits of PAT name.  Every wavefront follows one pattern: giving
+// the second wavefront of each SIMD the opposite phase (DMAs after the last
+// two steps) measured 37-57% slower.
 constexpr int spread_digit2(int pat, int s, int ks) {
   for (int i = 0; i < ks - 1 - s; ++i) pat /= 10;
   return pat % 10;
@@ -574,29 +572,32 @@ constexpr int spread_first2(int pat, int s) {
   return q < C::DMA_PER_WAVE ? q : C::DMA_PER_WAVE;
 }
 
-template <class C, typename T, bool TA, bool TB>
+template <class C, typename T, bool TA, bool TB, int PAT>
 struct PlanSpread {
   const DmaPlan<C, T, TA, TB>* plan;
   int stage;
   int64_t kt;
-  bool hi;
-  template <int PAT, int S>
-  __device__ __forceinline__ void run() const {
+  template <int S>
+  __device__ __forceinline__ void step() const {
     constexpr int KS = C::RB / 32;
     constexpr int Q0 = spread_first2<C>(PAT, S);
     constexpr int Q1 = S + 1 == KS ? C::DMA_PER_WAVE : spread_first2<C>(PAT, S + 1);
     plan->template issue_range<Q0, Q1>(stage, kt);
   }
-  template <int S>
-  __device__ __forceinline__ void step() const {
-    if constexpr (TRI_GEMM_SPREAD_HI == TRI_GEMM_SPREAD) {
-      run<TRI_GEMM_SPREAD, S>();
-    } else {
-      if (hi) run<TRI_GEMM_SPREAD_HI, S>();
-      else run<TRI_GEMM_SPREAD, S>();
-    }
-  }
 };
+
+// The K loop of the planned 2-stage pipeline with DMA pattern PAT.
+template <class C, typename T, bool TA, bool TB, int PAT>
+__device__ __forceinline__ void planned_loop(const DmaPlan<C, T, TA, TB>& plan, char* smem,
+                                             Acc<C>& acc, int wm, int wn, int64_t nfull) {
+  for (int64_t kt = 0; kt + 1 < nfull; ++kt) {
+    wait_vmcnt<0>();
+    __syncthreads();
+    const PlanSpread<C, T, TA, TB, PAT> spread{&plan, (int)((kt + 1) & 1), kt + 1};
+    compute_tile<C, T, PlanSpread<C, T, TA, TB, PAT>, TA, TB>(
+        smem + (int)(kt & 1) * C::STAGE_BYTES, acc, wm, wn, spread);
+  }
+}
 
 #ifndef TRI_GEMM_PLAN
 #define TRI_GEMM_PLAN 1
@@ -652,15 +653,8 @@ __device__ __forceinline__ void mainloop(const Problem& p, int tm, int tn, char*
     // into the buffer read at step kt - 1, compute tile kt
     DmaPlan<C, T, TA, TB> plan;
     plan.init(p, m0, n0, smem);
-    const bool hi = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6) >= C::WM * C::WN / 2;
     if (nfull > 0) plan.template issue_range<0, C::DMA_PER_WAVE>(0, 0);
-    for (int64_t kt = 0; kt + 1 < nfull; ++kt) {
-      wait_vmcnt<0>();
-      __syncthreads();
-      const PlanSpread<C, T, TA, TB> spread{&plan, (int)((kt + 1) & 1), kt + 1, hi};
-      compute_tile<C, T, PlanSpread<C, T, TA, TB>, TA, TB>(smem + (int)(kt & 1) * C::STAGE_BYTES,
-                                                           acc, wm, wn, spread);
-    }
+    planned_loop<C, T, TA, TB, TRI_GEMM_SPREAD>(plan, smem, acc, wm, wn, nfull);
     if (nfull > 0) {
       wait_vmcnt<0>();
       __syncthreads();

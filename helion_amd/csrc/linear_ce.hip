@@ -145,15 +145,24 @@ lce_fwd_kernel(FwdArgs a) {
   const int64_t v0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
   const TT* target = (const TT*)a.target;
 
+  // every vocabulary row of an interior tile exists: no per-element check
+  const bool full = v0 + C::BM <= a.V;
   float mx[C::NT];
 #pragma unroll
   for (int j = 0; j < C::NT; ++j) {
     float m = -INFINITY;
+    if (full) {
 #pragma unroll
-    for (int i = 0; i < C::MT; ++i)
+      for (int i = 0; i < C::MT; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (v0 + acc_row<C>(wm, i, r, g) < a.V) m = fmaxf(m, acc.t[i][j][r]);
+        for (int r = 0; r < 16; ++r) m = fmaxf(m, acc.t[i][j][r]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (v0 + acc_row<C>(wm, i, r, g) < a.V) m = fmaxf(m, acc.t[i][j][r]);
+    }
     m = fmaxf(m, __shfl_xor(m, 32, 64));
     if (g == 0) red[wm][acc_col<C>(wn, j, l32)] = m;
   }
@@ -173,11 +182,18 @@ lce_fwd_kernel(FwdArgs a) {
     const int64_t n = n0 + col;
     const float ms = mx[j] * kLog2e;
     float s = 0.f;
+    if (full) {
 #pragma unroll
-    for (int i = 0; i < C::MT; ++i)
+      for (int i = 0; i < C::MT; ++i)
 #pragma unroll
-      for (int r = 0; r < 16; ++r)
-        if (v0 + acc_row<C>(wm, i, r, g) < a.V) s += fast_exp2(acc.t[i][j][r] * kLog2e - ms);
+        for (int r = 0; r < 16; ++r) s += fast_exp2(acc.t[i][j][r] * kLog2e - ms);
+    } else {
+#pragma unroll
+      for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (v0 + acc_row<C>(wm, i, r, g) < a.V) s += fast_exp2(acc.t[i][j][r] * kLog2e - ms);
+    }
     s += __shfl_xor(s, 32, 64);
     if (g == 0) red[wm][col] = s;
     // the target logit: written by the single lane that holds its row
@@ -326,9 +342,8 @@ struct GArgs {
   const float* lse;     // [N]
   const float* grad_out;
   const float* n_valid;
-  void* gt;             // [Vc, ld_gt]   (may be null)
-  void* gm;             // [N, ld_g]     (may be null)
-  int64_t N, D, Vc, ld, ld_gt, ld_g, vc0, ignore_index;
+  void* gm;             // [N, ld_g]
+  int64_t N, D, Vc, ld, ld_g, vc0, ignore_index;
   int tiles_v, tiles_n;
 };
 
@@ -348,7 +363,6 @@ lce_g_kernel(GArgs a) {
   const int wm = wave / C::WN, wn = wave % C::WN;
   const int64_t v0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
   const float coef_all = a.grad_out[0] / a.n_valid[0];
-  T* gt = (T*)a.gt;
   T* gm = (T*)a.gm;
   // G [N, Vc] is row-major by token while a lane holds 4 consecutive vocab
   // rows of one token: stored directly, every store instruction would touch
@@ -367,26 +381,46 @@ lce_g_kernel(GArgs a) {
     const int64_t t = nvalid ? load_target((const TT*)a.target, n) : a.ignore_index;
     const float coef = (t == a.ignore_index) ? 0.f : coef_all;
     const int64_t tl = t - a.vc0;  // target row inside this chunk
+    if constexpr (kStage) {
+      // exp(S - lse) * coef everywhere, then the target entry rewritten as
+      // (p - 1) * coef by the one lane holding it (a branch almost every
+      // wavefront skips): the same arithmetic as forming each entry with
+      // its one-hot term, without a 64-bit compare per entry
 #pragma unroll
-    for (int i = 0; i < C::MT; ++i) {
+      for (int i = 0; i < C::MT; ++i)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int vl = acc_row<C>(wm, i, 4 * rr, g);  // 4 consecutive vocab rows
-        const int64_t vb = v0 + vl;
-        float gv[4];
+        for (int rr = 0; rr < 4; ++rr) {
+          float gv[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const float pr = fast_exp2(acc.t[i][j][4 * rr + e] * kLog2e - l2);
-          gv[e] = (pr - (vb + e == tl ? 1.f : 0.f)) * coef;
+          for (int e = 0; e < 4; ++e) gv[e] = fast_exp2(acc.t[i][j][4 * rr + e] * kLog2e - l2) * coef;
+          stage_put4(tile, tok, acc_row<C>(wm, i, 4 * rr, g), pack4<T>(gv));
         }
-        if (gt != nullptr && nvalid) {
+      const int64_t dt = tl - v0 - wm * C::WTM;  // target row inside this wavefront's rows
+      if (dt >= 0 && dt < C::WTM) {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (vb + e < a.Vc) gt[(vb + e) * a.ld_gt + n] = from_f32<T>(gv[e]);
-        }
-        if constexpr (kStage) {
-          if (gm != nullptr) stage_put4(tile, tok, vl, pack4<T>(gv));
-        } else if (gm != nullptr && nvalid) {
+        for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+          for (int r = 0; r < 16; ++r)
+            if (acc_row<C>(0, i, r, g) == dt) {
+              const float gv = (fast_exp2(acc.t[i][j][r] * kLog2e - l2) - 1.f) * coef;
+              const int vl = acc_row<C>(wm, i, r, g);
+              *reinterpret_cast<uint16_t*>(tile + tok * 512 + (((vl >> 2) ^ (tok & 63)) << 3) +
+                                           2 * (vl & 3)) = bits16(from_f32<T>(gv));
+            }
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < C::MT; ++i) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int64_t vb = v0 + acc_row<C>(wm, i, 4 * rr, g);  // 4 consecutive vocab rows
+          float gv[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const float pr = fast_exp2(acc.t[i][j][4 * rr + e] * kLog2e - l2);
+            gv[e] = (pr - (vb + e == tl ? 1.f : 0.f)) * coef;
+          }
+          if (!nvalid) continue;
           T* dst = gm + n * a.ld_g + vb;
           if (vb + 4 <= a.Vc) {
             store_f32<T, 4>(dst, gv);
@@ -400,7 +434,6 @@ lce_g_kernel(GArgs a) {
     }
   }
   if constexpr (kStage) {
-    if (gm == nullptr) return;
     __syncthreads();
     stage_out<C::THREADS, C::BN>(tile, (uint16_t*)gm, a.ld_g, n0, v0, a.N, a.Vc);
   }
@@ -422,6 +455,54 @@ gemm_store_kernel(gemm::Problem p, const float* acc_in, OT* out, int64_t ldc, in
   const int l32 = lane & 31, g = lane >> 5;
   const int wm = wave / C::WN, wn = wave % C::WN;
   const int64_t m0 = (int64_t)tm * C::BM, n0 = (int64_t)tn * C::BN;
+  if constexpr (C::WTM * C::BN * 4 <= C::SMEM_BYTES && C::BN % 128 == 0) {
+    // Through the (now idle) LDS, one wavefront row of sub-tiles at a time:
+    // the WTM x BN fp32 block of the wavefronts with wm == h is staged
+    // row-major (columns XOR 32 on every other group of 4 rows, so the two
+    // half-wavefronts of a store write distinct banks), then every thread
+    // moves 4 consecutive columns: whole rows leave as 16-byte (fp32) or
+    // 8-byte (16-bit) stores instead of one 2- or 4-byte store per element.
+    float* st = reinterpret_cast<float*>(smem);
+    const bool vec_ok = ldc % 4 == 0 && ((uintptr_t)out | (uintptr_t)acc_in) % 16 == 0;
+    constexpr int RPI = C::THREADS * 4 / C::BN;  // rows per iteration
+#pragma unroll 1
+    for (int h = 0; h < C::WM; ++h) {
+      if (wm == h) {
+#pragma unroll
+        for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+          for (int j = 0; j < C::NT; ++j)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int row = acc_row<C>(0, i, r, g), col = acc_col<C>(wn, j, l32);
+              st[row * C::BN + (col ^ (((row >> 2) & 1) << 5))] = acc.t[i][j][r];
+            }
+      }
+      __syncthreads();
+#pragma unroll 4
+      for (int it = 0; it < C::WTM / RPI; ++it) {
+        const int idx = it * C::THREADS + threadIdx.x;
+        const int row = idx / (C::BN / 4), c = (idx % (C::BN / 4)) * 4;
+        const int64_t m = m0 + h * C::WTM + row, n = n0 + c;
+        if (m >= p.M || n >= p.N) continue;
+        float4 v = *reinterpret_cast<const float4*>(st + row * C::BN + (c ^ (((row >> 2) & 1) << 5)));
+        if (vec_ok && n + 4 <= p.N) {
+          if (acc_in != nullptr) {
+            const float4 a = *reinterpret_cast<const float4*>(acc_in + m * ldc + n);
+            v.x += a.x; v.y += a.y; v.z += a.z; v.w += a.w;
+          }
+          const float f[4] = {v.x, v.y, v.z, v.w};
+          store_f32<OT, 4>(out + m * ldc + n, f);
+        } else {
+          const float f[4] = {v.x, v.y, v.z, v.w};
+          for (int e = 0; e < 4 && n + e < p.N; ++e)
+            out[m * ldc + n + e] = from_f32<OT>(f[e] + (acc_in != nullptr ? acc_in[m * ldc + n + e] : 0.f));
+        }
+      }
+      __syncthreads();
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < C::NT; ++j) {
     const int64_t n = n0 + acc_col<C>(wn, j, l32);
@@ -588,10 +669,9 @@ int bwd_impl(const float* grad_out, const void* hidden, const void* weight, cons
     ga.lse = lse;
     ga.grad_out = grad_out;
     ga.n_valid = n_valid;
-    ga.gt = nullptr;
     ga.gm = gm;
     ga.N = N; ga.D = D; ga.Vc = vc; ga.ld = D;
-    ga.ld_gt = 0; ga.ld_g = L.ld_g; ga.vc0 = vc0; ga.ignore_index = ignore_index;
+    ga.ld_g = L.ld_g; ga.vc0 = vc0; ga.ignore_index = ignore_index;
     ga.tiles_v = (int)cdiv(vc, CfgT<T>::BM);
     ga.tiles_n = (int)cdiv(N, CfgT<T>::BN);
     lce_g_kernel<T, TT><<<(unsigned)((int64_t)ga.tiles_v * ga.tiles_n), CfgT<T>::THREADS, 0, st>>>(ga);
@@ -630,10 +710,9 @@ int grad_logits_impl(const float* grad_out, const float* n_valid, const void* hi
   ga.lse = lse;
   ga.grad_out = grad_out;
   ga.n_valid = n_valid;
-  ga.gt = nullptr;
   ga.gm = g;
   ga.N = N; ga.D = D; ga.Vc = vc; ga.ld = D;
-  ga.ld_gt = 0; ga.ld_g = ld_g; ga.vc0 = v0; ga.ignore_index = ignore_index;
+  ga.ld_g = ld_g; ga.vc0 = v0; ga.ignore_index = ignore_index;
   ga.tiles_v = (int)cdiv(vc, CfgT<T>::BM);
   ga.tiles_n = (int)cdiv(N, CfgT<T>::BN);
   lce_g_kernel<T, TT><<<(unsigned)((int64_t)ga.tiles_v * ga.tiles_n), CfgT<T>::THREADS, 0, st>>>(ga);
