@@ -441,14 +441,25 @@ lce_g_kernel(GArgs a) {
 
 // Plain GEMM: out[m, n] = (acc_in[m, n] if acc_in) + (A B^T)[m, n], A and B
 // in the layouts TA, TB select (gemm_nt.h).
+// With gridDim.y = S > 1 the reduction is split: split s takes K range
+// [s ks, min((s + 1) ks, K)) and writes (and reads acc_in) at an offset of
+// s * split_stride elements -- fp32 partials that a fixed-order sum finishes.
 template <typename T, typename OT, bool TA, bool TB>
 __global__ void __launch_bounds__(CfgT<T>::THREADS)
 gemm_store_kernel(gemm::Problem p, const float* acc_in, OT* out, int64_t ldc, int tiles_m,
-                  int tiles_n) {
+                  int tiles_n, int64_t ks, int64_t split_stride) {
   typedef CfgT<T> C;
   __shared__ __attribute__((aligned(1024))) char smem[C::SMEM_BYTES];
   int tm, tn;
   gemm::tile_of(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+  if (gridDim.y > 1) {
+    const int64_t s = blockIdx.y, k0 = s * ks;
+    p.K = gemm::imin(ks, p.K - k0);
+    p.a = (const T*)p.a + (TA ? k0 * p.lda : k0);
+    p.b = (const T*)p.b + (TB ? k0 * p.ldb : k0);
+    out += s * split_stride;
+    if (acc_in != nullptr) acc_in += s * split_stride;
+  }
   Acc<C> acc;
   gemm::mainloop<C, T, TA, TB>(p, tm, tn, smem, acc);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -549,16 +560,33 @@ FwdLayout fwd_layout(int64_t N, int64_t V, int bm, int bn) {
   return L;
 }
 
+// K splits for an M x N product over K: the smallest power of two (at most 8,
+// at least 16 K tiles per split) whose grid fills the GPU twice; 1 for grids
+// that already do (config 4's dH and dW).
+template <typename T>
+int split_count(int64_t M, int64_t N, int64_t K) {
+  typedef CfgT<T> C;
+  const int64_t tiles = cdiv(M, C::BM) * cdiv(N, C::BN), target = 2 * (int64_t)cu_count();
+  int s = 1;
+  while (s < 8 && tiles * s < target && K / (2 * s) >= 16 * gemm::bk<C, T>()) s *= 2;
+  return s;
+}
+
 struct BwdLayout {
   int64_t chunk, n_chunks, ld_g;
-  size_t n_valid, gm, dh_acc, total;
+  int sh, sw;  // K splits of the dH and dW products
+  size_t n_valid, gm, dh_acc, dw_part, total;
 };
 
 // The backward's workspace: the count of valid rows, G of one vocabulary
 // chunk [N, ld_g] (chunk rows chosen so that G fits kGBudget bytes, or
-// chunk_rows rounded up to the row tile) and, with more than one chunk, the
-// fp32 dH accumulator [N, D].
-BwdLayout bwd_layout(int64_t N, int64_t D, int64_t V, int esz, bool need_dh, int64_t chunk_rows) {
+// chunk_rows rounded up to the row tile), the fp32 dH accumulator [sh, N, D]
+// when there is more than one chunk or dH is split over K, and the fp32 dW
+// partials [sw, chunk, D] when dW is split.
+template <typename T>
+BwdLayout bwd_layout(int64_t N, int64_t D, int64_t V, bool need_dh, bool need_dw,
+                     int64_t chunk_rows) {
+  const int esz = (int)sizeof(T);
   BwdLayout L;
   const int64_t vpad = round_up(V, kMaxBM);
   int64_t chunk = chunk_rows > 0 ? round_up(chunk_rows, kMaxBM)
@@ -575,9 +603,12 @@ BwdLayout bwd_layout(int64_t N, int64_t D, int64_t V, int esz, bool need_dh, int
     off += (size_t)round_up((int64_t)bytes, 256);
     return at;
   };
+  L.sh = need_dh ? split_count<T>(N, D, std::min(chunk, V)) : 1;
+  L.sw = need_dw ? split_count<T>(std::min(chunk, V), D, N) : 1;
   L.n_valid = take(4);
   L.gm = take((size_t)N * L.ld_g * esz);
-  L.dh_acc = (need_dh && L.n_chunks > 1) ? take((size_t)N * D * 4) : 0;
+  L.dh_acc = (need_dh && (L.n_chunks > 1 || L.sh > 1)) ? take((size_t)L.sh * N * D * 4) : 0;
+  L.dw_part = (need_dw && L.sw > 1) ? take((size_t)L.sw * std::min(chunk, V) * D * 4) : 0;
   L.total = off;
   return L;
 }
@@ -598,20 +629,28 @@ int check_sizes(int64_t N, int64_t D, int64_t V, int dtype) {
   return TRI_OK;
 }
 
+// out (+)= A B^T; with splits > 1, K is cut into `splits` ranges of whole K
+// tiles, each writing fp32 partials at out + s * M * ldc (acc_in alike).
 template <typename T, bool TA, bool TB>
 int gemm_store(const gemm::Problem& p, const float* acc_in, void* out, bool out_f32, int64_t ldc,
-               hipStream_t st) {
+               hipStream_t st, int splits = 1) {
   typedef CfgT<T> C;
   const int tiles_m = (int)cdiv(p.M, C::BM), tiles_n = (int)cdiv(p.N, C::BN);
   const unsigned blocks = (unsigned)((int64_t)tiles_m * tiles_n);
+  const int64_t bkk = gemm::bk<C, T>();
+  const int64_t ks = splits > 1 ? cdiv(cdiv(p.K, splits), bkk) * bkk : p.K;
+  splits = splits > 1 ? (int)cdiv(p.K, ks) : 1;
+  const dim3 grid(blocks, (unsigned)splits);
+  const int64_t stride = p.M * ldc;
   if (out_f32)
-    gemm_store_kernel<T, float, TA, TB><<<blocks, C::THREADS, 0, st>>>(p, acc_in, (float*)out,
-                                                                       ldc, tiles_m, tiles_n);
+    gemm_store_kernel<T, float, TA, TB><<<grid, C::THREADS, 0, st>>>(p, acc_in, (float*)out, ldc,
+                                                                     tiles_m, tiles_n, ks, stride);
   else
-    gemm_store_kernel<T, T, TA, TB><<<blocks, C::THREADS, 0, st>>>(p, acc_in, (T*)out, ldc,
-                                                                   tiles_m, tiles_n);
+    gemm_store_kernel<T, T, TA, TB><<<grid, C::THREADS, 0, st>>>(p, acc_in, (T*)out, ldc,
+                                                                 tiles_m, tiles_n, ks, stride);
   return check_launch("linear_ce gemm");
 }
+
 
 template <typename T, typename TT>
 int fwd_impl(const void* hidden, const void* weight, const void* target, int64_t ignore_index,
@@ -651,7 +690,7 @@ int bwd_impl(const float* grad_out, const void* hidden, const void* weight, cons
   static_assert(sizeof(T) == 2, "16-bit backward (MN-contiguous GEMM operands)");
   const bool need_dh = dhidden != nullptr, need_dw = dweight != nullptr;
   if (!need_dh && !need_dw) return TRI_OK;
-  const BwdLayout L = bwd_layout(N, D, V, (int)sizeof(T), need_dh, chunk_rows);
+  const BwdLayout L = bwd_layout<T>(N, D, V, need_dh, need_dw, chunk_rows);
   if (ws_bytes < L.total) return fail(TRI_EINVAL, "linear_ce backward: workspace too small");
   char* w = (char*)ws;
   float* n_valid = (float*)(w + L.n_valid);
@@ -659,6 +698,7 @@ int bwd_impl(const float* grad_out, const void* hidden, const void* weight, cons
   if (int e = check_launch("linear_ce count")) return e;
   T* gm = (T*)(w + L.gm);
   float* dh_acc = L.dh_acc ? (float*)(w + L.dh_acc) : nullptr;
+  float* dw_part = L.dw_part ? (float*)(w + L.dw_part) : nullptr;
   for (int64_t c = 0; c < L.n_chunks; ++c) {
     const int64_t vc0 = c * L.chunk;
     const int64_t vc = std::min<int64_t>(L.chunk, V - vc0);
@@ -679,19 +719,37 @@ int bwd_impl(const float* grad_out, const void* hidden, const void* weight, cons
     const T* wc = (const T*)weight + vc0 * D;
     if (need_dw) {
       // dW[vc0 : vc0 + vc, :] = G^T H: A[v][n] = G[n][v] and B[d][n] = H[n][d],
-      // both MN-contiguous; the whole token reduction in one product, rounded once
+      // both MN-contiguous; the token reduction in one product (or in sw
+      // fp32 partials summed in order), rounded once
       gemm::Problem p{gm, hidden, L.ld_g, D, vc, D, N};
-      if (int e = gemm_store<T, true, true>(p, nullptr, (T*)dweight + vc0 * D, false, D, st))
-        return e;
+      T* dst = (T*)dweight + vc0 * D;
+      if (L.sw == 1) {
+        if (int e = gemm_store<T, true, true>(p, nullptr, dst, false, D, st)) return e;
+      } else {
+        if (int e = gemm_store<T, true, true>(p, nullptr, dw_part, true, D, st, L.sw)) return e;
+        if (int e = tritium_sum_splits(dw_part, dst, L.sw, vc * D, std::is_same<T, bf16_t>::value ? kBF16 : kF16, st))
+          return e;
+      }
     }
     if (need_dh) {
-      // dH[N, D] (+)= G W_c: A = G (K-contiguous), B[d][v] = W_c[v][d] (MN-contiguous)
+      // dH[N, D] (+)= G W_c: A = G (K-contiguous), B[d][v] = W_c[v][d] (MN-contiguous);
+      // with one chunk and no split straight into dH, else into sh fp32
+      // accumulators (one per K split, each summed over the chunks in order)
+      // that a fixed-order sum rounds once after the last chunk
       gemm::Problem p{gm, wc, L.ld_g, D, N, D, vc};
       const bool last = c + 1 == L.n_chunks;
-      const float* in = c > 0 ? dh_acc : nullptr;
-      if (int e = last ? gemm_store<T, false, true>(p, in, dhidden, false, D, st)
-                       : gemm_store<T, false, true>(p, in, dh_acc, true, D, st))
-        return e;
+      if (dh_acc == nullptr) {
+        if (int e = gemm_store<T, false, true>(p, nullptr, dhidden, false, D, st)) return e;
+      } else if (L.sh == 1 && last) {
+        if (int e = gemm_store<T, false, true>(p, dh_acc, dhidden, false, D, st)) return e;
+      } else {
+        if (int e = gemm_store<T, false, true>(p, c > 0 ? dh_acc : nullptr, dh_acc, true, D, st, L.sh))
+          return e;
+        if (last) {
+          if (int e = tritium_sum_splits(dh_acc, dhidden, L.sh, N * D, std::is_same<T, bf16_t>::value ? kBF16 : kF16, st))
+            return e;
+        }
+      }
     }
   }
   return TRI_OK;
@@ -758,9 +816,10 @@ extern "C" size_t tritium_linear_ce_bwd_workspace_size(int64_t n_rows, int64_t h
                                                        int64_t vocab, int dtype,
                                                        int need_dhidden, int need_dweight,
                                                        int64_t chunk_rows) {
-  (void)need_dweight;
   if (n_rows <= 0 || vocab <= 0 || hidden_size <= 0 || dtype == kF32) return 0;
-  return bwd_layout(n_rows, hidden_size, vocab, 2, need_dhidden != 0, chunk_rows).total;
+  return bwd_layout<bf16_t>(n_rows, hidden_size, vocab, need_dhidden != 0, need_dweight != 0,
+                            chunk_rows)
+      .total;
 }
 
 extern "C" int tritium_linear_ce_bwd(const float* grad_out, const void* hidden, const void* weight,

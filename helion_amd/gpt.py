@@ -47,7 +47,9 @@ import torch.nn.functional as F
 from . import _lib
 from .adamw import adamw_step_mixed
 from .attention import attention
-from .linear_ce import linear_cross_entropy
+from .embedding import embedding_backward
+from .linear_ce import _backward as _lce_backward
+from .linear_ce import _linear_cross_entropy_forward
 from .rmsnorm import residual_rmsnorm
 from .rope import rope_rows
 from .swiglu import swiglu_rows, swiglu_rows_backward
@@ -209,7 +211,8 @@ class HipGPT:
         nh, hd = cfg.n_heads, cfg.head_dim
         pos = torch.arange(s, device=tokens.device).repeat(b)
         cos, sin = self.cos[:s], self.sin[:s]
-        delta = self._w("embed")[tokens]
+        tied = _TiedGrad()
+        delta = _TiedEmbed.apply(self._w("embed"), tokens, tied)
         residual = torch.zeros_like(delta)
         t, d = b * s, cfg.d_model
         for i in range(cfg.n_layers):
@@ -225,7 +228,7 @@ class HipGPT:
             h = _GateUpSwiGLU.apply(_Proj.apply(normed.view(t, d), self._w(p + "w_gu")))
             delta = _Proj.apply(h, self._w(p + "w_down")).view(b, s, d)
         hidden, _ = residual_rmsnorm(delta, residual, self._w("final_norm"), cfg.eps)
-        return linear_cross_entropy(hidden, self._w("embed"), targets)
+        return _TiedHeadCE.apply(hidden, self._w("embed"), targets, tied)
 
     def train_step(self, tokens: torch.Tensor, targets: torch.Tensor) -> torch.Tensor:
         """One step: forward, backward, fp32-master AdamW; returns the loss."""
@@ -307,6 +310,62 @@ class TorchTwin:
         self.last_grad_norm = float(torch.norm(torch.stack([
             work[k].grad.float().norm() for k in self.master])))
         return loss.detach()
+
+
+class _TiedGrad:
+    """Carries the output head's weight gradient from the head's backward (which
+    autograd runs first) to the embedding gather's backward (which it runs
+    last), so the two gradients of the tied weight are summed in one pass."""
+
+    def __init__(self) -> None:
+        self.dw: torch.Tensor | None = None
+
+
+class _TiedHeadCE(torch.autograd.Function):
+    """linear_cross_entropy(hidden, weight, targets) whose weight gradient goes
+    to the ``_TiedGrad`` holder instead of to autograd (the gather's backward
+    returns the tied weight's whole gradient)."""
+
+    @staticmethod
+    def forward(ctx, hidden, weight, targets, holder):
+        n = targets.numel()
+        loss, lse = _linear_cross_entropy_forward(hidden, weight, targets)
+        ctx.holder = holder
+        ctx.save_for_backward(hidden.view(n, hidden.shape[-1]), weight, targets.view(n), lse)
+        ctx.hidden_shape = tuple(hidden.shape)
+        return loss
+
+    @staticmethod
+    def backward(ctx, g):
+        hidden_2d, weight, targets, lse = ctx.saved_tensors
+        dh, dw = _lce_backward(g, hidden_2d, weight, targets, lse, ctx.needs_input_grad[0], True,
+                               -100)
+        ctx.holder.dw = dw
+        return (dh.view(ctx.hidden_shape) if dh is not None else None), None, None, None
+
+
+class _TiedEmbed(torch.autograd.Function):
+    """weight[tokens] (helion/nn.py:24-28); the backward adds the scatter of the
+    upstream rows into the head's weight gradient from the holder, in place,
+    with ``tritium_embedding_bwd`` (deterministic: token-order fp32 sums, one
+    rounding), replacing torch's sort + scatter and the separate add."""
+
+    @staticmethod
+    def forward(ctx, weight, tokens, holder):
+        ctx.holder = holder
+        ctx.save_for_backward(tokens)
+        ctx.weight_shape, ctx.dtype = tuple(weight.shape), weight.dtype
+        return F.embedding(tokens, weight)
+
+    @staticmethod
+    def backward(ctx, dx):
+        (tokens,) = ctx.saved_tensors
+        dw, ctx.holder.dw = ctx.holder.dw, None
+        if dw is None:
+            dw = torch.zeros(ctx.weight_shape, device=dx.device, dtype=ctx.dtype)
+        d = ctx.weight_shape[1]
+        embedding_backward(tokens.reshape(-1), dx.reshape(-1, d), dw, out=dw)
+        return dw, None, None
 
 
 class _QKVRope(torch.autograd.Function):

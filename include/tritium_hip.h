@@ -264,6 +264,27 @@ int tritium_linear_ce_grad_logits(const float* grad_out, const float* n_valid, c
                                   int64_t n_rows, int64_t hidden_size, int64_t vocab, int64_t v0,
                                   int64_t vc, int dtype, void* stream);
 
+/* ---- Embedding backward with a tied output head ---------------------------
+ * No tritium.ops counterpart: replaces torch's backward of the gather in the
+ * reference's Embedding (helion/nn.py:24-28, weight[ids]; torch sorts the ids
+ * and scatter-adds) and, for an embedding tied to the output head
+ * (examples/common.py), the separate add of the head's weight gradient:
+ *   dw_out[v] = dw_in[v] + sum over tokens i with ids[i] == v of dx[i]
+ * summed in fp32 in token order and rounded once (bitwise deterministic: the
+ * tokens are bucketed by vocabulary row with integer counts, and each row
+ * sums its tokens in order; no floating-point atomics).  ids:
+ * [n_tokens] int32 (id_kind 1) or int64 (2); dx: [n_tokens, dim] with row
+ * stride ld_dx; dw_in, dw_out: [vocab, dim] contiguous, all in `dtype`.
+ * dw_out may be dw_in (rows no id names are then left as they are).  Ids
+ * outside [0, vocab) contribute nothing.  workspace:
+ * tritium_embedding_bwd_workspace_size bytes (counts and the bucketed token
+ * list; cleared by the call itself). */
+size_t tritium_embedding_bwd_workspace_size(int64_t n_tokens, int64_t vocab, int64_t dim);
+int tritium_embedding_bwd(const void* ids, int id_kind, int64_t n_tokens, const void* dx,
+                          int64_t ld_dx, const void* dw_in, void* dw_out, int64_t vocab,
+                          int64_t dim, void* workspace, size_t workspace_bytes, int dtype,
+                          void* stream);
+
 /* ---- Split-K finish -------------------------------------------------------
  * dst[i] = (dtype)(src[0 * n + i] + src[1 * n + i] + ... + src[(n_splits - 1) * n + i]),
  * summed in fp32 in split order, for src [n_splits, n] float32 (the fp32

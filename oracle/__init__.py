@@ -22,11 +22,12 @@ docstring of every module; the CPU test-suite (``tests/test_oracle.py``)
 runs those checks.
 """
 
-from . import adamw, attention, linear_ce, numerics, rmsnorm, rope, swiglu, torch_ref
+from . import adamw, attention, embedding, linear_ce, numerics, rmsnorm, rope, swiglu, torch_ref
 
 __all__ = [
     "adamw",
     "attention",
+    "embedding",
     "linear_ce",
     "numerics",
     "rmsnorm",

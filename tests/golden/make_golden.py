@@ -1,4 +1,5 @@
-"""Write the golden fixtures under tests/golden/ (run: python tests/golden/make_golden.py).
+"""Write the golden fixtures under tests/golden/ (run: python tests/golden/make_golden.py
+[name ...]; no names = all of them).
 
 The reference's own implementation cannot run here (it needs Triton and a
 GPU), and it holds no golden vectors.  Its tests compare each kernel against
@@ -14,6 +15,8 @@ those expected values, computed in float64 by torch's *library* routines
              repeat_interleave                                    (tests/tritium/test_attention.py:9-21)
 * linear_ce: torch.nn.functional.cross_entropy(linear(h, W), t, ignore_index=-100) + autograd
                                                                   (tests/tritium/test_cross_entropy.py:72, 93)
+* embedding: torch.nn.functional.embedding + autograd, plus the tied head's weight gradient
+                                                                  (helion/nn.py:24-28)
 
 Each fixture is an .npz of plain arrays (no pickles).
 """
@@ -148,6 +151,25 @@ def linear_ce():
          lse=torch.logsumexp(logits.detach(), dim=-1), dhidden=hs.grad, dweight=ws.grad)
 
 
+def embedding():
+    # tied embedding: the gather's scatter-add gradient plus the head's weight
+    # gradient; ids repeat (rows hit several times) and leave rows untouched
+    g = gen(106)
+    vocab, dim, n = 40, 12, 60
+    w = torch.randn(vocab, dim, generator=g, dtype=D)
+    ids = torch.randint(0, vocab // 2, (n,), generator=g)
+    ids[::7] = 3  # one frequent id
+    dx = torch.randn(n, dim, generator=g, dtype=D)
+    dw_head = torch.randn(vocab, dim, generator=g, dtype=D)
+    ws = w.clone().requires_grad_(True)
+    loss = (F.embedding(ids, ws) * dx).sum() + (ws * dw_head).sum()
+    loss.backward()
+    save("embedding", ids=ids, dx=dx, dw_head=dw_head, dw=ws.grad)
+
+
 if __name__ == "__main__":
-    for fn in (rmsnorm, rope, swiglu, adamw, attention, linear_ce):
-        fn()
+    import sys
+
+    fns = {f.__name__: f for f in (rmsnorm, rope, swiglu, adamw, attention, linear_ce, embedding)}
+    for name in (sys.argv[1:] or list(fns)):
+        fns[name]()

@@ -191,6 +191,9 @@ def test_linear_ce_empty_rows():
     (64, 40, 300, 0.0, torch.int64, 0),       # hidden_size padded to 48
     (300, 264, 1537, 0.02, torch.int64, 512), # 3 chunks, the last one 513 rows
     (513, 96, 640, 0.0, torch.int32, 256),    # K tiles of 64 tokens plus a partial one
+    (300, 264, 5000, 0.02, torch.int64, 0),   # dH split over K (4 fp32 partials, summed in order)
+    (2100, 64, 600, 0.01, torch.int64, 0),    # dW split over the tokens (2 partials)
+    (300, 64, 6000, 0.0, torch.int32, 2560),  # 3 chunks with dH split in 2
 ])
 def test_linear_ce_mfma_backward_edges(dtype, n, d, v, ignore_frac, tdtype, chunk):
     print(f"[lce bwd] {dtype} n={n} d={d} v={v} chunk={chunk}", flush=True)

@@ -331,3 +331,51 @@ def test_torch_ref_formulas_agree_with_library_routines():
     v = torch.randn(1, 2, 10, 16, generator=g)
     o_np, _ = oracle.attention.forward(q.numpy(), k.numpy(), v.numpy(), True)
     assert np.allclose(oracle.torch_ref.attention(q, k, v, True).numpy(), o_np, atol=1e-5)
+
+
+def test_torch_ref_rmsnorm_backward_and_rope_against_golden():
+    """The CPU-baseline RMSNorm backward and RoPE formulas against the golden fixtures
+    (torch's F.rms_norm autograd; complex multiplication and its autograd)."""
+    g = fixture("rmsnorm")
+    x, w, dy = (torch.from_numpy(g[k]) for k in ("x", "w", "dy"))
+    dx, dw = oracle.torch_ref.rmsnorm_backward(dy, x, w, float(g["eps"]))
+    assert close(dx.numpy(), g["dx"], 1e-5) and close(dw.numpy(), g["dw"], 1e-5)
+    r = fixture("rope")
+    q, k, cos, sin, pos = (torch.from_numpy(r[n]) for n in ("q", "k", "cos", "sin", "pos"))
+    qo, ko = oracle.torch_ref.rope(q, k, cos, sin, pos)
+    assert close(qo.numpy(), r["q_out_0"], 1e-5) and close(ko.numpy(), r["k_out_0"], 1e-5)
+    # the backward of a rotation is the inverse rotation
+    dq, _ = oracle.torch_ref.rope(torch.from_numpy(r["dq_out"]), k, cos, sin, pos, inverse=True)
+    assert close(dq.numpy(), r["dq_0"], 1e-5)
+    # planted mistake: the forward rotation used as the backward
+    dq_wrong, _ = oracle.torch_ref.rope(torch.from_numpy(r["dq_out"]), k, cos, sin, pos)
+    assert not close(dq_wrong.numpy(), r["dq_0"], 1e-3)
+
+
+# -------------------------------------------------------------- embedding --
+def test_embedding_backward_against_torch_golden():
+    g = fixture("embedding")
+    got = oracle.embedding.backward(g["ids"], g["dx"], g["dw_head"])
+    assert close(got, g["dw"], 1e-6)
+    assert (np.bincount(g["ids"]) > 1).any()  # the fixture repeats ids
+
+
+def test_embedding_backward_distinct_ids_closed_form():
+    rng = np.random.default_rng(3)
+    vocab, dim = 50, 8
+    ids = rng.permutation(vocab)[:20]
+    dx = rng.standard_normal((20, dim)).astype(np.float32)
+    dw = rng.standard_normal((vocab, dim)).astype(np.float32)
+    got = oracle.embedding.backward(ids, dx, dw)
+    want = dw.astype(np.float64).copy()
+    want[ids] += dx
+    assert close(got, want, 1e-6)
+    # out-of-range ids contribute nothing
+    assert close(oracle.embedding.backward(np.array([-1, vocab]), dx[:2], dw), dw, 0)
+
+
+def test_embedding_backward_planted_dropped_repeat_is_rejected():
+    g = fixture("embedding")
+    wrong = g["dw_head"].copy()
+    wrong[g["ids"]] += g["dx"]  # fancy-index += keeps one of each repeated id
+    assert not close(wrong, g["dw"], 1e-3)
