@@ -484,8 +484,15 @@ struct BtDma1 {
     for (int i = 0; i < PER; ++i) off[i] = fast ? offset(lane, wv, i, sx, 63) : 0u;
   }
   __device__ __forceinline__ void issue(char* dst, const T* x, int64_t sx, int r0, int n_rows) const {
-    const T* bx = x + (int64_t)r0 * sx;
-    if (fast && r0 + 64 <= n_rows) {
+    issue_at(dst, x + (int64_t)r0 * sx, sx, n_rows - r0);
+  }
+  // DMA i of this wavefront's share of a full tile from bx (init's offsets)
+  __device__ __forceinline__ void issue_one(char* dst, const T* bx, int i) const {
+    dma16s(bx, off[i], __builtin_amdgcn_readfirstlane(lds_addr(dst + (wv * PER + i) * 1024)));
+  }
+  // the tile whose first row is bx, with rows_left rows from bx on
+  __device__ __forceinline__ void issue_at(char* dst, const T* bx, int64_t sx, int rows_left) const {
+    if (fast && rows_left >= 64) {
 #pragma unroll
       for (int i = 0; i < PER; ++i)
         dma16s(bx, off[i], __builtin_amdgcn_readfirstlane(lds_addr(dst + (wv * PER + i) * 1024)));
@@ -496,15 +503,15 @@ struct BtDma1 {
     if (fast) {
 #pragma unroll
       for (int i = 0; i < PER; ++i)
-        dma16s(bx, offset(lane, wv, i, sx, n_rows - 1 - r0),
+        dma16s(bx, offset(lane, wv, i, sx, rows_left - 1),
                __builtin_amdgcn_readfirstlane(lds_addr(dst + (wv * PER + i) * 1024)));
     } else {
 #pragma unroll
       for (int i = 0; i < PER; ++i) {
         const int trow = (wv * PER + i) * P::DMA_ROWS + lane / P::GR;
-        const int row = min(r0 + trow, n_rows - 1);
+        const int row = min(trow, rows_left - 1);
         const int c = (lane % P::GR) ^ P::key(trow);
-        dma16(x + (int64_t)row * sx + c * 8,
+        dma16(bx + (int64_t)row * sx + c * 8,
               __builtin_amdgcn_readfirstlane(lds_addr(dst + (wv * PER + i) * 1024)));
       }
     }
@@ -572,11 +579,38 @@ struct BtOffs {
     return *reinterpret_cast<const V*>(tile + row[st] + rb * P::RB);
   }
   __device__ __forceinline__ V rd_tr(const char* tile, int rb, int mt) const {
+    return rd_tr(tr_base(tile), rb, mt);
+  }
+  // The lane's transposing-read addresses in one tile (its 32-bit LDS
+  // address plus the lane offsets), computed once per tile and made opaque:
+  // the row block then goes into each read's immediate offset.  Left to
+  // itself the compiler reassociates tile + (offset + row block), keeps the
+  // 4 D / 16 sums of the last two in registers for the whole kernel and
+  // spends one or two VALU ops per read rebasing them.
+  struct TrBase {
+    uint32_t v[MT][2];
+  };
+  __device__ __forceinline__ TrBase tr_base(const char* tile) const {
+    TrBase r;
+    const uint32_t t = lds_addr(tile);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        uint32_t x = t + tr[mt][k];
+        asm("" : "+v"(x));
+        r.v[mt][k] = x;
+      }
+    }
+    return r;
+  }
+  __device__ __forceinline__ V rd_tr(const TrBase& bs, int rb, int mt) const {
     typedef short v4s __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) v4s lds_v4s;
     const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) v4s*)(lds_addr(tile + tr[mt][0] + rb * P::RB)));
+        (lds_v4s*)(uintptr_t)(bs.v[mt][0] + (uint32_t)(rb * P::RB)));
     const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) v4s*)(lds_addr(tile + tr[mt][1] + rb * P::RB)));
+        (lds_v4s*)(uintptr_t)(bs.v[mt][1] + (uint32_t)(rb * P::RB)));
     return __builtin_bit_cast(V, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
   }
 };
@@ -811,7 +845,8 @@ __device__ __forceinline__ void pp_mfma(bool dpv, bool ds, const char* Vs, const
   constexpr int MT = D / 32, NP = 4 * MT, NS = 2 * (D / 16);
   static_assert(NP % kRing == 0 && NS >= kRing, "ring");
   auto kread = [&](int i) { return fo.rd_row(Ks, 32 * (i & 1), i >> 1); };
-  auto vread = [&](int i) { return fo.rd_tr(Vs, 16 * (i / MT), i % MT); };
+  const typename BtOffs<T, D>::TrBase vb = fo.tr_base(Vs);
+  auto vread = [&](int i) { return fo.rd_tr(vb, 16 * (i / MT), i % MT); };
   if (dpv) {
 #pragma unroll
     for (int i = 0; i < NP; ++i) {
@@ -983,9 +1018,9 @@ attn_fwd_pp(FwdArgs a) {
         }
         l += (ls[0] + ls[1]) + (ls[2] + ls[3]);
         // first V^T operands of MFMA(j + 1), read ahead of its barrier
-        const char* Vn = smem + (j % kPPStages) * STAGE + P::BYTES;
+        const auto vn = fo.tr_base(smem + (j % kPPStages) * STAGE + P::BYTES);
 #pragma unroll
-        for (int i = 0; i < kRing; ++i) rb[i] = fo.rd_tr(Vn, 16 * (i / MT), i % MT);
+        for (int i = 0; i < kRing; ++i) rb[i] = fo.rd_tr(vn, 16 * (i / MT), i % MT);
       }
       // publish tile j + 1 (tile j + 2's DMAs may stay in flight)
       if (j + 2 < n_kv) wait_vmcnt<Dma::PER>();
@@ -1494,6 +1529,10 @@ attn_bwd_dkdv_v2(BwdArgs a) {
 constexpr int kPairWaves = 8;
 constexpr int kPairBN = 128;
 constexpr int kDkvPPStages = 3;
+#ifndef TRI_ATTN_DKDV_RING
+#define TRI_ATTN_DKDV_RING 8
+#endif
+constexpr int kDkvRing = TRI_ATTN_DKDV_RING;  // MFMA operands in flight ahead of use
 
 template <typename T, int D>
 __global__ void __launch_bounds__(64 * kPairWaves, 1)  // 2 wavefronts per SIMD
@@ -1537,97 +1576,172 @@ attn_bwd_dkdv_pair(BwdArgs a) {
   const int q_begin = a.causal ? kv0 : 0;
   const int n_q = a.Tq > q_begin ? (int)cdiv(a.Tq - q_begin, 64) : 0;
   const int n_steps = n_q * group;
+  const int q_end = q_begin + 64 * n_q;
   BtOffs<T, D> fo;
   fo.init();
-  // role A streams the dO tiles, role B the Q tiles with lse and D
-  BtDma1<T, D, 4> dma;
-  dma.init(role_b ? a.sq_s : a.sdo_s, role_b ? 4 : 0);
-  auto q0_of = [&](int step) { return q_begin + (step % n_q) * 64; };
-  auto stage = [&](int step) { return smem + (step % kDkvPPStages) * STAGE; };
-  auto issue = [&](int step) {
-    const int hq = hk * group + step / n_q;
-    const int q0 = q0_of(step);
-    char* st = stage(step);
-    if (role_b) {
-      dma.issue(st, (const T*)a.q + b * a.sq_b + hq * a.sq_h, a.sq_s, q0, a.Tq);
-      const int64_t row = ((int64_t)b * a.H + hq) * a.Tq + min(q0 + lane, a.Tq - 1);
-      if (wave == 4) dma4(a.lse + row, __builtin_amdgcn_readfirstlane(lds_addr(st + 2 * P::BYTES)));
-      if (wave == 5)
-        dma4(a.delta + row, __builtin_amdgcn_readfirstlane(lds_addr(st + 2 * P::BYTES + 256)));
+  typedef typename BtOffs<T, D>::TrBase TrBase;
+  // Role A streams every tile: Q and dO (a quarter of each per wavefront,
+  // issued between the MFMAs of its MFMA phase, whose issue slots are
+  // mostly free), lse (wavefront 0) and D (wavefront 1).  Steps run over the
+  // query tiles from the last one down (then the next query head), so that
+  // the workgroups of one kv head, started together, read the same tiles at
+  // about the same time.  The tile the next issue loads is advanced one step
+  // per issue: the loop divides by nothing.
+  BtDma1<T, D, 4> dq_dma, do_dma;
+  dq_dma.init(a.sq_s, 0);
+  do_dma.init(a.sdo_s, 0);
+  constexpr int PER = BtDma1<T, D, 4>::PER;
+  const int q_last = q_end - 64;
+  const int hq0 = hk * group;
+  const T* q_head = (const T*)a.q + b * a.sq_b + hq0 * a.sq_h;
+  const T* do_head = (const T*)a.dout + b * a.sdo_b + hq0 * a.sdo_h;
+  const T* q_src = q_head + (int64_t)q_last * a.sq_s;
+  const T* do_src = do_head + (int64_t)q_last * a.sdo_s;
+  const float* lse_h = a.lse + ((int64_t)b * a.H + hq0) * a.Tq;
+  const float* del_h = a.delta + ((int64_t)b * a.H + hq0) * a.Tq;
+  int ld_q0 = q_last, ld_stage = 0;
+  // a full tile whose DMAs take the per-lane offsets of init (else clamped rows)
+  auto ld_fast = [&]() { return dq_dma.fast && do_dma.fast && ld_q0 + 64 <= a.Tq; };
+  auto issue_stats = [&]() {
+    char* st = smem + ld_stage * STAGE;
+    const int r = min(ld_q0 + lane, a.Tq - 1);
+    if (wave == 0) dma4(lse_h + r, __builtin_amdgcn_readfirstlane(lds_addr(st + 2 * P::BYTES)));
+    if (wave == 1) dma4(del_h + r, __builtin_amdgcn_readfirstlane(lds_addr(st + 2 * P::BYTES + 256)));
+  };
+  // DMA k of this wavefront's share of the tile: k < PER of Q, then of dO
+  auto issue_part = [&](int k) {
+    char* st = smem + ld_stage * STAGE;
+    if (k < PER) dq_dma.issue_one(st, q_src, k);
+    else do_dma.issue_one(st + P::BYTES, do_src, k - PER);
+  };
+  auto issue_all = [&]() {
+    char* st = smem + ld_stage * STAGE;
+    issue_stats();
+    dq_dma.issue_at(st, q_src, a.sq_s, a.Tq - ld_q0);
+    do_dma.issue_at(st + P::BYTES, do_src, a.sdo_s, a.Tq - ld_q0);
+  };
+  auto advance = [&]() {
+    ld_stage = ld_stage == kDkvPPStages - 1 ? 0 : ld_stage + 1;
+    if (ld_q0 == q_begin) {
+      ld_q0 = q_last;
+      q_head += a.sq_h;
+      do_head += a.sdo_h;
+      q_src = q_head + (int64_t)q_last * a.sq_s;
+      do_src = do_head + (int64_t)q_last * a.sdo_s;
+      lse_h += a.Tq;
+      del_h += a.Tq;
     } else {
-      dma.issue(st + P::BYTES, (const T*)a.dout + b * a.sdo_b + hq * a.sdo_h, a.sdo_s, q0, a.Tq);
+      ld_q0 -= 64;
+      q_src -= 64 * a.sq_s;
+      do_src -= 64 * a.sdo_s;
     }
   };
-  // pair-uniform: the query tile of step has rows at or past this pair's kv rows
-  auto active = [&](int step) { return !(a.causal && q0_of(step) + 63 < kvb); };
+  // pair-uniform: the query tile from q0 has rows at or past this pair's kv rows
+  auto active = [&](int q0) { return !(a.causal && q0 + 63 < kvb); };
 
-  // x[mq] = T1 frag^T over a tile's two 32-row query halves (MFMA i = 2 st + mq)
-  auto mma_rows = [&](const char* T1, f32x16 (&x)[2]) {
-    V rb[kRing];
+  // MFMA phase: acc^T += T2^T op over the previous tile (MFMA i = MT t + mt,
+  // t the 16-row slice), then x[mq] = T1 frag^T over the current one (MFMA
+  // i = 2 st + mq).  One kRing-deep operand ring runs from the first chain
+  // into the second; the caller has read the first kDkvRing T2 operands into
+  // it already (before the phase barrier).
+  constexpr int N2 = 4 * MT, N1 = 2 * KS, NPART = 2 * PER;
+  static_assert(N2 % kDkvRing == 0 && N1 >= kDkvRing, "operand ring");
+  static_assert(2 * NPART <= N2 && 2 * NPART <= N1, "DMA slots");
+  V ring[kDkvRing];
+  auto pre_tr = [&](const TrBase& b2) {
 #pragma unroll
-    for (int i = 0; i < kRing; ++i) rb[i] = fo.rd_row(T1, 32 * (i & 1), i >> 1);
-#pragma unroll
-    for (int i = 0; i < 2 * KS; ++i) {
-      sched_fence();
-      x[i & 1] = M::mma(rb[i % kRing], frag[i >> 1], i < 2 ? zero16() : x[i & 1]);
-      if (i + kRing < 2 * KS) rb[i % kRing] = fo.rd_row(T1, 32 * ((i + kRing) & 1), (i + kRing) >> 1);
-    }
-    sched_fence();
+    for (int i = 0; i < kDkvRing; ++i) ring[i] = fo.rd_tr(b2, 16 * (i / MT), i % MT);
   };
-  // acc^T += T2^T op (MFMA i = MT t + mt, t the 16-row slice of the tile)
-  auto mma_tr = [&](const char* T2, const V (&op)[4]) {
-    constexpr int N2 = 4 * MT;
-    V tb[kRing];
-#pragma unroll
-    for (int i = 0; i < kRing; ++i) tb[i] = fo.rd_tr(T2, 16 * (i / MT), i % MT);
+  // the first chain: acc^T += T2^T op, the ring then running on into the
+  // first T1 operands (read even when T1 is not multiplied after: a branch
+  // per MFMA costs more than the unused reads of a resident tile); with
+  // inter the next tile's DMAs go out after its odd MFMAs
+  auto tr_chain = [&](bool inter, const TrBase& b2, const char* T1, const V (&op)[4]) {
 #pragma unroll
     for (int i = 0; i < N2; ++i) {
       sched_fence();
-      acc[i % MT] = M::mma(tb[i % kRing], op[i / MT], acc[i % MT]);
-      if (i + kRing < N2) tb[i % kRing] = fo.rd_tr(T2, 16 * ((i + kRing) / MT), (i + kRing) % MT);
+      acc[i % MT] = M::mma(ring[i % kDkvRing], op[i / MT], acc[i % MT]);
+      const int n = i + kDkvRing;
+      if (n < N2) ring[i % kDkvRing] = fo.rd_tr(b2, 16 * (n / MT), n % MT);
+      else ring[i % kDkvRing] = fo.rd_row(T1, 32 * ((n - N2) & 1), (n - N2) >> 1);
+      if ((i & 1) && i < 2 * NPART && inter) issue_part(i >> 1);
     }
+  };
+  auto rows_chain = [&](const char* T1, f32x16 (&x)[2]) {
+#pragma unroll
+    for (int i = 0; i < N1; ++i) {
+      sched_fence();
+      x[i & 1] = M::mma(ring[i % kDkvRing], frag[i >> 1], i < 2 ? zero16() : x[i & 1]);
+      const int n = i + kDkvRing;
+      if (n < N1) ring[i % kDkvRing] = fo.rd_row(T1, 32 * (n & 1), n >> 1);
+    }
+  };
+  // dtr: tr_chain (the ring pre-read by the caller), drows: rows_chain;
+  // inter: the next tile's DMAs interleaved with tr_chain (needs dtr)
+  auto mfma_phase = [&](bool dtr, bool drows, bool inter, const TrBase& b2, const char* T1,
+                        const V (&op)[4], f32x16 (&x)[2]) {
+    if (dtr) {
+      tr_chain(inter, b2, T1, op);
+    } else {
+#pragma unroll
+      for (int i = 0; i < kDkvRing; ++i) ring[i] = fo.rd_row(T1, 32 * (i & 1), i >> 1);
+    }
+    if (drows) rows_chain(T1, x);
     sched_fence();
   };
 
-  if (n_steps > 0) issue(0);
+  // (role A's wavefronts only: the DMA offsets of init cover a tile with
+  // wavefronts 0..3)
+  if (n_steps > 0 && !role_b) {
+    issue_all();
+    advance();
+  }
   wait_vmcnt<0>();
   lds_barrier();
   f32x16 x[2];
   V op[4];  // MFMA operand: slice t = 2 mq + u holds query rows 16t + 4g + {0..3}, 16t + 8 + 4g + {0..3}
+  // per step s: q0 of s and s - 1, the LDS stage of s (s - 1 is the stage before it)
+  int q0c = q_last, q0p = q_last, sc = 0;
   if (!role_b) {
     for (int s = 0; s <= n_steps; ++s) {
-      const bool cur = s < n_steps && active(s), prev = s >= 1 && active(s - 1);
-      // half-step 2s: dV^T += dO_{s-1}^T P_{s-1}, S_s = Q_s K^T
+      const int sp = sc == 0 ? kDkvPPStages - 1 : sc - 1;
+      char* const stc = smem + sc * STAGE;
+      const bool cur = s < n_steps && active(q0c), prev = s >= 1 && active(q0p);
+      // half-step 2s: dV^T += dO_{s-1}^T P_{s-1}, S_s = Q_s K^T (the first dO
+      // operands were read ahead, at the end of half-step 2s - 1), and the
+      // DMAs of tile s + 1 (into the stage of tile s - 2, whose last reads
+      // were in half-step 2s - 1)
+      const bool nxt = s + 1 < n_steps;
+      const bool inter = nxt && prev && ld_fast();
+      if (nxt && !inter) issue_all();
+      if (inter) issue_stats();
 #if TRI_ATTN_PP_PRIO
       __builtin_amdgcn_s_setprio(1);
 #endif
-      if (prev) mma_tr(stage(s + kDkvPPStages - 1) + P::BYTES, op);
-      if (cur) mma_rows(stage(s), x);
+      mfma_phase(prev, cur, inter, fo.tr_base(smem + sp * STAGE + P::BYTES), stc, op, x);
 #if TRI_ATTN_PP_PRIO
       __builtin_amdgcn_s_setprio(0);
 #endif
-      wait_vmcnt<0>();  // dO_s (issued in half-step 2s - 1)
+      if (nxt) advance();
       lds_barrier();
-      // half-step 2s + 1: P_s
-      if (s + 1 < n_steps) issue(s + 1);
+      // half-step 2s + 1: P_s (lse_s scaled by log2 e in half-step 2s)
       if (cur) {
-        const int q0 = q0_of(s);
-        const float* lse_s = reinterpret_cast<const float*>(stage(s) + 2 * P::BYTES);
-        const bool need_mask = (a.causal && q0 < kvb + 31) || q0 + 64 > a.Tq;
+        const float* lse_s = reinterpret_cast<const float*>(stc + 2 * P::BYTES);
+        const bool need_mask = (a.causal && q0c < kvb + 31) || q0c + 64 > a.Tq;
 #pragma unroll
         for (int mq = 0; mq < 2; ++mq) {
           // x[mq][r] = S[q0 + 32mq + 8(r/4) + 4g + r%4][kvw]; masked scores -> -inf (P = 0)
           if (need_mask) {
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
-              const int q = q0 + 32 * mq + 8 * (r >> 2) + 4 * g + (r & 3);
+              const int q = q0c + 32 * mq + 8 * (r >> 2) + 4 * g + (r & 3);
               x[mq][r] = (q >= a.Tq || (a.causal && kvw > q)) ? -INFINITY : x[mq][r];
             }
           }
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) {
             const float4 L = *reinterpret_cast<const float4*>(lse_s + 32 * mq + 8 * rr + 4 * g);
-            const float lv[4] = {L.x * kLog2e, L.y * kLog2e, L.z * kLog2e, L.w * kLog2e};
+            const float lv[4] = {L.x, L.y, L.z, L.w};
             float4 pv;
             float* pf = reinterpret_cast<float*>(&pv);
 #pragma unroll
@@ -1639,16 +1753,31 @@ attn_bwd_dkdv_pair(BwdArgs a) {
             *reinterpret_cast<float4*>(xch + ((mq * 4 + rr) * 64 + lane) * 16) = pv;
           }
         }
+        // dO_s landed long ago: the first dV operands of half-step 2s + 2
+        // are read here, under the barrier wait
+        pre_tr(fo.tr_base(stc + P::BYTES));
       }
+      wait_vmcnt<0>();  // tile s + 1 (issued in half-step 2s)
       lds_barrier();
+      q0p = q0c;
+      q0c = q0c == q_begin ? q_last : q0c - 64;
+      sc = sc == kDkvPPStages - 1 ? 0 : sc + 1;
     }
   } else {
     for (int s = 0; s <= n_steps; ++s) {
-      const bool cur = s < n_steps && active(s), prev = s >= 1 && active(s - 1);
-      // half-step 2s: dS_{s-1}
-      if (s + 1 < n_steps) issue(s + 1);
+      const int sp = sc == 0 ? kDkvPPStages - 1 : sc - 1;
+      char* const stc = smem + sc * STAGE;
+      char* const stp = smem + sp * STAGE;
+      const bool cur = s < n_steps && active(q0c), prev = s >= 1 && active(q0p);
+      // half-step 2s: dS_{s-1}; lse_s (landed at the end of half-step
+      // 2s - 1) to log2 units for role A's exponentials, one value a lane
+      if (wave == 4 && s < n_steps) {
+        float* l = reinterpret_cast<float*>(stc + 2 * P::BYTES);
+        l[lane] *= kLog2e;
+      }
+      const TrBase qb = fo.tr_base(stp);
       if (prev) {
-        const float* del_s = reinterpret_cast<const float*>(stage(s + kDkvPPStages - 1) + 2 * P::BYTES + 256);
+        const float* del_s = reinterpret_cast<const float*>(stp + 2 * P::BYTES + 256);
 #pragma unroll
         for (int mq = 0; mq < 2; ++mq) {
 #pragma unroll
@@ -1661,19 +1790,22 @@ attn_bwd_dkdv_pair(BwdArgs a) {
               op[2 * mq + (rr >> 1)][4 * (rr & 1) + j] = (T)(pp[j] * (x[mq][4 * rr + j] - dd[j]));
           }
         }
+        // the first dK operands (Q_{s-1}^T) of the coming MFMA phase
+        pre_tr(qb);
       }
       lds_barrier();
       // half-step 2s + 1: dK^T += Q_{s-1}^T dS_{s-1}, dP_s = dO_s V^T
 #if TRI_ATTN_PP_PRIO
       __builtin_amdgcn_s_setprio(1);
 #endif
-      if (prev) mma_tr(stage(s + kDkvPPStages - 1), op);
-      if (cur) mma_rows(stage(s) + P::BYTES, x);
+      mfma_phase(prev, cur, false, qb, stc + P::BYTES, op, x);
 #if TRI_ATTN_PP_PRIO
       __builtin_amdgcn_s_setprio(0);
 #endif
-      wait_vmcnt<0>();  // Q, lse, D of tile s + 1 (issued in half-step 2s)
       lds_barrier();
+      q0p = q0c;
+      q0c = q0c == q_begin ? q_last : q0c - 64;
+      sc = sc == kDkvPPStages - 1 ? 0 : sc + 1;
     }
   }
 
