@@ -13,7 +13,8 @@ generated on a seeded CPU generator and are resident in HBM before timing.
 Also reported in the same line (``ops``): each op's time and fraction of its
 roofline, causal flash attention fwd+bwd [4, 32, 4096, 128] bf16 in TFLOP/s,
 fused linear-cross-entropy fwd+bwd N=8192 D=4096 V=128256 in TFLOP/s, and the
-reference PyTorch CPU path timed on this host's cores (``cpu_baseline``).
+reference PyTorch CPU path timed on this host's cores (``cpu_baseline``; the
+attention, linear-CE and GPT legs carry their own).
 
 Kernel times are measured with HIP events recorded on the stream every kernel
 is launched on (torch's current stream).
@@ -243,6 +244,8 @@ def attention_leg(torch, tritium, iters: int = 5, warmup: int = 2,
         "bwd_TFLOP/s": round(fb / (bwd_ms * 1e-3) / 1e12, 1),
         "TFLOP/s": round(tot, 1),
         "frac_mfma_peak": round(tot / MFMA_BF16_PEAK_TFLOPS, 4),
+        "roofline": mfma_roofline("attn_fwd_pp + attn_bwd_dq_v2 + attn_bwd_dkdv_pair (one fwd+bwd)",
+                                  ff + fb, fwd_ms + bwd_ms, "attention_config3_counters.txt"),
     }
 
 
@@ -281,6 +284,9 @@ def lce_leg(torch, tritium, iters: int = 3, warmup: int = 1, n=8192, d=4096, v=1
         "TFLOP/s": round(tot, 1),
         "frac_mfma_peak": round(tot / MFMA_BF16_PEAK_TFLOPS, 4),
         "flops_basis": "6NVD algorithmic",
+        "roofline": mfma_roofline("lce_fwd_kernel + lce_g_kernel + gemm_store_kernel (dW, dH) "
+                                  "+ sum_splits (one fwd+bwd)", ff + fb, fwd_ms + bwd_ms,
+                                  "linear_ce_config4_counters.txt"),
     }
 
 
@@ -546,15 +552,7 @@ def cpu_baseline(budget_s: float = 12.0):
     med = times[len(times) // 2]
     nbytes = (sum(rmsnorm_bytes(n_rows, ROWS_D)) + sum(rope_bytes(n_rows, ROPE_H, ROPE_HD, ROWS_T))
               + sum(swiglu_bytes(n_rows * SWIGLU_F)) + adamw_bytes(n_params))
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        model = platform.processor()
+    model = _cpu_model()
     return {
         "value": round(nbytes / med / 1e9, 3),
         "unit": "GB/s",
@@ -566,6 +564,142 @@ def cpu_baseline(budget_s: float = 12.0):
                    f"reference's test formulas; median of {len(times)} runs ({med:.3f} s each)"),
         "cpu_model": model,
     }
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor()
+
+
+def _time_cpu(fn, budget_s: float, min_runs: int = 2, max_runs: int = 20):
+    """Median wall time of ``fn`` (one untimed warm-up call first)."""
+    fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_runs or (time.perf_counter() - t_start < budget_s and len(times) < max_runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    times.sort()
+    return times[len(times) // 2], len(times)
+
+
+def attention_cpu_baseline(budget_s: float = 10.0, t: int = 4096, d: int = 128):
+    """The reference's attention formula (SDPA in float32, tests/tritium/
+    test_attention.py:9-21) forward+backward on this host's cores over a
+    sample of the config-3 workload: n_heads of the 4 x 32 (batch, head)
+    slices at T=4096, D=128, in TFLOP/s (the same causal flop convention)."""
+    import torch
+
+    from oracle import torch_ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    heads = 4
+    q, k, v, do = (torch.randn((1, heads, t, d), generator=g) for _ in range(4))
+    qs, ks, vs = (x.clone().requires_grad_(True) for x in (q, k, v))
+
+    def one():
+        o = torch_ref.attention(qs, ks, vs, is_causal=True)
+        o.backward(do)
+        qs.grad = ks.grad = vs.grad = None
+
+    med, n = _time_cpu(one, budget_s)
+    ff, fb = attention_flops(1, heads, t, d)
+    return {"value": round((ff + fb) / med / 1e12, 4), "unit": "TFLOP/s", "cores": cores,
+            "kind": "port", "cpu_model": _cpu_model(),
+            "sample": (f"{heads} of the 128 (batch, head) slices of config 3 (T={t}, D={d}, causal), "
+                       f"fp32 SDPA forward+backward through autograd; median of {n} runs "
+                       f"({med:.3f} s each)")}
+
+
+def lce_cpu_baseline(budget_s: float = 10.0, n_rows: int = 128, d: int = 4096, v: int = 128256):
+    """The reference's linear-cross-entropy formula (F.linear then
+    F.cross_entropy with ignore_index -100, float32; tests/tritium/
+    test_cross_entropy.py:72) forward+backward on this host's cores over
+    n_rows of the 8192 config-4 rows, full vocabulary, in TFLOP/s (6NVD)."""
+    import torch
+
+    from oracle import torch_ref
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    g = torch.Generator().manual_seed(0)
+    hidden = torch.randn((n_rows, d), generator=g).requires_grad_(True)
+    weight = (torch.randn((v, d), generator=g) * 0.02).requires_grad_(True)
+    target = torch.randint(0, v, (n_rows,), generator=g)
+
+    def one():
+        torch_ref.linear_cross_entropy(hidden, weight, target).backward()
+        hidden.grad = weight.grad = None
+
+    med, n = _time_cpu(one, budget_s)
+    ff, fb = lce_flops(n_rows, d, v)
+    del weight
+    return {"value": round((ff + fb) / med / 1e12, 4), "unit": "TFLOP/s", "cores": cores,
+            "kind": "port", "cpu_model": _cpu_model(),
+            "sample": (f"{n_rows} of the 8192 rows of config 4 (D={d}, V={v}), fp32 "
+                       f"F.linear + F.cross_entropy forward+backward through autograd; "
+                       f"median of {n} runs ({med:.3f} s each)")}
+
+
+def gpt_cpu_baseline(budget_s: float = 10.0):
+    """The config-5 training step as plain PyTorch (gpt.TorchTwin: the same
+    model, bf16 matmuls, fp32 master weights and torch.optim.AdamW) on this
+    host's cores, batch 1 x 1024 tokens instead of 16 x 1024, in tokens/s."""
+    import dataclasses
+
+    import torch
+
+    from helion_amd import gpt
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    cfg = gpt.GPTConfig()
+    tc = dataclasses.replace(gpt.TrainConfig(), batch=1)
+    twin = gpt.TorchTwin(cfg, tc, gpt.init_params(cfg, tc.seed), torch.device("cpu"))
+    gen = torch.Generator().manual_seed(1)
+    tokens, targets = gpt.lm_batch(cfg, tc, gen, torch.device("cpu"))
+    med, n = _time_cpu(lambda: twin.train_step(tokens, targets), budget_s, min_runs=1, max_runs=5)
+    del twin
+    ntok = tc.batch * tc.seq_len
+    return {"value": round(ntok / med, 1), "unit": "tokens/s", "cores": cores, "kind": "port",
+            "cpu_model": _cpu_model(),
+            "sample": (f"1 x {tc.seq_len} tokens of the 16 x {tc.seq_len} config-5 batch, one "
+                       f"TorchTwin training step (forward, backward, AdamW); median of {n} "
+                       f"steps ({med:.2f} s each)")}
+
+
+def _profile_figure(name: str, key: str):
+    """A number recorded in profiles/NAME as a line ``KEY: value`` (None if absent)."""
+    path = os.path.join(ROOT, "profiles", name)
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith(key + ":"):
+                return int(float(line.split(":", 1)[1].split()[0]))
+    return None
+
+
+def mfma_roofline(kernels: str, flops: float, ms: float, counters: str) -> dict:
+    """Roofline object of an MFMA-bound leg: algorithmic flops of one pass over
+    its time measured here, and the HBM bytes one pass moves as the counter
+    summary in profiles/COUNTERS records them."""
+    achieved = flops / (ms * 1e-3) / 1e12
+    return {"kernels": kernels, "bound": "mfma", "achieved": round(achieved, 1),
+            "peak": MFMA_BF16_PEAK_TFLOPS, "unit": "TFLOP/s",
+            "frac": round(achieved / MFMA_BF16_PEAK_TFLOPS, 4),
+            "traffic": _profile_figure(counters, "traffic_bytes_per_pass"),
+            "algorithmic_flops_per_pass": flops, "counters": f"profiles/{counters}"}
+
 
 
 def main(argv=None) -> int:
@@ -665,6 +799,14 @@ def main(argv=None) -> int:
         "algorithmic_bytes_per_launch": rows["adamw_bytes"],
     }
     cpu = None if args.no_cpu else cpu_baseline()
+    if not args.no_cpu:
+        # the other legs' reference PyTorch paths on the same host cores
+        for key, fn in (("attention_fwd_bwd", attention_cpu_baseline),
+                        ("linear_ce_fwd_bwd", lce_cpu_baseline),
+                        ("gpt_train_step", gpt_cpu_baseline)):
+            if isinstance(ops.get(key), dict):
+                ops[key]["cpu_baseline"] = fn()
+                print(f"[bench] cpu {key}: {ops[key]['cpu_baseline']}", file=sys.stderr, flush=True)
     line = {
         "metric": METRIC,
         "value": round(rows["value"], 1),

@@ -80,6 +80,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P,
          _I32, _I32, _P],
     ),
+    "tritium_attention_fwd_rope": (
+        _I32,
+        [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I32, _I32,
+         _P, _P, _P, _I32, _I64, _P],
+    ),
+    "tritium_attention_bwd_rope": (
+        _I32,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P,
+         _I32, _I32, _P, _P, _P, _I32, _I64, _P],
+    ),
     "tritium_attention_decode_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "tritium_attention_decode": (
         _I32,

@@ -229,3 +229,115 @@ def attention(
         o, _ = _attention_forward(q, k, v, is_causal)
         return o
     return _AttentionAutograd.apply(q, k, v, is_causal)
+
+
+# ------------------------------------------------------- RoPE on q's load --
+# Not part of the reference's surface: its model rotates q and k into new
+# tensors and then calls attention (helion/nn.py:196-220).  These run that
+# sequence with q rotated as the attention kernels load it, so no rotated
+# copy of q is written in the forward or kept for the backward; k arrives
+# rotated (tritium_rope_strided rotates it alone).
+
+
+def _check_rope_q(q, k, v, cos, sin, position_ids):
+    batch, n_heads, n_kv_heads, q_len, kv_len, head_dim = _check_attention_inputs(q, k, v)
+    if q.dtype not in (torch.bfloat16, torch.float16) or head_dim not in (64, 128):
+        raise ValueError("attention with rope on q needs bf16/fp16 tensors with head_dim 64 or "
+                         f"128, got {q.dtype} and head_dim {head_dim}")
+    for name, t in (("q", q), ("k", k), ("v", v)):
+        if not _rows_aligned(t):
+            raise ValueError(f"attention with rope on q: {name} needs a unit head_dim stride and "
+                             "16-byte aligned rows")
+    for name, t in (("cos", cos), ("sin", sin)):
+        if (t.dtype != torch.float32 or t.dim() != 2 or t.shape[1] != head_dim // 2
+                or not t.is_contiguous() or t.device != q.device):
+            raise ValueError(f"attention with rope on q: {name} must be a contiguous float32 "
+                             f"[max_position, {head_dim // 2}] tensor on {q.device}")
+    if cos.shape != sin.shape:
+        raise ValueError("attention with rope on q: cos and sin shapes differ")
+    if position_ids is not None:
+        if (position_ids.dtype not in (torch.int32, torch.int64) or not position_ids.is_contiguous()
+                or position_ids.numel() != batch * q_len or position_ids.device != q.device):
+            raise ValueError("attention with rope on q: position_ids must be a contiguous int32 "
+                             f"or int64 tensor of batch * q_len = {batch * q_len} positions")
+    return batch, n_heads, n_kv_heads, q_len, kv_len, head_dim
+
+
+def _pos_args(position_ids):
+    if position_ids is None:
+        return None, 0
+    return position_ids.data_ptr(), (1 if position_ids.dtype == torch.int32 else 2)
+
+
+def attention_rope_fwd(q, k, v, cos, sin, position_ids, is_causal: bool, o=None):
+    """Forward of attention(rope(q), k, v): q unrotated, k rotated; returns
+    (o, lse).  ``o`` may be given (any layout with 16-byte aligned rows)."""
+    batch, n_heads, n_kv_heads, q_len, kv_len, head_dim = _check_rope_q(q, k, v, cos, sin,
+                                                                         position_ids)
+    if o is None:
+        o = torch.empty((batch, q_len, n_heads, head_dim), device=q.device,
+                        dtype=q.dtype).transpose(1, 2)
+    lse = torch.empty((batch, n_heads, q_len), device=q.device, dtype=torch.float32)
+    if q_len == 0 or batch == 0:
+        return o, lse
+    pos_ptr, kind = _pos_args(position_ids)
+    _lib.call("tritium_attention_fwd_rope", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
+              lse.data_ptr(), batch, n_heads, n_kv_heads, q_len, kv_len, head_dim,
+              _strides(q, k, v, o), int(bool(is_causal)), _lib.dtype_code(q.dtype),
+              cos.data_ptr(), sin.data_ptr(), pos_ptr, kind, cos.shape[0], _lib.stream_of(q))
+    return o, lse
+
+
+def attention_rope_bwd(do, q, k, v, o, lse, cos, sin, position_ids, is_causal: bool,
+                       dq=None, dk=None, dv=None):
+    """Backward of ``attention_rope_fwd``: dq is the gradient of the unrotated
+    q.  dq/dk/dv may be given as strided views (16-byte aligned rows)."""
+    batch, n_heads, n_kv_heads, q_len, kv_len, head_dim = _check_rope_q(q, k, v, cos, sin,
+                                                                         position_ids)
+    dq = torch.empty_like(q) if dq is None else dq
+    dk = torch.empty_like(k) if dk is None else dk
+    dv = torch.empty_like(v) if dv is None else dv
+    if q_len == 0 or batch == 0 or kv_len == 0:
+        for t in (dq, dk, dv):
+            t.zero_()
+        return dq, dk, dv
+    if not _rows_aligned(do):
+        do = do.contiguous()
+    delta = torch.empty((batch * n_heads * q_len,), device=q.device, dtype=torch.float32)
+    q_rot = torch.empty((batch, n_heads, q_len, head_dim), device=q.device, dtype=q.dtype)
+    pos_ptr, kind = _pos_args(position_ids)
+    _lib.call("tritium_attention_bwd_rope", do.data_ptr(), q.data_ptr(), k.data_ptr(),
+              v.data_ptr(), o.data_ptr(), lse.data_ptr(), dq.data_ptr(), dk.data_ptr(),
+              dv.data_ptr(), delta.data_ptr(), q_rot.data_ptr(), batch, n_heads, n_kv_heads,
+              q_len, kv_len, head_dim, _strides(q, k, v, o, do, dq, dk, dv),
+              int(bool(is_causal)), _lib.dtype_code(q.dtype), cos.data_ptr(), sin.data_ptr(),
+              pos_ptr, kind, cos.shape[0], _lib.stream_of(q))
+    return dq, dk, dv
+
+
+class _AttentionRopeQ(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx: Any, q, k, v, cos, sin, position_ids, is_causal: bool):
+        o, lse = attention_rope_fwd(q, k, v, cos, sin, position_ids, is_causal)
+        ctx.save_for_backward(q, k, v, o, lse, cos, sin, position_ids)
+        ctx.is_causal = is_causal
+        return o
+
+    @staticmethod
+    def backward(ctx: Any, *grad_outputs: torch.Tensor):
+        q, k, v, o, lse, cos, sin, position_ids = ctx.saved_tensors
+        dq, dk, dv = attention_rope_bwd(grad_outputs[0], q, k, v, o, lse, cos, sin, position_ids,
+                                        ctx.is_causal)
+        return dq, dk, dv, None, None, None, None
+
+
+def attention_rope_q(q, k, v, cos, sin, position_ids=None, *, is_causal: bool = True):
+    """``attention(rope(q), k, v, is_causal=...)`` with q rotated as the kernels
+    load it: q unrotated (batch, n_heads, q_len, head_dim), k already
+    rotated, cos/sin float32 [max_position, head_dim / 2] (non-interleaved
+    halves, as ``rope``), position_ids one per (batch, query row) in
+    batch-major order or None (position = query row).  The gradient of q is
+    that of the unrotated q.  bf16/fp16 with head_dim 64 or 128."""
+    if not requires_autograd(q, k, v):
+        return attention_rope_fwd(q, k, v, cos, sin, position_ids, is_causal)[0]
+    return _AttentionRopeQ.apply(q, k, v, cos, sin, position_ids, is_causal)

@@ -113,11 +113,22 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
   return (bid % kXcds) * (n / kXcds) + bid / kXcds;
 }
 
+// RoPE applied to q as it is loaded (cos == nullptr: q is used as given).
+// Non-interleaved halves: element i pairs with i + D/2 at table column i of
+// the row's position; tables [max_pos, D/2] float32; the position of query
+// row t of batch b is pos[b * Tq + t] (kind 1 int32, 2 int64) or t (kind 0).
+struct RopeQ {
+  const float* cos; const float* sin; const void* pos;
+  int kind;
+  int64_t max_pos;
+};
+
 struct FwdArgs {
   const void* q; const void* k; const void* v; void* o; float* lse;
   int64_t sq_b, sq_h, sq_s, sk_b, sk_h, sk_s, sv_b, sv_h, sv_s, so_b, so_h, so_s;
   int B, H, Hkv, Tq, Tkv, n_tiles, causal;
   float scale;  // head_dim ** -0.5
+  RopeQ rope;
 };
 
 struct BwdArgs {
@@ -127,7 +138,47 @@ struct BwdArgs {
   int64_t sdo_b, sdo_h, sdo_s, sdq_b, sdq_h, sdq_s, sdk_b, sdk_h, sdk_s, sdv_b, sdv_h, sdv_s;
   int B, H, Hkv, Tq, Tkv, n_tiles, causal;
   float scale;
+  RopeQ rope;
+  void* q_rot;  // with rope: [B, H, Tq, D] rotated q, written by the dQ kernel for dK/dV
 };
+
+// Position of query row t of batch b under r, and whether the tables hold it.
+__device__ __forceinline__ bool rope_position(const RopeQ& r, int b, int Tq, int t, int64_t& pos) {
+  const int64_t token = (int64_t)b * Tq + t;
+  pos = r.kind == 1 ? (int64_t)((const int32_t*)r.pos)[token]
+                    : r.kind == 2 ? ((const int64_t*)r.pos)[token] : (int64_t)t;
+  return pos >= 0 && pos < r.max_pos;
+}
+
+// Rotate a lane's q fragment in place: qf[st] holds elements 16 st + 8 g ..
+// + 7 of one row, so the pairs (i, i + D/2) are qf[st][j], qf[st + KS/2][j].
+// Rounded to T as the RoPE kernel rounds its output; NaN outside the tables.
+template <typename T, int D>
+__device__ __forceinline__ void rope_q_frag(typename Mfma<T>::V (&qf)[D / 16], const RopeQ& r,
+                                            int64_t pos, bool valid, int g) {
+  constexpr int H2 = D / 32, HALF = D / 2;
+  const float nan = __builtin_nanf("");
+#pragma unroll
+  for (int st = 0; st < H2; ++st) {
+    float c[8] = {}, s[8] = {};
+    if (valid) {
+      const float* cr = r.cos + pos * HALF + 16 * st + 8 * g;
+      const float* sr = r.sin + pos * HALF + 16 * st + 8 * g;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        c[j] = cr[j];
+        s[j] = sr[j];
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float oa, ob;
+      rope_pair((float)qf[st][j], (float)qf[st + H2][j], c[j], s[j], oa, ob);
+      qf[st][j] = (T)(valid ? oa : nan);
+      qf[st + H2][j] = (T)(valid ? ob : nan);
+    }
+  }
+}
 
 // Transposed LDS tiles are [d][64] with no padding: the 8-byte unit u (4
 // elements) of row d sits at slot u ^ tr_key(d).  A 32-lane 8-byte read of
@@ -673,6 +724,11 @@ attn_fwd_v2(FwdArgs a) {
 #pragma unroll
   for (int s = 0; s < KS; ++s)
     qf[s] = qvalid ? ld8(qp + (int64_t)qrow * a.sq_s + 16 * s + 8 * g) : zero8<T>();
+  if (a.rope.cos != nullptr && qvalid) {
+    int64_t pos;
+    const bool ok = rope_position(a.rope, b, a.Tq, qrow, pos);
+    rope_q_frag<T, D>(qf, a.rope, pos, ok, g);
+  }
 
   f32x16 o[MT];
 #pragma unroll
@@ -920,6 +976,11 @@ attn_fwd_pp(FwdArgs a) {
 #pragma unroll
     for (int st = 0; st < KS; ++st)
       qf[st] = qvalid ? ld8(qp + (int64_t)qrow * a.sq_s + 16 * st + 8 * g) : zero8<T>();
+    if (a.rope.cos != nullptr && qvalid) {
+      int64_t pos;
+      const bool ok = rope_position(a.rope, b, a.Tq, qrow, pos);
+      rope_q_frag<T, D>(qf, a.rope, pos, ok, g);
+    }
     f32x16 o[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) o[mt] = zero16();
@@ -1864,6 +1925,17 @@ attn_bwd_dq_v2(BwdArgs a) {
     qf[s] = qvalid ? ld8(qp + (int64_t)qrow * a.sq_s + 16 * s + 8 * g) : zero8<T>();
     df[s] = qvalid ? ld8(dop + (int64_t)qrow * a.sdo_s + 16 * s + 8 * g) : zero8<T>();
   }
+  // with RoPE: rotate q on load, and hand the rotated rows to the dK/dV kernel
+  const bool rope = a.rope.cos != nullptr;
+  int64_t rpos = 0;
+  bool rpos_ok = false;
+  if (rope && qvalid) {
+    rpos_ok = rope_position(a.rope, b, a.Tq, qrow, rpos);
+    rope_q_frag<T, D>(qf, a.rope, rpos, rpos_ok, g);
+    T* qr = (T*)a.q_rot + ((int64_t)bh * a.Tq + qrow) * D;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) *reinterpret_cast<V*>(qr + 16 * s + 8 * g) = qf[s];
+  }
   const float lse2 = qvalid ? a.lse[(int64_t)bh * a.Tq + qrow] * kLog2e : INFINITY;
   // delta = rowsum(dO * O) for this lane's query row (the two lanes of a row
   // hold alternate 8-column halves); written out for the dK/dV kernel
@@ -1939,12 +2011,43 @@ attn_bwd_dq_v2(BwdArgs a) {
     T* dqr = (T*)a.dq + b * a.sdq_b + h * a.sdq_h + (int64_t)qrow * a.sdq_s;
     const float sc = a.scale;
 #pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) dq[mt][r] *= sc;
+    if (rope) {
+      // the gradient of the unrotated q: the inverse rotation of dq, element
+      // d = 32 mt + 8 rr + 4 g + j pairing with d + D/2 in dq[mt + MT/2]
+      const float nan = __builtin_nanf("");
+#pragma unroll
+      for (int mt = 0; mt < MT / 2; ++mt) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int d0 = 32 * mt + 8 * rr + 4 * g;
+          float c[4] = {}, s[4] = {};
+          if (rpos_ok) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+              c[j] = a.rope.cos[rpos * (D / 2) + d0 + j];
+              s[j] = a.rope.sin[rpos * (D / 2) + d0 + j];
+            }
+          }
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            float oa, ob;
+            rope_pair(dq[mt][4 * rr + j], dq[mt + MT / 2][4 * rr + j], c[j], -s[j], oa, ob);
+            dq[mt][4 * rr + j] = rpos_ok ? oa : nan;
+            dq[mt + MT / 2][4 * rr + j] = rpos_ok ? ob : nan;
+          }
+        }
+      }
+    }
+#pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int d0 = 32 * mt + 8 * rr + 4 * g;
-        store4<T>(dqr + d0, dq[mt][4 * rr] * sc, dq[mt][4 * rr + 1] * sc,
-                  dq[mt][4 * rr + 2] * sc, dq[mt][4 * rr + 3] * sc);
+        store4<T>(dqr + d0, dq[mt][4 * rr], dq[mt][4 * rr + 1], dq[mt][4 * rr + 2],
+                  dq[mt][4 * rr + 3]);
       }
     }
   }
@@ -2429,6 +2532,12 @@ int bwd_v2(const BwdArgs& a, hipStream_t st) {
   const int64_t q_blocks = (int64_t)x.n_tiles * a.B * a.H;
   attn_bwd_dq_v2<T, D, WQ><<<(unsigned)q_blocks, 64 * WQ, 0, st>>>(x);
   if (int e = check_launch("attention backward (dq, mfma)")) return e;
+  if (a.rope.cos != nullptr) {  // dK/dV take the rotated q the dQ kernel wrote
+    x.q = a.q_rot;
+    x.sq_s = D;
+    x.sq_h = (int64_t)a.Tq * D;
+    x.sq_b = (int64_t)a.H * a.Tq * D;
+  }
   // head_dim 128: wavefront pairs; head_dim 64 has half the MFMAs per tile
   // for the same VALU work, and one wavefront doing both roles with its
   // K and V fragments (attn_bwd_dkdv_v2) measured faster there (0.27 vs
@@ -2510,10 +2619,13 @@ int check_dims(int64_t B, int64_t H, int64_t Hkv, int64_t Tq, int64_t Tkv, int64
 
 using namespace tri;
 
-extern "C" int tritium_attention_fwd(const void* q, const void* k, const void* v, void* o,
-                                     float* lse, int64_t B, int64_t H, int64_t Hkv, int64_t Tq,
-                                     int64_t Tkv, int64_t D, const int64_t* strides, int causal,
-                                     int dtype, void* stream) {
+namespace {
+
+// tritium_attention_fwd / _fwd_rope: rope.cos == nullptr leaves q as given
+int attention_fwd(const void* q, const void* k, const void* v, void* o, float* lse, int64_t B,
+                  int64_t H, int64_t Hkv, int64_t Tq, int64_t Tkv, int64_t D,
+                  const int64_t* strides, int causal, int dtype, const RopeQ& rope,
+                  void* stream) {
   if (int e = check_dims(B, H, Hkv, Tq, Tkv, D)) return e;
   if (B == 0 || Tq == 0) return TRI_OK;
   FwdArgs a;
@@ -2526,12 +2638,16 @@ extern "C" int tritium_attention_fwd(const void* q, const void* k, const void* v
   a.causal = causal != 0;
   a.n_tiles = 0;
   a.scale = (float)(1.0 / sqrt((double)D));
+  a.rope = rope;
   hipStream_t st = (hipStream_t)stream;
   const bool mfma = dtype != kF32 && mfma_head_dim(D) &&
                     rows_aligned(q, a.sq_b, a.sq_h, a.sq_s) &&
                     rows_aligned(k, a.sk_b, a.sk_h, a.sk_s) &&
                     rows_aligned(v, a.sv_b, a.sv_h, a.sv_s) && aligned16(o) &&
                     a.so_s % 4 == 0 && a.so_b % 4 == 0 && a.so_h % 4 == 0;
+  if (rope.cos != nullptr && !(mfma && (D == 64 || D == 128)))
+    return fail(TRI_EINVAL, "attention with rope: needs 16-bit q/k/v with head_dim 64 or 128 and "
+                "16-byte aligned rows (dtype %d, head_dim %lld)", dtype, (long long)D);
   if (mfma) {
     if (dtype == kBF16) return fwd_mfma<bf16_t>(a, D, st);
     return fwd_mfma<f16_t>(a, D, st);
@@ -2540,12 +2656,11 @@ extern "C" int tritium_attention_fwd(const void* q, const void* k, const void* v
   return TRI_OK;
 }
 
-extern "C" int tritium_attention_bwd(const void* dout, const void* q, const void* k,
-                                     const void* v, const void* o, const float* lse, void* dq,
-                                     void* dk, void* dv, float* delta, int64_t B, int64_t H,
-                                     int64_t Hkv, int64_t Tq, int64_t Tkv, int64_t D,
-                                     const int64_t* strides, int causal, int dtype,
-                                     void* stream) {
+int attention_bwd(const void* dout, const void* q, const void* k, const void* v, const void* o,
+                  const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t B,
+                  int64_t H, int64_t Hkv, int64_t Tq, int64_t Tkv, int64_t D,
+                  const int64_t* strides, int causal, int dtype, const RopeQ& rope, void* q_rot,
+                  void* stream) {
   if (int e = check_dims(B, H, Hkv, Tq, Tkv, D)) return e;
   if (B == 0 || Tq == 0 || Tkv == 0) return TRI_OK;
   BwdArgs a;
@@ -2563,6 +2678,8 @@ extern "C" int tritium_attention_bwd(const void* dout, const void* q, const void
   a.causal = causal != 0;
   a.n_tiles = 0;
   a.scale = (float)(1.0 / sqrt((double)D));
+  a.rope = rope;
+  a.q_rot = q_rot;
   const bool out_ok = [&] {
     const int64_t* s = strides + 15;
     for (int i = 0; i < 9; ++i)
@@ -2576,8 +2693,78 @@ extern "C" int tritium_attention_bwd(const void* dout, const void* q, const void
                     rows_aligned(dout, a.sdo_b, a.sdo_h, a.sdo_s) &&
                     rows_aligned(o, a.so_b, a.so_h, a.so_s) && out_ok;
   hipStream_t st = (hipStream_t)stream;
+  if (rope.cos != nullptr) {
+    if (!(mfma && (D == 64 || D == 128)))
+      return fail(TRI_EINVAL, "attention backward with rope: needs 16-bit tensors with head_dim "
+                  "64 or 128 and 16-byte aligned rows (dtype %d, head_dim %lld)", dtype,
+                  (long long)D);
+    if (q_rot == nullptr || !aligned16(q_rot))
+      return fail(TRI_EINVAL, "attention backward with rope: q_rot workspace missing or unaligned");
+  }
   TRI_DISPATCH_FLOAT(dtype, T, return bwd_impl<T>(a, D, mfma, st));
   return TRI_OK;
+}
+
+int rope_tables(const float* cos_table, const float* sin_table, const void* position_ids,
+                int position_kind, int64_t max_position, RopeQ& r) {
+  if (cos_table == nullptr || sin_table == nullptr || max_position < 0 || position_kind < 0 ||
+      position_kind > 2 || (position_kind != 0 && position_ids == nullptr))
+    return fail(TRI_EINVAL, "attention rope: bad tables or position_ids (kind %d)", position_kind);
+  r.cos = cos_table;
+  r.sin = sin_table;
+  r.pos = position_ids;
+  r.kind = position_kind;
+  r.max_pos = max_position;
+  return TRI_OK;
+}
+
+}  // namespace
+
+extern "C" int tritium_attention_fwd(const void* q, const void* k, const void* v, void* o,
+                                     float* lse, int64_t B, int64_t H, int64_t Hkv, int64_t Tq,
+                                     int64_t Tkv, int64_t D, const int64_t* strides, int causal,
+                                     int dtype, void* stream) {
+  return attention_fwd(q, k, v, o, lse, B, H, Hkv, Tq, Tkv, D, strides, causal, dtype, RopeQ{},
+                       stream);
+}
+
+extern "C" int tritium_attention_bwd(const void* dout, const void* q, const void* k,
+                                     const void* v, const void* o, const float* lse, void* dq,
+                                     void* dk, void* dv, float* delta, int64_t B, int64_t H,
+                                     int64_t Hkv, int64_t Tq, int64_t Tkv, int64_t D,
+                                     const int64_t* strides, int causal, int dtype,
+                                     void* stream) {
+  return attention_bwd(dout, q, k, v, o, lse, dq, dk, dv, delta, B, H, Hkv, Tq, Tkv, D, strides,
+                       causal, dtype, RopeQ{}, nullptr, stream);
+}
+
+extern "C" int tritium_attention_fwd_rope(const void* q, const void* k, const void* v, void* o,
+                                          float* lse, int64_t B, int64_t H, int64_t Hkv,
+                                          int64_t Tq, int64_t Tkv, int64_t D,
+                                          const int64_t* strides, int causal, int dtype,
+                                          const float* cos_table, const float* sin_table,
+                                          const void* position_ids, int position_kind,
+                                          int64_t max_position, void* stream) {
+  RopeQ r{};
+  if (int e = rope_tables(cos_table, sin_table, position_ids, position_kind, max_position, r))
+    return e;
+  return attention_fwd(q, k, v, o, lse, B, H, Hkv, Tq, Tkv, D, strides, causal, dtype, r, stream);
+}
+
+extern "C" int tritium_attention_bwd_rope(const void* dout, const void* q, const void* k,
+                                          const void* v, const void* o, const float* lse,
+                                          void* dq, void* dk, void* dv, float* delta,
+                                          void* q_rot, int64_t B, int64_t H, int64_t Hkv,
+                                          int64_t Tq, int64_t Tkv, int64_t D,
+                                          const int64_t* strides, int causal, int dtype,
+                                          const float* cos_table, const float* sin_table,
+                                          const void* position_ids, int position_kind,
+                                          int64_t max_position, void* stream) {
+  RopeQ r{};
+  if (int e = rope_tables(cos_table, sin_table, position_ids, position_kind, max_position, r))
+    return e;
+  return attention_bwd(dout, q, k, v, o, lse, dq, dk, dv, delta, B, H, Hkv, Tq, Tkv, D, strides,
+                       causal, dtype, r, q_rot, stream);
 }
 
 extern "C" size_t tritium_attention_decode_workspace_size(int64_t B, int64_t H, int64_t Hkv,

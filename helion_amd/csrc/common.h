@@ -133,6 +133,20 @@ __device__ __forceinline__ float wave_max(float v) {
 // weights that small are negligible, and exp2(-inf) = 0 either way.
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// One RoPE pair (a, b) at angle (c = cos, s = sin): (a c - b s, b c + a s);
+// the inverse rotation passes -s.  Shared by the RoPE kernels and the
+// attention kernels that rotate q on load, so that both round alike: the
+// fused multiply-adds are spelled out, since the compiler's own contraction
+// of a * c - b * s may pick either product depending on the surrounding code,
+// and the fp32 results are materialised, since a 16-bit conversion that
+// follows could otherwise be folded into a mixed-precision fma that rounds
+// once (v_fma_mix*) where the other kernel rounds to fp32 first.
+__device__ __forceinline__ void rope_pair(float a, float b, float c, float s, float& oa, float& ob) {
+  oa = fmaf(a, c, -(b * s));
+  ob = fmaf(b, c, a * s);
+  asm volatile("" : "+v"(oa), "+v"(ob));
+}
+
 __host__ __device__ constexpr inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // ---- global -> LDS DMA -----------------------------------------------------

@@ -67,43 +67,49 @@ rope_kernel(const T* q, const T* k, const CT* __restrict__ cos_t,
   }
   const float nan = __builtin_nanf("");
 
+  // q == nullptr: k only (a caller that rotates q elsewhere); qa, qb stay 0
+  const bool has_q = q != nullptr;
   if (!interleaved) {
-    float qa[P], qb[P], ka[P], kb[P];
-    load_stream<T, P>(q + base + p0, qa);
-    load_stream<T, P>(q + base + half + p0, qb);
+    float qa[P] = {}, qb[P] = {}, ka[P], kb[P];
+    if (has_q) {
+      load_stream<T, P>(q + base + p0, qa);
+      load_stream<T, P>(q + base + half + p0, qb);
+    }
     load_stream<T, P>(k + base + p0, ka);
     load_stream<T, P>(k + base + half + p0, kb);
     float oqa[P], oqb[P], oka[P], okb[P];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-      oqa[i] = valid ? qa[i] * c[i] - qb[i] * s[i] : nan;
-      oqb[i] = valid ? qb[i] * c[i] + qa[i] * s[i] : nan;
-      oka[i] = valid ? ka[i] * c[i] - kb[i] * s[i] : nan;
-      okb[i] = valid ? kb[i] * c[i] + ka[i] * s[i] : nan;
+      rope_pair(qa[i], qb[i], c[i], s[i], oqa[i], oqb[i]);
+      rope_pair(ka[i], kb[i], c[i], s[i], oka[i], okb[i]);
+      if (!valid) oqa[i] = oqb[i] = oka[i] = okb[i] = nan;
     }
-    store_stream<T, P>(q_out + obase + p0, oqa);
-    store_stream<T, P>(q_out + obase + half + p0, oqb);
+    if (has_q) {
+      store_stream<T, P>(q_out + obase + p0, oqa);
+      store_stream<T, P>(q_out + obase + half + p0, oqb);
+    }
     store_stream<T, P>(k_out + obase + p0, oka);
     store_stream<T, P>(k_out + obase + half + p0, okb);
   } else {
     // elements [2*p0, 2*p0 + 2P) hold P adjacent (a, b) pairs
-    float qv[2 * P], kv[2 * P];
-    load_stream<T, P>(q + base + 2 * p0, *reinterpret_cast<float(*)[P]>(qv));
-    load_stream<T, P>(q + base + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(qv + P));
+    float qv[2 * P] = {}, kv[2 * P];
+    if (has_q) {
+      load_stream<T, P>(q + base + 2 * p0, *reinterpret_cast<float(*)[P]>(qv));
+      load_stream<T, P>(q + base + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(qv + P));
+    }
     load_stream<T, P>(k + base + 2 * p0, *reinterpret_cast<float(*)[P]>(kv));
     load_stream<T, P>(k + base + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(kv + P));
     float oq[2 * P], ok[2 * P];
 #pragma unroll
     for (int i = 0; i < P; ++i) {
-      const float a = qv[2 * i], b = qv[2 * i + 1];
-      oq[2 * i] = valid ? a * c[i] - b * s[i] : nan;
-      oq[2 * i + 1] = valid ? b * c[i] + a * s[i] : nan;
-      const float ka = kv[2 * i], kb = kv[2 * i + 1];
-      ok[2 * i] = valid ? ka * c[i] - kb * s[i] : nan;
-      ok[2 * i + 1] = valid ? kb * c[i] + ka * s[i] : nan;
+      rope_pair(qv[2 * i], qv[2 * i + 1], c[i], s[i], oq[2 * i], oq[2 * i + 1]);
+      rope_pair(kv[2 * i], kv[2 * i + 1], c[i], s[i], ok[2 * i], ok[2 * i + 1]);
+      if (!valid) oq[2 * i] = oq[2 * i + 1] = ok[2 * i] = ok[2 * i + 1] = nan;
     }
-    store_stream<T, P>(q_out + obase + 2 * p0, *reinterpret_cast<float(*)[P]>(oq));
-    store_stream<T, P>(q_out + obase + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(oq + P));
+    if (has_q) {
+      store_stream<T, P>(q_out + obase + 2 * p0, *reinterpret_cast<float(*)[P]>(oq));
+      store_stream<T, P>(q_out + obase + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(oq + P));
+    }
     store_stream<T, P>(k_out + obase + 2 * p0, *reinterpret_cast<float(*)[P]>(ok));
     store_stream<T, P>(k_out + obase + 2 * p0 + P, *reinterpret_cast<float(*)[P]>(ok + P));
   }
@@ -169,6 +175,8 @@ extern "C" int tritium_rope_strided(const void* q, const void* k, const void* co
                 (long long)(n_heads * head_dim));
   if (position_kind < 0 || position_kind > 2 || (position_kind != 0 && position_ids == nullptr))
     return fail(TRI_EINVAL, "rope: bad position_ids kind %d", position_kind);
+  if ((q == nullptr) != (q_out == nullptr) || k == nullptr || k_out == nullptr)
+    return fail(TRI_EINVAL, "rope: k and k_out are required; q and q_out are both given or both null");
   if (n_tokens == 0) return TRI_OK;
   hipStream_t s = (hipStream_t)stream;
   TRI_DISPATCH_FLOAT(dtype, T,

@@ -21,9 +21,11 @@ as the reference's residual-RMSNorm does (rmsnorm.py:72-83).
 Plain projections (q/k/v fused into one, o, gate/up fused into one, down)
 are library GEMMs (hipBLASLt; weight gradients split over token slices by
 one batched GEMM, ``_Proj``); everything on the kernel
-layer's hot path is a HIP kernel: residual-RMSNorm, RoPE (applied in place
-to the fused q/k/v output), causal attention, SwiGLU (on the fused gate/up
-output), fused linear-cross-entropy and AdamW.
+layer's hot path is a HIP kernel: residual-RMSNorm, RoPE (k rotated once out
+of the fused q/k/v output; q rotated by the attention kernels as they load it,
+``_QKVRopeAttention``), causal attention, SwiGLU (on the fused gate/up
+output), fused linear-cross-entropy, the tied embedding's backward and
+AdamW.
 
 ``TorchTwin`` computes the same step with PyTorch only (F.rms_norm,
 F.scaled_dot_product_attention, F.silu, F.cross_entropy on materialised
@@ -46,7 +48,7 @@ import torch.nn.functional as F
 
 from . import _lib
 from .adamw import adamw_step_mixed
-from .attention import attention
+from .attention import attention_rope_bwd, attention_rope_fwd
 from .embedding import embedding_backward
 from .linear_ce import _backward as _lce_backward
 from .linear_ce import _linear_cross_entropy_forward
@@ -219,10 +221,7 @@ class HipGPT:
             p = f"blocks.{i}."
             normed, residual = residual_rmsnorm(delta, residual, self._w(p + "attn_norm"), cfg.eps)
             qkv = _Proj.apply(normed.view(t, d), self._w(p + "wqkv")).view(b, s, 3, nh, hd)
-            q, k, vv = _QKVRope.apply(qkv, cos, sin, pos)
-            o = attention(q.view(b, s, nh, hd).transpose(1, 2), k.view(b, s, nh, hd).transpose(1, 2),
-                          vv.transpose(1, 2), is_causal=True)
-            o = o.transpose(1, 2).reshape(t, nh * hd)
+            o = _QKVRopeAttention.apply(qkv, cos, sin, pos).reshape(t, nh * hd)
             delta = _Proj.apply(o, self._w(p + "wo")).view(b, s, d)
             normed, residual = residual_rmsnorm(delta, residual, self._w(p + "ffn_norm"), cfg.eps)
             h = _GateUpSwiGLU.apply(_Proj.apply(normed.view(t, d), self._w(p + "w_gu")))
@@ -368,35 +367,42 @@ class _TiedEmbed(torch.autograd.Function):
         return dw, None, None
 
 
-class _QKVRope(torch.autograd.Function):
-    """Split of the fused q/k/v projection ``[b, s, 3, heads, head_dim]`` with
-    RoPE on q and k: one kernel reads q and k in place and writes the rotated
-    rows contiguously (what ``rope`` computes on contiguous copies); v is
-    returned as a view.  The backward writes the inverse rotation of dq, dk
-    and a copy of dv straight into one fused gradient, instead of a stack of
-    three gradients after two contiguous copies and a separate rope pass."""
+class _QKVRopeAttention(torch.autograd.Function):
+    """Causal attention over the fused q/k/v projection ``[b, s, 3, heads,
+    head_dim]`` with RoPE on q and k (helion/nn.py:196-220): k is rotated once
+    into a contiguous copy; q and v are read in place, q unrotated and rotated
+    as the attention kernels load it (``attention_rope_fwd``), so no rotated q
+    is written or kept.  The output is ``[b, s, heads, head_dim]`` memory (a
+    free view of the o projection's input).  The backward writes dq (the dQ
+    kernel un-rotates it) and dv straight into one fused gradient and
+    un-rotates dk into it."""
 
     @staticmethod
     def forward(ctx, qkv, cos, sin, pos):
         b, s, _, nh, hd = qkv.shape
         flat = qkv.view(b * s, 3, nh, hd)
-        q = torch.empty((b * s, nh, hd), device=qkv.device, dtype=qkv.dtype)
-        k = torch.empty_like(q)
-        rope_rows(flat[:, 0], flat[:, 1], cos, sin, pos, q, k, inverse=False,
+        k = torch.empty((b * s, nh, hd), device=qkv.device, dtype=qkv.dtype)
+        rope_rows(None, flat[:, 1], cos, sin, pos, None, k, inverse=False,
                   in_token_stride=3 * nh * hd, out_token_stride=nh * hd)
-        ctx.save_for_backward(cos, sin, pos)
-        ctx.shape = qkv.shape
-        return q, k, qkv[:, :, 2]
+        q, v = qkv[:, :, 0].transpose(1, 2), qkv[:, :, 2].transpose(1, 2)
+        o, lse = attention_rope_fwd(q, k.view(b, s, nh, hd).transpose(1, 2), v, cos, sin, pos,
+                                    True)
+        ctx.save_for_backward(qkv, k, o, lse, cos, sin, pos)
+        return o.transpose(1, 2)
 
     @staticmethod
-    def backward(ctx, dq, dk, dv):
-        cos, sin, pos = ctx.saved_tensors
-        b, s, _, nh, hd = ctx.shape
-        dqkv = torch.empty(ctx.shape, device=dq.device, dtype=dq.dtype)
-        flat = dqkv.view(b * s, 3, nh, hd)
-        rope_rows(dq.contiguous(), dk.contiguous(), cos, sin, pos, flat[:, 0], flat[:, 1],
-                  inverse=True, in_token_stride=nh * hd, out_token_stride=3 * nh * hd)
-        dqkv[:, :, 2].copy_(dv)
+    def backward(ctx, do):
+        qkv, k, o, lse, cos, sin, pos = ctx.saved_tensors
+        b, s, _, nh, hd = qkv.shape
+        dqkv = torch.empty_like(qkv)
+        dk = torch.empty((b, s, nh, hd), device=qkv.device, dtype=qkv.dtype)
+        attention_rope_bwd(do.transpose(1, 2), qkv[:, :, 0].transpose(1, 2),
+                           k.view(b, s, nh, hd).transpose(1, 2), qkv[:, :, 2].transpose(1, 2),
+                           o, lse, cos, sin, pos, True, dq=dqkv[:, :, 0].transpose(1, 2),
+                           dk=dk.transpose(1, 2), dv=dqkv[:, :, 2].transpose(1, 2))
+        rope_rows(None, dk.view(b * s, nh, hd), cos, sin, pos, None,
+                  dqkv.view(b * s, 3, nh, hd)[:, 1], inverse=True, in_token_stride=nh * hd,
+                  out_token_stride=3 * nh * hd)
         return dqkv, None, None, None
 
 

@@ -152,14 +152,18 @@ def rope_rows(q, k, cos, sin, position_ids, q_out, k_out, *, inverse: bool,
     Not part of the reference's surface (its rope takes contiguous tensors
     only, rope.py:192-195): the training harness's fused split uses it.  q,
     k, q_out, k_out are [tokens, heads, head_dim]-shaped views with those
-    strides and a unit head_dim stride; positions as in ``rope``."""
-    n_tokens, n_heads, head_dim = q.shape
-    for t in (k, q_out, k_out):
-        if t.shape != q.shape or t.dtype != q.dtype or t.device != q.device:
+    strides and a unit head_dim stride; positions as in ``rope``.  q and
+    q_out may both be None: k alone is rotated (for attention_rope_q, which
+    rotates q as it loads it)."""
+    if (q is None) != (q_out is None):
+        raise ValueError("rope_rows: q and q_out are both given or both None (k alone)")
+    n_tokens, n_heads, head_dim = k.shape
+    for t in (q, q_out, k_out):
+        if t is not None and (t.shape != k.shape or t.dtype != k.dtype or t.device != k.device):
             raise ValueError("rope_rows: q, k, q_out, k_out must share shape, dtype and device")
     for t, ts in ((q, in_token_stride), (k, in_token_stride), (q_out, out_token_stride),
                   (k_out, out_token_stride)):
-        if t.stride() != (ts, head_dim, 1):
+        if t is not None and t.stride() != (ts, head_dim, 1):
             raise ValueError(f"rope_rows: expected strides {(ts, head_dim, 1)}, got {t.stride()}")
     if n_tokens == 0:
         return
@@ -167,11 +171,11 @@ def rope_rows(q, k, cos, sin, position_ids, q_out, k_out, *, inverse: bool,
         sin = sin.to(cos.dtype)
     kind = 0 if position_ids is None else (1 if position_ids.dtype == torch.int32 else 2)
     _lib.call(
-        "tritium_rope_strided", q.data_ptr(), k.data_ptr(), cos.data_ptr(), sin.data_ptr(),
-        _lib.ptr(position_ids), kind, q_out.data_ptr(), k_out.data_ptr(), n_tokens, n_heads,
+        "tritium_rope_strided", _lib.ptr(q), k.data_ptr(), cos.data_ptr(), sin.data_ptr(),
+        _lib.ptr(position_ids), kind, _lib.ptr(q_out), k_out.data_ptr(), n_tokens, n_heads,
         head_dim, cos.shape[0], 0, 0, int(bool(inverse)), int(in_token_stride),
-        int(out_token_stride), _lib.dtype_code(q.dtype), _lib.dtype_code(cos.dtype),
-        _lib.stream_of(q),
+        int(out_token_stride), _lib.dtype_code(k.dtype), _lib.dtype_code(cos.dtype),
+        _lib.stream_of(k),
     )
 
 

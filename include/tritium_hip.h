@@ -82,7 +82,8 @@ int tritium_rope(const void* q, const void* k, const void* cos_table, const void
  * it lets a caller rotate q and k in place inside a fused
  * [tokens, 3, heads, head_dim] q/k/v projection (token stride
  * 3 * heads * head_dim), and write the backward's inverse rotation straight
- * into the fused gradient. */
+ * into the fused gradient.  q and q_out may both be null: k alone is rotated
+ * (for a caller whose attention rotates q on load). */
 int tritium_rope_strided(const void* q, const void* k, const void* cos_table,
                          const void* sin_table, const void* position_ids, int position_kind,
                          void* q_out, void* k_out, int64_t n_tokens, int64_t n_heads,
@@ -177,6 +178,37 @@ int tritium_attention_bwd(const void* dout, const void* q, const void* k, const 
                           float* delta, int64_t B, int64_t H, int64_t Hkv, int64_t Tq,
                           int64_t Tkv, int64_t D, const int64_t* strides, int causal, int dtype,
                           void* stream);
+
+/* tritium_attention_fwd with RoPE applied to q as each row is loaded: q holds
+ * the unrotated rows, k the rotated ones (tritium_rope_strided with a null q
+ * rotates k alone).  No counterpart in the reference, which rotates q and k
+ * into new tensors right before attention (helion/nn.py:196-220): this is
+ * that sequence for q without the rotated copy in memory.  The rotation is
+ * tritium_rope's (non-interleaved halves, rounded to `dtype`): cos_table /
+ * sin_table [max_position, D/2] float32; the position of query row t of
+ * batch b is position_ids[b * Tq + t] (position_kind 1: int32, 2: int64) or
+ * t (position_kind 0); positions outside [0, max_position) give NaN rows.
+ * 16-bit tensors with D in {64, 128} and 16-byte aligned rows only
+ * (TRI_EINVAL otherwise). */
+int tritium_attention_fwd_rope(const void* q, const void* k, const void* v, void* o, float* lse,
+                               int64_t B, int64_t H, int64_t Hkv, int64_t Tq, int64_t Tkv,
+                               int64_t D, const int64_t* strides, int causal, int dtype,
+                               const float* cos_table, const float* sin_table,
+                               const void* position_ids, int position_kind,
+                               int64_t max_position, void* stream);
+
+/* Backward of tritium_attention_fwd_rope (no counterpart in the reference;
+ * see above): q unrotated as in the forward, dq the gradient of the
+ * unrotated q (the inverse rotation applied before the store).  q_rot:
+ * [B, H, Tq, D] contiguous workspace in `dtype`, 16-byte aligned, which the
+ * dQ kernel fills with the rotated q for the dK/dV kernel. */
+int tritium_attention_bwd_rope(const void* dout, const void* q, const void* k, const void* v,
+                               const void* o, const float* lse, void* dq, void* dk, void* dv,
+                               float* delta, void* q_rot, int64_t B, int64_t H, int64_t Hkv,
+                               int64_t Tq, int64_t Tkv, int64_t D, const int64_t* strides,
+                               int causal, int dtype, const float* cos_table,
+                               const float* sin_table, const void* position_ids,
+                               int position_kind, int64_t max_position, void* stream);
 
 /* The attention forward for one query row per (batch, head) against a K/V
  * cache (the reference's decode branch, attention.py:144-217, 354-396:

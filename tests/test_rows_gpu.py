@@ -94,24 +94,48 @@ def test_rope_rows_in_fused_qkv_matches_rope(dtype, head_dim):
     assert torch.equal(back[:, 2], torch.full_like(back[:, 2], 7.0))  # v rows untouched
 
 
-def test_fused_qkv_split_matches_unbind_rope():
-    # the training harness's split (gpt._QKVRope) against unbind + contiguous + rope, fwd and bwd
-    from helion_amd.gpt import _QKVRope
+def test_fused_qkv_rope_attention_matches_unbind_rope_attention():
+    # the training harness's attention block (gpt._QKVRopeAttention: k rotated once out of
+    # the fused projection, q rotated by the attention kernels as they load it, v read in
+    # place) against unbind + rope on contiguous copies + attention, forward and backward
+    from helion_amd.gpt import _QKVRopeAttention
     b, s, h, d = 2, 96, 3, 64
     cos, sin = _tables(128, d)
     pos = torch.arange(s, device="cuda").repeat(b)
     base = randn((b, s, 3, h, d), torch.bfloat16, 5)
-    gq, gk, gv = (randn((b * s, h, d), torch.bfloat16, 10 + i) for i in range(3))
+    go = randn((b, s, h, d), torch.bfloat16, 10)
     x1 = base.clone().requires_grad_(True)
-    q1, k1, v1 = _QKVRope.apply(x1, cos, sin, pos)
-    torch.autograd.backward([q1, k1, v1], [gq, gk, gv.view(b, s, h, d)])
+    o1 = _QKVRopeAttention.apply(x1, cos, sin, pos)
+    o1.backward(go)
     x2 = base.clone().requires_grad_(True)
     qv, kv, vv = x2.unbind(2)
     q2, k2 = tritium.rope(qv.reshape(b * s, h, d).contiguous(), kv.reshape(b * s, h, d).contiguous(),
                           cos, sin, position_ids=pos)
-    torch.autograd.backward([q2, k2, vv], [gq, gk, gv.view(b, s, h, d)])
-    assert torch.equal(q1, q2) and torch.equal(k1, k2) and torch.equal(v1, vv)
-    assert torch.equal(x1.grad, x2.grad)
+    o2 = tritium.attention(q2.view(b, s, h, d).transpose(1, 2), k2.view(b, s, h, d).transpose(1, 2),
+                           vv.transpose(1, 2), is_causal=True).transpose(1, 2)
+    o2.backward(go)
+    # the rotation rounds as the rope kernel does: forward, dk and dv are bitwise equal
+    assert torch.equal(o1, o2)
+    assert torch.equal(x1.grad[:, :, 1], x2.grad[:, :, 1])
+    assert torch.equal(x1.grad[:, :, 2], x2.grad[:, :, 2])
+    # dq is un-rotated from its fp32 accumulators (one rounding instead of two)
+    dq2 = x2.grad[:, :, 0].float()
+    torch.testing.assert_close(x1.grad[:, :, 0].float(), dq2, rtol=1.6e-2,
+                               atol=float(1e-2 * dq2.abs().max()))
+
+
+def test_rope_rows_k_alone_matches_rope():
+    # q = q_out = None rotates k alone (the attention with rope on q's load needs only k)
+    from helion_amd.rope import rope_rows
+    t, h, d = 130, 4, 128
+    k = randn((t, h, d), torch.bfloat16, 41)
+    cos, sin = _tables(256, d)
+    pos = torch.randint(0, 256, (t,), generator=torch.Generator().manual_seed(4)).cuda()
+    out = torch.empty_like(k)
+    rope_rows(None, k, cos, sin, pos, None, out, inverse=False, in_token_stride=h * d,
+              out_token_stride=h * d)
+    _, ek = tritium.rope(k, k, cos, sin, position_ids=pos)
+    assert torch.equal(out, ek)
 
 
 def test_rope_out_of_range_position_is_nan_not_a_fault():
