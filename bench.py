@@ -702,6 +702,47 @@ def mfma_roofline(kernels: str, flops: float, ms: float, counters: str) -> dict:
 
 
 
+def stream_probe(torch, tritium, reps: int = 10):
+    """GB/s of the plain streaming patterns of ``tritium_stream_probe`` (nontemporal
+    16-byte accesses, persistent grids of 2048-16384 workgroups): read 1 GiB, copy
+    1 GiB, fill 1 GiB, and the AdamW-shaped in-place update over 124,439,808 fp32
+    elements (4 streams read, 3 written).  Median of ``reps`` event-timed launches."""
+    import statistics
+
+    from helion_amd import _lib
+
+    dev = torch.device("cuda")
+    n = 1 << 26  # 16-byte vectors: 1 GiB
+    a = torch.ones(n * 4, device=dev)
+    b = torch.empty(n * 4, device=dev)
+    sink = torch.zeros(256, device=dev)
+    npar = 124439808 // 4 * 4
+    p, g, m, v = (torch.rand(npar, device=dev) for _ in range(4))
+    cases = [("read 1 GiB", 0, (a, sink, None, None), n, 1 << 30),
+             ("copy 1 GiB", 1, (a, b, None, None), n, 2 << 30),
+             ("fill 1 GiB", 2, (b, None, None, None), n, 1 << 30),
+             ("adamw-shaped 4 read + 3 write", 3, (p, g, m, v), npar // 4, 28 * npar)]
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    out = []
+    for name, pat, bufs, nv, nbytes in cases:
+        row = {"pattern": name, "bytes": nbytes}
+        for blocks in (2048, 4096, 8192, 16384):
+            ptrs = [None if x is None else x.data_ptr() for x in bufs]
+            times = []
+            for _ in range(reps + 1):
+                s.record()
+                _lib.call("tritium_stream_probe", pat, *ptrs, nv, blocks, _lib.stream_of(a))
+                e.record()
+                torch.cuda.synchronize()
+                times.append(s.elapsed_time(e))
+            ms = statistics.median(times[1:])
+            row[f"GB/s b{blocks}"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+        row["best_frac_of_8TB/s"] = round(max(vv for k, vv in row.items() if k.startswith("GB/s"))
+                                          / HBM_PEAK_GBS, 4)
+        out.append(row)
+    return {"stream_probe": out}
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -711,6 +752,9 @@ def main(argv=None) -> int:
     ap.add_argument("--legs", default="rows,attention,lce,gpt,refbench,decode",
                     help="comma list of rows,attention,lce,gpt,refbench (rows is the headline; "
                          "refbench reruns the reference's published benchmark rows)")
+    ap.add_argument("--stream-probe", action="store_true",
+                    help="only time the HBM streaming probes (read, copy, fill, AdamW-shaped "
+                         "update; tritium_stream_probe) that set the row kernels' ceilings")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only run a plain 1 GiB device copy 5 times (calibrates the HBM "
                          "byte counters of a profiler against a kernel of known traffic)")
@@ -737,6 +781,10 @@ def main(argv=None) -> int:
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes_read": src.numel() * 4,
                           "copy_probe_bytes_written": dst.numel() * 4, "launches": 5}))
+        return 0
+
+    if args.stream_probe:
+        print(json.dumps(stream_probe(torch, tritium)))
         return 0
 
     ops: dict = {}

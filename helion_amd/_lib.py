@@ -100,6 +100,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I32,
         [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P],
     ),
+    "tritium_stream_probe": (_I32, [_I32, _P, _P, _P, _P, _I64, _I32, _P]),
     "tritium_embedding_bwd_workspace_size": (_SZ, [_I64, _I64, _I64]),
     "tritium_embedding_bwd": (
         _I32, [_P, _I32, _I64, _P, _I64, _P, _P, _I64, _I64, _P, _SZ, _I32, _P],

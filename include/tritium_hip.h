@@ -347,6 +347,15 @@ int tritium_cross_entropy_bwd(const float* grad_out, const void* logits, const v
                               int target_kind, const float* lse, void* dlogits, int64_t n_rows,
                               int64_t vocab, double grad_denominator, int dtype, void* stream);
 
+/* ---- measurement ---------------------------------------------------------
+ * HBM streaming probes for bench.py --stream-probe (no counterpart in the
+ * reference; measurement only): pattern 0 reads n_vec4 16-byte vectors of a
+ * (b: a 1 KB scratch sink), 1 copies a to b, 2 fills a, 3 runs an AdamW-shaped
+ * update reading a, b, c, d and writing a, c, d in place -- all with
+ * nontemporal 16-byte accesses from `blocks` 256-lane workgroups. */
+int tritium_stream_probe(int pattern, void* a, void* b, void* c, void* d, int64_t n_vec4,
+                         int blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
