@@ -417,51 +417,61 @@ DECODE_SHAPES = ((1, 32, 32, 4096, 128), (8, 32, 32, 4096, 128), (8, 32, 8, 8192
                  (16, 12, 12, 1024, 64))
 
 
-def decode_leg(torch, tritium, calls: int = 50):
+def decode_leg(torch, tritium, calls: int = 50, rotate_bytes: int = 3 << 28):
     """KV-cache decode: ``attention`` with one query row per head against a
     bf16 cache slice (B, H, H_kv, L, D) in ``DECODE_SHAPES``.  Per shape the
     eager time per call (host path included: back-to-back calls) and the time
     per call of the same calls replayed from one captured graph (the kernels
-    alone), with GB/s on the K + V bytes the call must read (HBM-bound)."""
+    alone), with GB/s on the K + V bytes the call must read (HBM-bound).  The
+    calls rotate over enough copies of the cache (at least ``rotate_bytes``,
+    3x the 256 MB last-level cache) that each call reads its K and V from HBM,
+    not from a cache the previous call left warm."""
     dev = torch.device("cuda")
     g = torch.Generator(device=dev).manual_seed(0)
     out = []
     for b, h, hkv, L, d in DECODE_SHAPES:
-        kc = torch.randn((b, hkv, L + 512, d), generator=g, device=dev).to(torch.bfloat16)
-        vc = torch.randn((b, hkv, L + 512, d), generator=g, device=dev).to(torch.bfloat16)
+        per_copy = 2 * b * hkv * (L + 512) * d * 2
+        n_copies = max(2, -(-rotate_bytes // per_copy))
+        caches = []
+        for _ in range(n_copies):
+            kc = torch.randn((b, hkv, L + 512, d), generator=g, device=dev).to(torch.bfloat16)
+            vc = torch.randn((b, hkv, L + 512, d), generator=g, device=dev).to(torch.bfloat16)
+            caches.append((kc[:, :, :L], vc[:, :, :L]))
         q = torch.randn((b, h, 1, d), generator=g, device=dev).to(torch.bfloat16)
-        k, v = kc[:, :, :L], vc[:, :, :L]
 
-        def fn():
+        def fn(i):
+            k, v = caches[i % n_copies]
             return tritium.attention(q, k, v, is_causal=False)
 
-        for _ in range(5):
-            ref = fn()
+        for i in range(5):
+            fn(i)
+        ref = [fn(i) for i in range(n_copies)]
         torch.cuda.synchronize()
         s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         s.record()
-        for _ in range(calls):
-            fn()
+        for i in range(calls):
+            fn(i)
         e.record()
         torch.cuda.synchronize()
         eager_us = s.elapsed_time(e) / calls * 1e3
         nbytes = 2 * b * hkv * L * d * 2
-        row = {"shape": [b, h, hkv, L, d], "kv_bytes": nbytes, "eager_us": round(eager_us, 1)}
+        row = {"shape": [b, h, hkv, L, d], "kv_bytes": nbytes, "cache_copies": n_copies,
+               "eager_us": round(eager_us, 1)}
         try:
             side = torch.cuda.Stream()
             side.wait_stream(torch.cuda.current_stream())
             with torch.cuda.stream(side):
-                for _ in range(3):
-                    fn()
+                for i in range(3):
+                    fn(i)
             torch.cuda.current_stream().wait_stream(side)
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):
-                for _ in range(calls):
-                    got = fn()
+                got = [fn(i) for i in range(calls)]
             for _ in range(2):
                 graph.replay()
             torch.cuda.synchronize()
-            row["graph_matches_eager"] = bool(torch.equal(got, ref))
+            row["graph_matches_eager"] = bool(all(torch.equal(got[i], ref[i % n_copies])
+                                                  for i in range(calls)))
             reps = 5
             s.record()
             for _ in range(reps):
@@ -471,11 +481,11 @@ def decode_leg(torch, tritium, calls: int = 50):
             us = s.elapsed_time(e) / (reps * calls) * 1e3
             row.update({"graph_us": round(us, 1), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1),
                         "frac_hbm_peak": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)})
-            del graph
+            del graph, got
         except RuntimeError as exc:  # capture refused: report the eager figure only
             row["graph_error"] = str(exc)[:200]
         out.append(row)
-        del kc, vc
+        del caches, ref
     torch.cuda.synchronize()
     torch.cuda.empty_cache()
     return out
