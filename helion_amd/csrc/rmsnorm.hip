@@ -445,7 +445,7 @@ FastCfg pick_fast(int64_t hidden, int vec, int max_nv) {
 #define TRI_RMS_FWD_MAX_NV 1
 #endif
 #ifndef TRI_RMS_FWD_BLOCKS
-#define TRI_RMS_FWD_BLOCKS 2048
+#define TRI_RMS_FWD_BLOCKS 8192
 #endif
 constexpr int kFwdMaxNV = TRI_RMS_FWD_MAX_NV;
 constexpr int64_t kFwdBlocks = TRI_RMS_FWD_BLOCKS;  // persistent forward grid (rows loop inside)
