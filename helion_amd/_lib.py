@@ -120,6 +120,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _I32, _I64, _F32, _F32, _F32, _F32, _F32, _F64, _F64, _P],
     ),
     "tritium_cross_entropy_fwd": (_I32, [_P, _P, _I32, _P, _P, _P, _I64, _I64, _I32, _P]),
+    "tritium_cross_entropy_fwd_workspace_size": (_SZ, [_I64, _I64, _I32]),
     "tritium_cross_entropy_bwd": (
         _I32, [_P, _P, _P, _I32, _P, _P, _I64, _I64, _F64, _I32, _P],
     ),

@@ -79,11 +79,13 @@ def _cross_entropy_forward(logits: torch.Tensor, target: torch.Tensor):
     if n_rows == 0:
         return torch.zeros((), device=dev, dtype=torch.float32), lse
     loss = torch.empty((), device=dev, dtype=torch.float32)
-    nll = torch.empty((n_rows,), device=dev, dtype=torch.float32)
+    code = _lib.dtype_code(logits.dtype)
+    ws_bytes = _lib.lib().tritium_cross_entropy_fwd_workspace_size(n_rows, vocab_size, code)
+    work = torch.empty((max(1, -(-ws_bytes // 4)),), device=dev, dtype=torch.float32)
     _lib.call(
         "tritium_cross_entropy_fwd", logits.data_ptr(), target.data_ptr(), _target_kind(target),
-        loss.data_ptr(), lse.data_ptr(), nll.data_ptr(), n_rows, vocab_size,
-        _lib.dtype_code(logits.dtype), _lib.stream_of(logits),
+        loss.data_ptr(), lse.data_ptr(), work.data_ptr(), n_rows, vocab_size, code,
+        _lib.stream_of(logits),
     )
     return loss, lse
 

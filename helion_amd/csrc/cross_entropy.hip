@@ -11,9 +11,13 @@
 // then merge their pairs with cross-lane shuffles (and LDS across the
 // wavefronts of a block when a whole block shares one row).  Rows shorter
 // than kWideRow get one wavefront each, longer ones a 256-lane block, so both
-// small vocabularies with many rows and one long row fill the machine.  The
-// per-row nll values are summed by one block in a fixed order (the reference
-// accumulates them with atomics), so the loss is deterministic.
+// small vocabularies with many rows and one long row fill the machine; a few
+// long rows are cut into spans over more blocks (ce_span_kernel).  The per-row
+// nll values are summed by one wavefront in a fixed order (the reference
+// accumulates them with atomics), so the loss is deterministic.  A one-launch
+// form (the last block to finish forms the loss behind an arrival counter)
+// was measured slower: its agent-scope release and acquire fences cost more
+// on this 8-XCD part than the second launch.
 #include "common.h"
 #include "../../include/tritium_hip.h"
 
@@ -139,19 +143,101 @@ ce_fwd_kernel(const T* __restrict__ logits, const void* __restrict__ target, flo
   }
 }
 
-// loss = sum(nll) / n_rows, summed in a fixed order (fp64 partials).
-__global__ void __launch_bounds__(kBlock)
+// sum over the 64 lanes of fp64 partials; lane 0's total is formed in a fixed order
+__device__ __forceinline__ double wave_sum_f64(double v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, kWave);
+  return v;
+}
+
+// loss = sum(nll) / n_rows by one wavefront, summed in a fixed order (fp64
+// partials: lane l takes rows l, l + 64, ...).  A single wavefront needs no
+// barrier, which keeps this tail launch short (4.0 -> 3.6 us at 128 rows).
+__global__ void __launch_bounds__(kWave)
 ce_mean_kernel(const float* __restrict__ nll, int64_t n_rows, float* __restrict__ loss) {
-  __shared__ double part[kBlock];
   double acc = 0.0;
-  for (int64_t i = threadIdx.x; i < n_rows; i += kBlock) acc += (double)nll[i];
-  part[threadIdx.x] = acc;
-  __syncthreads();
-  for (int w = kBlock / 2; w > 0; w >>= 1) {
-    if (threadIdx.x < w) part[threadIdx.x] += part[threadIdx.x + w];
-    __syncthreads();
+  int64_t i = threadIdx.x;
+  for (; i + 3 * kWave < n_rows; i += 4 * kWave) {
+    const float a = nll[i], b = nll[i + kWave], c = nll[i + 2 * kWave], d = nll[i + 3 * kWave];
+    acc += (double)a;
+    acc += (double)b;
+    acc += (double)c;
+    acc += (double)d;
   }
-  if (threadIdx.x == 0) loss[0] = (float)(part[0] / (double)n_rows);
+  for (; i < n_rows; i += kWave) acc += (double)nll[i];
+  acc = wave_sum_f64(acc);
+  if (threadIdx.x == 0) loss[0] = (float)(acc / (double)n_rows);
+}
+
+// Few long rows (fewer rows than the GPU has room for blocks): each row is
+// cut into `chunks` spans of `span` elements (a multiple of 8), one 256-lane
+// block per span writes the span's (max, sum) in log2 units; ce_finish_kernel
+// merges a row's spans in span order.  A single block per row would leave
+// most compute units idle and stream each row through one of them.
+template <typename T>
+__global__ void __launch_bounds__(kBlock)
+ce_span_kernel(const T* __restrict__ logits, float2* __restrict__ part, int64_t V, int64_t span,
+               int chunks, int vec_ok) {
+  const int64_t row = blockIdx.x / chunks;
+  const int c = (int)(blockIdx.x - row * chunks);
+  const int64_t c0 = (int64_t)c * span;
+  const int64_t len = min(span, V - c0);
+  float m = -INFINITY, s = 0.0f;
+  row_ms<T, kBlock>(logits + row * V + c0, len, vec_ok != 0, threadIdx.x, m, s);
+  wave_merge(m, s);
+  __shared__ float sm[kBlock / kWave], ss[kBlock / kWave];
+  const int w = threadIdx.x / kWave;
+  if ((threadIdx.x & (kWave - 1)) == 0) {
+    sm[w] = m;
+    ss[w] = s;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    m = sm[0];
+    s = ss[0];
+#pragma unroll
+    for (int i = 1; i < kBlock / kWave; ++i) merge_ms(m, s, sm[i], ss[i]);
+    part[blockIdx.x] = make_float2(m, s);
+  }
+}
+
+// One wavefront: lane l finishes rows l, l + 64, ... (the spans merged in
+// order, lse, nll) and the loss is their mean in a fixed order (fp64).
+template <typename T, typename TT>
+__global__ void __launch_bounds__(kWave)
+ce_finish_kernel(const T* __restrict__ logits, const void* __restrict__ target,
+                 const float2* __restrict__ part, float* __restrict__ lse, float* __restrict__ loss,
+                 int64_t n_rows, int64_t V, int chunks) {
+  double acc = 0.0;
+  for (int64_t row = threadIdx.x; row < n_rows; row += kWave) {
+    const int64_t t = target_at<TT>(target, row);
+    const float xt = (t >= 0 && t < V) ? to_f32(logits[row * V + t]) : 0.0f;
+    float m = -INFINITY, s = 0.0f;
+    for (int c = 0; c < chunks; ++c) {
+      const float2 p = part[row * chunks + c];
+      merge_ms(m, s, p.x, p.y);
+    }
+    const float l = (m + __log2f(s)) * kLn2;
+    lse[row] = l;
+    acc += (t >= 0 && t < V) ? (double)(l - xt) : (double)__builtin_nanf("");
+  }
+  acc = wave_sum_f64(acc);
+  if (threadIdx.x == 0) loss[0] = (float)(acc / (double)n_rows);
+}
+
+// Span split of the forward: (chunks, span) with chunks = 1 for the per-row
+// kernels.  Rows of at least 2 kMinSpan elements are split when there are
+// fewer rows than two blocks per compute unit, into spans of at least
+// kMinSpan elements, enough of them to give every compute unit two blocks.
+constexpr int64_t kMinSpan = 4096;
+void span_split(int64_t n_rows, int64_t V, int& chunks, int64_t& span) {
+  chunks = 1;
+  span = V;
+  const int64_t want = 2 * (int64_t)cu_count();
+  if (V < 2 * kMinSpan || n_rows >= want) return;
+  const int64_t c = std::min<int64_t>(V / kMinSpan, cdiv(want, n_rows));
+  span = cdiv(cdiv(V, c), 8) * 8;
+  chunks = (int)cdiv(V, span);
 }
 
 // dlogits for one kBwdChunk-element span of one row per block.
@@ -206,14 +292,41 @@ bool rows_vec_ok(const void* p, int64_t V, int dtype) {
 
 using namespace tri;
 
+extern "C" size_t tritium_cross_entropy_fwd_workspace_size(int64_t n_rows, int64_t vocab, int dtype) {
+  (void)dtype;
+  if (n_rows <= 0 || vocab <= 0) return 0;
+  int chunks;
+  int64_t span;
+  span_split(n_rows, vocab, chunks, span);
+  return chunks > 1 ? (size_t)(n_rows * chunks) * sizeof(float2) : (size_t)n_rows * sizeof(float);
+}
+
 extern "C" int tritium_cross_entropy_fwd(const void* logits, const void* target, int target_kind,
-                                         float* loss, float* lse, float* nll, int64_t n_rows,
+                                         float* loss, float* lse, float* work, int64_t n_rows,
                                          int64_t vocab, int dtype, void* stream) {
   if (n_rows < 0 || vocab <= 0) return fail(TRI_EINVAL, "cross_entropy: bad sizes");
   if (n_rows >= ((int64_t)1 << 31)) return fail(TRI_EINVAL, "cross_entropy: too many rows");
   hipStream_t st = (hipStream_t)stream;
   if (n_rows == 0) return TRI_OK;
   const int vec_ok = rows_vec_ok(logits, vocab, dtype);
+  int chunks;
+  int64_t span;
+  span_split(n_rows, vocab, chunks, span);
+  if (chunks > 1) {
+    if ((reinterpret_cast<uintptr_t>(work) & 7u) != 0)
+      return fail(TRI_EINVAL, "cross_entropy: workspace must be 8-byte aligned");
+    float2* part = reinterpret_cast<float2*>(work);
+    TRI_DISPATCH_INDEX(target_kind, TT,
+      TRI_DISPATCH_FLOAT(dtype, T, {
+        ce_span_kernel<T><<<(unsigned)(n_rows * chunks), kBlock, 0, st>>>(
+            (const T*)logits, part, vocab, span, chunks, vec_ok);
+        if (int e = check_launch("cross_entropy_fwd")) return e;
+        ce_finish_kernel<T, TT><<<1, kWave, 0, st>>>((const T*)logits, target, part, lse, loss,
+                                                   n_rows, vocab, chunks);
+      }));
+    return check_launch("cross_entropy_finish");
+  }
+  float* nll = work;
   TRI_DISPATCH_INDEX(target_kind, TT,
     TRI_DISPATCH_FLOAT(dtype, T, {
       if (vocab >= kWideRow) {
@@ -225,7 +338,7 @@ extern "C" int tritium_cross_entropy_fwd(const void* logits, const void* target,
       }
     }));
   if (int e = check_launch("cross_entropy_fwd")) return e;
-  ce_mean_kernel<<<1, kBlock, 0, st>>>(nll, n_rows, loss);
+  ce_mean_kernel<<<1, kWave, 0, st>>>(nll, n_rows, loss);
   return check_launch("cross_entropy_mean");
 }
 

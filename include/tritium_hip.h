@@ -333,11 +333,14 @@ int tritium_sum_splits(const float* src, void* dst, int64_t n_splits, int64_t n,
  * in `dtype` (row-major, contiguous) and int32 (target_kind 1) or int64 (2)
  * targets, lse[row] = logsumexp(logits[row]) in fp32, nll[row] = lse[row] -
  * logits[row, target[row]] (NaN for a target outside [0, vocab)), and
- * loss[0] = mean(nll) summed in a fixed order.  `nll` is caller-provided
- * scratch of n_rows floats. */
+ * loss[0] = mean(nll) summed in a fixed order.  `work` is caller-provided
+ * scratch (8-byte aligned) of tritium_cross_entropy_fwd_workspace_size bytes:
+ * the n_rows nll values, or, for fewer rows than the GPU has room for blocks
+ * of long rows, a (max, sum) pair per span of each row. */
 int tritium_cross_entropy_fwd(const void* logits, const void* target, int target_kind,
-                              float* loss, float* lse, float* nll, int64_t n_rows, int64_t vocab,
+                              float* loss, float* lse, float* work, int64_t n_rows, int64_t vocab,
                               int dtype, void* stream);
+size_t tritium_cross_entropy_fwd_workspace_size(int64_t n_rows, int64_t vocab, int dtype);
 
 /* tritium.cross_entropy_backward (cross_entropy.py:71-100
  * `_cross_entropy_backward_kernel`, host 728-799): dlogits = (exp(logits -

@@ -40,7 +40,9 @@ def _close(actual, expected, dtype=None, tol=None):
 
 # ------------------------------------------------------------- cross_entropy
 CE_SHAPES = [(1, 10), (7, 100), (64, 1000), (33, 8191), (16, 8192), (8, 50304), (3, 131072),
-             (5, 12345), (300, 257)]
+             (5, 12345), (300, 257),
+             # the one-launch path (<= 128 rows of <= 128 16-byte vectors) and its edges
+             (128, 1024), (129, 1024), (128, 1032), (16, 512), (1, 8)]
 
 
 def _targets(n, v, seed, dtype=torch.int64):
@@ -255,3 +257,20 @@ def test_layernorm_only_needs_dx():
     w, b = randn(256, seed=2), randn(256, seed=3)
     tritium.layernorm(x, w, b).sum().backward()
     assert x.grad is not None and w.grad is None and b.grad is None
+
+
+@pytest.mark.parametrize(("n", "v"), [(128, 1024), (3, 131072), (700, 8192)])
+def test_cross_entropy_forward_repeated_calls(n, v):
+    # calls of different sizes in a row (per-row and row-span paths, the span
+    # count changing with the row count) each match the float64 reference, and a
+    # repeated call is bitwise identical (fixed-order merges and mean)
+    shapes = [(n, v), (max(1, n // 2), v), (n, v)]
+    for i, (nn, vv) in enumerate(shapes):
+        logits = randn((nn, vv), torch.bfloat16, seed=i + nn, scale=2.0)
+        target = _targets(nn, vv, seed=i)
+        loss, lse = ce_mod._cross_entropy_forward(logits, target)
+        ref_loss, ref_lse, _ = _ce_ref(logits, target)
+        _close(loss, ref_loss, tol=1e-5)
+        _close(lse, ref_lse, tol=1e-5)
+        loss2, _ = ce_mod._cross_entropy_forward(logits, target)
+        assert torch.equal(loss, loss2)
