@@ -206,8 +206,16 @@ def dtype_code(dtype: torch.dtype) -> int:
     return DTYPE_CODES[dtype]
 
 
+# torch's raw current-stream query (what its own C++ extensions use) returns
+# the handle without building a Stream object: 0.1 us per call against about
+# 2 us for torch.cuda.current_stream(...).cuda_stream
+_raw_stream = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+
+
 def stream_of(t: torch.Tensor) -> int:
     """Handle of torch's current stream on ``t``'s device."""
+    if _raw_stream is not None and t.is_cuda:
+        return _raw_stream(t.get_device())
     return torch.cuda.current_stream(t.device).cuda_stream
 
 

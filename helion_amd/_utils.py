@@ -22,8 +22,8 @@ def next_power_of_2(n: int) -> int:
 
 
 def check_cuda_tensor(name: str, tensor: torch.Tensor) -> None:
-    """_utils.py:25-27."""
-    if tensor.device.type != "cuda":
+    """_utils.py:25-27 (``is_cuda``: device type "cuda", without building a device object)."""
+    if not tensor.is_cuda:
         raise ValueError(f"{name} must be a CUDA tensor.")
 
 

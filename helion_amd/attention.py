@@ -41,31 +41,30 @@ def _check_attention_inputs(q, k, v) -> tuple[int, int, int, int, int, int]:
     if q.dim() != 4:
         raise ValueError("q must be a 4D tensor shaped (batch, n_heads, q_seq_len, head_dim).")
     batch, n_heads, q_len, head_dim = q.shape
-    n_kv_heads = k.shape[1] if k.dim() == 4 else 0
-    kv_len = k.shape[2] if k.dim() == 4 else 0
+    ks = k.shape
+    n_kv_heads = ks[1] if len(ks) == 4 else 0
+    kv_len = ks[2] if len(ks) == 4 else 0
+    qdtype, qdev = q.dtype, q.device
     for name, t in (("k", k), ("v", v)):
-        if t.dim() != 4:
+        s = t.shape
+        if len(s) != 4:
             raise ValueError(
                 f"{name} must be a 4D tensor shaped (batch, n_kv_heads, kv_seq_len, head_dim)."
             )
-        if t.shape[0] != batch:
-            raise ValueError(f"Shape mismatch: {name} has batch {t.shape[0]}, expected {batch}.")
-        if t.shape[2] != kv_len:
+        if s[0] != batch:
+            raise ValueError(f"Shape mismatch: {name} has batch {s[0]}, expected {batch}.")
+        if s[2] != kv_len:
+            raise ValueError(f"Shape mismatch: {name} has seq_len {s[2]}, expected {kv_len}.")
+        if s[3] != head_dim:
+            raise ValueError(f"Shape mismatch: {name} has head_dim {s[3]}, expected {head_dim}.")
+        if s[1] != n_kv_heads:
             raise ValueError(
-                f"Shape mismatch: {name} has seq_len {t.shape[2]}, expected {kv_len}."
+                f"Shape mismatch: {name} has {s[1]} kv heads, expected {n_kv_heads}."
             )
-        if t.shape[3] != head_dim:
-            raise ValueError(
-                f"Shape mismatch: {name} has head_dim {t.shape[3]}, expected {head_dim}."
-            )
-        if t.shape[1] != n_kv_heads:
-            raise ValueError(
-                f"Shape mismatch: {name} has {t.shape[1]} kv heads, expected {n_kv_heads}."
-            )
-        if t.dtype != q.dtype:
-            raise ValueError(f"Dtype mismatch: {name} has dtype {t.dtype}, q has dtype {q.dtype}.")
-        if t.device != q.device:
-            raise ValueError(f"Device mismatch: {name} is on {t.device}, q is on {q.device}.")
+        if t.dtype != qdtype:
+            raise ValueError(f"Dtype mismatch: {name} has dtype {t.dtype}, q has dtype {qdtype}.")
+        if t.device != qdev:
+            raise ValueError(f"Device mismatch: {name} is on {t.device}, q is on {qdev}.")
     if n_kv_heads == 0 or n_heads % n_kv_heads != 0:
         raise ValueError(
             f"n_heads ({n_heads}) must be divisible by n_kv_heads ({n_kv_heads})."
@@ -87,8 +86,12 @@ def _rows_aligned(t: torch.Tensor) -> bool:
     """Unit head_dim stride, 16-byte aligned base and row strides (what the MFMA
     kernels need of every operand to take it in place)."""
     es = t.element_size()
-    return (t.stride(-1) == 1 and t.data_ptr() % 16 == 0
-            and all((st * es) % 16 == 0 for st in t.stride()[:-1]))
+    st = t.stride()
+    return (st[3] == 1 and t.data_ptr() % 16 == 0
+            and (st[0] * es) % 16 == 0 and (st[1] * es) % 16 == 0 and (st[2] * es) % 16 == 0)
+
+
+_Strides12 = ctypes.c_int64 * 12
 
 
 def _strides(*ts: torch.Tensor):
@@ -97,7 +100,27 @@ def _strides(*ts: torch.Tensor):
     vals: list[int] = []
     for t in ts:
         vals.extend(t.stride()[:3])
+    if len(vals) == 12:
+        return _Strides12(*vals)
     return (ctypes.c_int64 * len(vals))(*vals)
+
+
+# Decode workspaces, one per (device, stream), grown on demand: calls on one
+# stream never overlap, so each reuses its stream's buffer instead of
+# allocating one per call (the partials are written before they are read).
+_DECODE_WS: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _decode_workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    n = max(nbytes, 4) // 4
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty((n,), device=dev, dtype=torch.float32)
+    key = (dev.index if dev.index is not None else torch.cuda.current_device(), stream)
+    buf = _DECODE_WS.get(key)
+    if buf is None or buf.numel() < n:
+        buf = torch.empty((n,), device=dev, dtype=torch.float32)
+        _DECODE_WS[key] = buf
+    return buf
 
 
 def _attention_forward(q, k, v, is_causal: bool):
@@ -117,11 +140,12 @@ def _attention_forward(q, k, v, is_causal: bool):
         # decode: one query row per head against a K/V cache, split over the keys
         ws_bytes = _lib.lib().tritium_attention_decode_workspace_size(
             batch, n_heads, n_kv_heads, kv_len, head_dim)
-        ws = torch.empty((max(ws_bytes, 4) // 4,), device=q.device, dtype=torch.float32)
+        stream = _lib.stream_of(q)
+        ws = _decode_workspace(q.device, stream, ws_bytes)
         _lib.call(
             "tritium_attention_decode", q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(),
             lse.data_ptr(), ws.data_ptr(), ws_bytes, batch, n_heads, n_kv_heads, kv_len,
-            head_dim, strides, _lib.dtype_code(q.dtype), _lib.stream_of(q),
+            head_dim, strides, _lib.dtype_code(q.dtype), stream,
         )
         return o, lse
     _lib.call(
