@@ -71,6 +71,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _P, _P, _P, _I64, _F32, _F32, _F32, _F32, _F32, _F64, _F64, _I32, _P],
     ),
     "tritium_adamw_chunk_elements": (_I64, []),
+    "tritium_adamw_mixed_chunk_elements": (_I64, []),
     "tritium_attention_fwd": (
         _I32,
         [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I32, _I32, _P],

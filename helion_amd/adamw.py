@@ -253,7 +253,7 @@ def adamw_step_mixed(
     if gdt not in (torch.float16, torch.bfloat16):
         raise ValueError(f"grads must be float16 or bfloat16, got {gdt}.")
     device = params[0].device
-    chunk = int(_lib.lib().tritium_adamw_chunk_elements())
+    chunk = int(_lib.lib().tritium_adamw_mixed_chunk_elements())
     rows: list[int] = []
     first = 0
     for i in range(n):

@@ -128,6 +128,8 @@ int tritium_adamw_step(void* param, const void* grad, float* exp_avg, float* exp
 
 /* Elements one block of the multi-tensor kernel updates. */
 int64_t tritium_adamw_chunk_elements(void);
+/* Elements one block of the mixed-precision multi-tensor kernel updates. */
+int64_t tritium_adamw_mixed_chunk_elements(void);
 
 /* Multi-tensor AdamW in ONE launch (replaces the per-parameter loop of
  * helion.AdamW.step, helion/optim.py:50-70, each iteration of which calls
@@ -145,7 +147,7 @@ int tritium_adamw_step_multi(const int64_t* table, int n_tensors, int64_t total_
  * Arithmetic per element as tritium_adamw_step on the widened gradient.
  * table: device int64 rows of 8 words [param, grad, exp_avg, exp_avg_sq,
  * numel, flags (bit 0: all pointers 16-byte aligned), first_chunk, shadow or
- * 0], first_chunk the prefix sum of ceil(numel / tritium_adamw_chunk_elements()).
+ * 0], first_chunk the prefix sum of ceil(numel / tritium_adamw_mixed_chunk_elements()).
  * No counterpart in the reference (whose adamw_step requires grad and param
  * of one dtype, adamw.py:86-90): it serves a training step whose weights are
  * 16-bit copies of fp32 masters, which would otherwise widen every gradient

@@ -261,7 +261,8 @@ def test_adamw_mixed_matches_fp32_step(gdtype):
     # tritium_adamw_step_mixed: same update as adamw_step on the widened gradient; the
     # shadow is the updated fp32 param rounded once; ragged sizes take the element path
     from helion_amd.adamw import adamw_step_mixed
-    shapes = [(4096,), (33, 7), (1,), (768, 768), (5000,)]
+    # (tensors of one or many 8192-element blocks, with and without a ragged last block)
+    shapes = [(4096,), (33, 7), (1,), (768, 768), (5000,), (8193,), (3, 8191), (16384,)]
     ps = [randn(s, torch.float32, 40 + i, scale=0.02) for i, s in enumerate(shapes)]
     gs = [randn(s, gdtype, 50 + i, scale=1e-2) for i, s in enumerate(shapes)]
     ms = [randn(s, torch.float32, 60 + i, scale=1e-3) for i, s in enumerate(shapes)]
