@@ -253,31 +253,48 @@ def adamw_step_mixed(
     if gdt not in (torch.float16, torch.bfloat16):
         raise ValueError(f"grads must be float16 or bfloat16, got {gdt}.")
     device = params[0].device
+    check_cuda_tensor("param", params[0])
+    dev_index = params[0].get_device()
     chunk = int(_lib.lib().tritium_adamw_mixed_chunk_elements())
+    f32 = torch.float32
+    sh_list = shadows if shadows is not None else [None] * n
+    # every tensor of a model passes through here once per step, and this
+    # host time sits between the backward's last kernel and the update: the
+    # common case is checked in bulk, the per-tensor loop below only runs to
+    # name the first bad tensor
+    def good(ts, dt):
+        return all(t.is_cuda and t.dtype is dt and t.get_device() == dev_index and t.is_contiguous()
+                   for t in ts)
+
+    fast = (good(params, f32) and good(exp_avgs, f32) and good(exp_avg_sqs, f32) and good(grads, gdt)
+            and (shadows is None or good(shadows, gdt))
+            and all(p.shape == g.shape == m.shape == v.shape
+                    for p, g, m, v in zip(params, grads, exp_avgs, exp_avg_sqs))
+            and (shadows is None or all(p.shape == s.shape for p, s in zip(params, shadows))))
+    if not fast:
+        for i in range(n):
+            p, sh = params[i], sh_list[i]
+            for name, t, dt in (("param", p, f32), ("grad", grads[i], gdt), ("exp_avg", exp_avgs[i], f32),
+                                ("exp_avg_sq", exp_avg_sqs[i], f32)) + ((("shadow", sh, gdt),) if sh is not None else ()):
+                check_cuda_tensor(name, t)
+                if t.dtype != dt:
+                    raise ValueError(f"{name} must have dtype {dt}, got {t.dtype}.")
+                if t.shape != p.shape:
+                    raise ValueError(f"Shape mismatch: {name} has shape {tuple(t.shape)}, "
+                                     f"param has shape {tuple(p.shape)}.")
+                if t.device != device:
+                    raise ValueError(f"Device mismatch: {name} is on {t.device}, expected {device}.")
+                check_contiguous(name, t, "for tritium.adamw_step_mixed")
     rows: list[int] = []
     first = 0
-    for i in range(n):
-        p, g, m, v = params[i], grads[i], exp_avgs[i], exp_avg_sqs[i]
-        sh = shadows[i] if shadows is not None else None
-        for name, t, dt in (("param", p, torch.float32), ("grad", g, gdt), ("exp_avg", m, torch.float32),
-                            ("exp_avg_sq", v, torch.float32)) + ((("shadow", sh, gdt),) if sh is not None else ()):
-            check_cuda_tensor(name, t)
-            if t.dtype != dt:
-                raise ValueError(f"{name} must have dtype {dt}, got {t.dtype}.")
-            if t.shape != p.shape:
-                raise ValueError(f"Shape mismatch: {name} has shape {tuple(t.shape)}, "
-                                 f"param has shape {tuple(p.shape)}.")
-            if t.device != device:
-                raise ValueError(f"Device mismatch: {name} is on {t.device}, expected {device}.")
-            check_contiguous(name, t, "for tritium.adamw_step_mixed")
+    for p, g, m, v, sh in zip(params, grads, exp_avgs, exp_avg_sqs, sh_list):
         numel = p.numel()
         if numel == 0:
             continue
-        ptrs = [p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr()]
+        pp, gp, mp, vp = p.data_ptr(), g.data_ptr(), m.data_ptr(), v.data_ptr()
         sp = sh.data_ptr() if sh is not None else 0
-        aligned = all(x % 16 == 0 for x in ptrs + ([sp] if sp else []))
-        rows.extend(ptrs)
-        rows.extend((numel, int(aligned), first, sp))
+        aligned = ((pp | gp | mp | vp | sp) & 15) == 0
+        rows += (pp, gp, mp, vp, numel, int(aligned), first, sp)
         first += -(-numel // chunk)
     if not rows:
         return
