@@ -92,3 +92,28 @@ def test_sum_splits_bitwise_against_ordered_fp32_sum(dtype, s, n):
     _lib.call("tritium_sum_splits", part2.data_ptr(), out.data_ptr(), s, n,
               _lib.dtype_code(dtype), _lib.stream_of(part2))
     assert torch.equal(out, want2.to(dtype))
+
+
+@pytest.mark.gpu
+def test_train_step_weight_gradients_on_second_stream_are_bitwise_equal():
+    # HipGPT.train_step runs the projections' weight-gradient GEMMs on a second
+    # stream (waited for before the update): the gradients and the updated
+    # weights must be bitwise those of the one-stream step
+    cfg = gpt.GPTConfig(vocab_size=1024, d_model=256, n_layers=2, n_heads=4, head_dim=64,
+                        d_ff=512, max_seq_len=256)
+    tc = gpt.TrainConfig(batch=4, seq_len=256, lr=1e-3)
+    init = gpt.init_params(cfg, tc.seed)
+    batch = gpt.lm_batch(cfg, tc, torch.Generator().manual_seed(3), torch.device("cuda"))
+    out = {}
+    saved = gpt.OVERLAP_DW
+    try:
+        for mode in (False, True):
+            gpt.OVERLAP_DW = mode
+            m = gpt.HipGPT(cfg, tc, init, torch.device("cuda"))
+            losses = [float(m.train_step(*batch)) for _ in range(3)]
+            out[mode] = (losses, [g.clone() for g in m._last_grads], m.master.flat.clone())
+    finally:
+        gpt.OVERLAP_DW = saved
+    assert out[False][0] == out[True][0]
+    assert all(torch.equal(a, b) for a, b in zip(out[False][1], out[True][1]))
+    assert torch.equal(out[False][2], out[True][2])
