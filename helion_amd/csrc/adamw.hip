@@ -16,7 +16,8 @@
 //    first_chunk]
 // flags = dtype code | (1 << 8 if all four pointers are 16-byte aligned).
 // first_chunk is the exclusive prefix sum of per-tensor chunk counts; block b
-// finds its tensor by binary search over it.
+// finds its tensor as the length of the prefix of rows with first_chunk <= b
+// (find_tensor).
 #include "common.h"
 #include "../../include/tritium_hip.h"
 
@@ -114,16 +115,35 @@ adamw_single_kernel(T* __restrict__ p, const T* __restrict__ g, float* __restric
 
 constexpr int kDescWords = 7;
 
+// The tensor of block b: the last table row whose first_chunk (word 6) is
+// <= b.  first_chunk does not decrease, so the rows that pass form a prefix
+// and its length is the count of passing rows: each lane tests four rows per
+// round, the loads issued together, where a binary search would chain
+// log2(n) dependent loads before the block's first data load.
+__device__ __forceinline__ int find_tensor(const int64_t* __restrict__ table, int words, int n,
+                                           int64_t b) {
+  const int lane = threadIdx.x & 63;
+  int count = 0;
+  for (int base = 0; base < n; base += 4 * 64) {
+    bool le[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = base + k * 64 + lane;
+      le[k] = i < n && table[(int64_t)i * words + 6] <= b;
+    }
+    int c = 0;
+#pragma unroll
+    for (int k = 0; k < 4; ++k) c += __popcll(__ballot(le[k]));
+    count += c;
+    if (c < 4 * 64) break;  // the prefix ended in this round
+  }
+  return __builtin_amdgcn_readfirstlane(count - 1);
+}
+
 __global__ void __launch_bounds__(kBlock)
 adamw_multi_kernel(const int64_t* __restrict__ table, int n_tensors, Hyper h) {
-  // binary search: last tensor whose first_chunk <= blockIdx.x
   const int64_t b = blockIdx.x;
-  int lo = 0, hi = n_tensors - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (table[mid * kDescWords + 6] <= b) lo = mid; else hi = mid - 1;
-  }
-  const int64_t* d = table + lo * kDescWords;
+  const int64_t* d = table + (int64_t)find_tensor(table, kDescWords, n_tensors, b) * kDescWords;
   const int64_t n = d[4];
   const int flags = (int)d[5];
   const int64_t start = (b - d[6]) * kChunk;
@@ -213,12 +233,7 @@ template <typename TG>
 __global__ void __launch_bounds__(kBlock)
 adamw_mixed_kernel(const int64_t* __restrict__ table, int n_tensors, Hyper h) {
   const int64_t b = blockIdx.x;
-  int lo = 0, hi = n_tensors - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (table[mid * kMixedWords + 6] <= b) lo = mid; else hi = mid - 1;
-  }
-  const int64_t* d = table + lo * kMixedWords;
+  const int64_t* d = table + (int64_t)find_tensor(table, kMixedWords, n_tensors, b) * kMixedWords;
   const int64_t n = d[4];
   const int64_t start = (b - d[6]) * kChunkMixed;
   if (start >= n) return;
