@@ -244,7 +244,7 @@ def attention_leg(torch, tritium, iters: int = 5, warmup: int = 2,
         "bwd_TFLOP/s": round(fb / (bwd_ms * 1e-3) / 1e12, 1),
         "TFLOP/s": round(tot, 1),
         "frac_mfma_peak": round(tot / MFMA_BF16_PEAK_TFLOPS, 4),
-        "roofline": mfma_roofline("attn_fwd_pp + attn_bwd_dq_v2 + attn_bwd_dkdv_pair (one fwd+bwd)",
+        "roofline": mfma_roofline("attn_fwd_pp + attn_bwd_delta_v + attn_bwd_dkdv_pair (storing dS) + attn_bwd_dq_ds (one fwd+bwd)",
                                   ff + fb, fwd_ms + bwd_ms, "attention_config3_counters.txt"),
     }
 

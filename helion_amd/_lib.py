@@ -81,6 +81,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P,
          _I32, _I32, _P],
     ),
+    "tritium_attention_bwd_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I32, _I32]),
+    "tritium_attention_bwd_ws": (
+        _I32,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64, _I64, _P,
+         _I32, _I32, _P],
+    ),
     "tritium_attention_fwd_rope": (
         _I32,
         [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P, _I32, _I32,

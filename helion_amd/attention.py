@@ -31,6 +31,10 @@ from ._utils import FLOAT_DTYPES, check_cuda_tensor, check_supported_dtype, requ
 
 SUPPORTED_DTYPES = FLOAT_DTYPES
 MAX_HEAD_DIM = 1024
+# The backward stores dS (2 bytes per visible (query, key) pair) for head_dim
+# 128 when that workspace stays within this many bytes; above it (long
+# sequences) it recomputes S and dP in its dQ kernel instead.
+DS_WORKSPACE_MAX_BYTES = 8 << 30
 
 
 def _check_attention_inputs(q, k, v) -> tuple[int, int, int, int, int, int]:
@@ -180,8 +184,14 @@ def _attention_backward_impl(do, q, k, v, o, lse, is_causal: bool):
         return dq.zero_(), dk.zero_(), dv.zero_()
     delta = torch.empty((batch * n_heads * q_len,), device=q.device, dtype=torch.float32)
     strides = _strides(q, k, v, o, do, dq, dk, dv)
+    code = _lib.dtype_code(q.dtype)
+    ws_bytes = _lib.lib().tritium_attention_bwd_workspace_size(
+        batch, n_heads, q_len, kv_len, head_dim, int(bool(is_causal)), code)
+    if not 0 < ws_bytes <= DS_WORKSPACE_MAX_BYTES:
+        ws_bytes = 0
+    ws = torch.empty((ws_bytes,), device=q.device, dtype=torch.uint8) if ws_bytes else None
     _lib.call(
-        "tritium_attention_bwd",
+        "tritium_attention_bwd_ws",
         do.data_ptr(),
         q.data_ptr(),
         k.data_ptr(),
@@ -192,6 +202,8 @@ def _attention_backward_impl(do, q, k, v, o, lse, is_causal: bool):
         dk.data_ptr(),
         dv.data_ptr(),
         delta.data_ptr(),
+        ws.data_ptr() if ws is not None else None,
+        ws_bytes,
         batch,
         n_heads,
         n_kv_heads,

@@ -24,6 +24,10 @@
 //            them in opposite phases, and accumulate dV^T and dK^T in registers
 //            (GQA: all query heads of the group), written once in the output
 //            dtype.  No atomics: results are bitwise deterministic.
+//            With a dS workspace (head_dim 128, no RoPE): delta first, then
+//            the dK/dV kernel storing every dS tile it forms (2 bytes per
+//            visible pair), then dQ = dS K * scale from the stored tiles --
+//            no second S and dP, at the price of the dS traffic.
 //
 // fp32 inputs (and head_dim outside the MFMA set, up to 1024) run on a SIMT
 // path: one wavefront per row, exact fp32 arithmetic.
@@ -47,6 +51,7 @@ namespace {
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr float kLn2 = 0.6931471805599453f;
@@ -140,7 +145,33 @@ struct BwdArgs {
   float scale;
   RopeQ rope;
   void* q_rot;  // with rope: [B, H, Tq, D] rotated q, written by the dQ kernel for dK/dV
+  void* ds;       // stored-dS path: the dS chunks (ds_row below), else nullptr
+  int64_t ds_bh;  // elements per (batch, query head) in ds
 };
+
+// Stored-dS layout.  Per (batch, query head) a run of ds_bh 16-bit elements
+// holds 64 x 64 chunks: those of query tile qt (rows 64 qt ..) are the kv
+// tiles j = 0 .. n_j(qt) - 1 in order from chunk ds_row(qt) on, with
+// n_j = min(qt + 1, n_kvt) under the causal mask (kv row <= query row) and
+// n_kvt without.  A chunk holds [64 kv rows][64 columns] as 16-byte granules
+// (8 columns of a row): granule c of row r at element
+// 2048 (r >> 5) + 512 (c & 3) + 8 (32 (c >> 2) + (r & 31)), i.e. in the
+// order in which the dK/dV kernel's wavefront pair holds the tile (row
+// r & 31 its lane's kv row, c >> 2 the lane half g, c & 3 the operand t), so
+// each of its four 16-byte stores per lane writes 1 KiB contiguous; column
+// 8 c + e holds query row 16 (c & 3) + 8 (e >> 2) + 4 (c >> 2) + (e & 3) of
+// the tile.
+__host__ __device__ __forceinline__ int64_t ds_row(int causal, int qt, int n_kvt) {
+  if (!causal) return (int64_t)qt * n_kvt;
+  if (qt <= n_kvt) return (int64_t)qt * (qt + 1) / 2;
+  return (int64_t)n_kvt * (n_kvt + 1) / 2 + (int64_t)(qt - n_kvt) * n_kvt;
+}
+
+// Query row (within its tile) of chunk column c.
+__device__ __forceinline__ int ds_col_row(int c) {
+  const int gr = c >> 3, e = c & 7;
+  return 16 * (gr & 3) + 8 * (e >> 2) + 4 * (gr >> 2) + (e & 3);
+}
 
 // Position of query row t of batch b under r, and whether the tables hold it.
 __device__ __forceinline__ bool rope_position(const RopeQ& r, int b, int Tq, int t, int64_t& pos) {
@@ -1599,6 +1630,8 @@ attn_bwd_dkdv_v2(BwdArgs a) {
 // tile s - 2, last read in 2s - 1) and has them landed by the end of 2s + 1
 // (Q first read in 2s + 2); A loads dO of tile s + 1 in 2s + 1 and has it
 // landed by the end of 2s + 2 (first read in 2s + 3).
+// DS: role B also stores each dS tile (cast to T, as the dK MFMAs take it)
+// in the stored-dS layout, for attn_bwd_dq_ds; zero in kv rows >= Tkv.
 constexpr int kPairWaves = 8;
 constexpr int kPairBN = 128;
 constexpr int kDkvPPStages = 3;
@@ -1607,7 +1640,7 @@ constexpr int kDkvPPStages = 3;
 #endif
 constexpr int kDkvRing = TRI_ATTN_DKDV_RING;  // MFMA operands in flight ahead of use
 
-template <typename T, int D>
+template <typename T, int D, bool DS>
 __global__ void __launch_bounds__(64 * kPairWaves, 1)  // 2 wavefronts per SIMD
 attn_bwd_dkdv_pair(BwdArgs a) {
   typedef Mfma<T> M;
@@ -1837,6 +1870,13 @@ attn_bwd_dkdv_pair(BwdArgs a) {
       sc = sc == kDkvPPStages - 1 ? 0 : sc + 1;
     }
   } else {
+    // stored dS: the pair's chunk column, its row there, whether it exists
+    // (n_kvt columns) and whether the pair has rows past Tkv (pair-uniform)
+    const int n_kvt = (a.Tkv + 63) >> 6;
+    const int ds_j = kvb >> 6;
+    const bool ds_on = DS && ds_j < n_kvt, ds_tail = kvb + 32 > a.Tkv;
+    T* const ds_lane = DS ? (T*)a.ds + ((kvb >> 5) & 1) * 2048 + lane * 8 : nullptr;
+    int hc = 0, hp = 0;  // query head (from hq0) of steps s and s - 1
     for (int s = 0; s <= n_steps; ++s) {
       const int sp = sc == 0 ? kDkvPPStages - 1 : sc - 1;
       char* const stc = smem + sc * STAGE;
@@ -1865,6 +1905,19 @@ attn_bwd_dkdv_pair(BwdArgs a) {
         }
         // the first dK operands (Q_{s-1}^T) of the coming MFMA phase
         pre_tr(qb);
+        // the stored dS, behind those reads (1.6% faster than ahead of them)
+        if constexpr (DS) {
+          if (ds_on) {
+            T* dst = ds_lane + ((int64_t)(b * a.H + hq0 + hp) * a.ds_bh +
+                                (ds_row(a.causal, q0p >> 6, n_kvt) + ds_j) * 4096);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+              u32x4 u = __builtin_bit_cast(u32x4, op[t]);
+              if (ds_tail && !kvvalid) u = u32x4{0u, 0u, 0u, 0u};
+              __builtin_nontemporal_store(u, reinterpret_cast<u32x4*>(dst + 512 * t));
+            }
+          }
+        }
       }
       lds_barrier();
       // half-step 2s + 1: dK^T += Q_{s-1}^T dS_{s-1}, dP_s = dO_s V^T
@@ -1877,6 +1930,8 @@ attn_bwd_dkdv_pair(BwdArgs a) {
 #endif
       lds_barrier();
       q0p = q0c;
+      hp = hc;
+      hc += q0c == q_begin;
       q0c = q0c == q_begin ? q_last : q0c - 64;
       sc = sc == kDkvPPStages - 1 ? 0 : sc + 1;
     }
@@ -2060,6 +2115,173 @@ attn_bwd_dq_v2(BwdArgs a) {
         const int d0 = 32 * mt + 8 * rr + 4 * g;
         store4<T>(dqr + d0, dq[mt][4 * rr], dq[mt][4 * rr + 1], dq[mt][4 * rr + 2],
                   dq[mt][4 * rr + 3]);
+      }
+    }
+  }
+}
+
+// --------------------------------------------- backward: stored-dS path --
+// With a dS workspace the dK/dV kernel stores the dS tiles it forms and dQ =
+// scale * dS K becomes a product over them, instead of a dQ kernel that forms
+// S and dP a second time (the recomputing backward executes 14 D flops per
+// visible (query, key) pair, this one the algorithmic 10 D, plus a 2-byte
+// store and load of dS per pair).  delta then comes from its own kernel,
+// ahead of dK/dV.
+
+// delta[bh][q] = sum_d dO[q][d] * O[q][d] (fp32), summed as the recomputing
+// dQ kernel sums it (two lanes a row, each over alternate 8-column granules
+// in column order, then their sum), so both paths give dK, dV bitwise alike.
+template <typename T, int D>
+__global__ void __launch_bounds__(256)
+attn_bwd_delta_v(BwdArgs a) {
+  constexpr int KS = D / 16;
+  const int lane = threadIdx.x & 63, g = lane >> 5;
+  const int64_t row = (int64_t)blockIdx.x * 128 + (threadIdx.x >> 6) * 32 + (lane & 31);
+  const int64_t n_rows = (int64_t)a.B * a.H * a.Tq;
+  float dl = 0.f;
+  if (row < n_rows) {
+    const int q = (int)(row % a.Tq);
+    const int64_t bh = row / a.Tq;
+    const int b = (int)(bh / a.H), h = (int)(bh % a.H);
+    const T* orow = (const T*)a.o + b * a.so_b + h * a.so_h + (int64_t)q * a.so_s;
+    const T* drow = (const T*)a.dout + b * a.sdo_b + h * a.sdo_h + (int64_t)q * a.sdo_s;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      const auto df = ld8(drow + 16 * s + 8 * g);
+      const auto of = ld8(orow + 16 * s + 8 * g);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dl += (float)df[j] * (float)of[j];
+    }
+  }
+  dl += __shfl_xor(dl, 32, 64);
+  if (row < n_rows && g == 0) a.delta[row] = dl;
+}
+
+// dQ from the stored dS: a workgroup owns query tiles 4 qb .. 4 qb + 3 of one
+// (batch, head) and sweeps the kv tiles they see; per kv tile, K [64][D] and
+// the four dS chunks arrive by DMA in a 3-stage LDS ring (one K tile per four
+// chunks: the sweep moves 1.5 bytes through the CU per byte of dS), and
+// wavefront w accumulates dQ^T over all D for chunk columns 32 (w & 1) .. + 31
+// of query tile 4 qb + (w >> 1): A = K^T and B = dS^T, both from transposing
+// reads (k = kv rows).
+constexpr int kDsWaves = 8;
+constexpr int kDsTiles = 4;  // query tiles per workgroup
+#ifndef TRI_ATTN_DQDS_STAGES
+#define TRI_ATTN_DQDS_STAGES 3
+#endif
+constexpr int kDsStages = TRI_ATTN_DQDS_STAGES;
+
+template <typename T, int D>
+__global__ void __launch_bounds__(64 * kDsWaves, 1)
+attn_bwd_dq_ds(BwdArgs a) {
+  typedef Mfma<T> M;
+  typedef typename M::V V;
+  typedef BTile<D> PK;
+  typedef BTile<64> PS;
+  constexpr int MT = D / 32;
+  constexpr int STAGE = PK::BYTES + kDsTiles * PS::BYTES;
+  __shared__ __attribute__((aligned(1024))) char smem[kDsStages * STAGE];
+  const int lane = threadIdx.x & 63, wave = wave_id();
+  const int l32 = lane & 31, g = lane >> 5;
+  const int w = xcd_remap(blockIdx.x, gridDim.x);
+  const int bh = w / a.n_tiles;
+  const int qb = a.n_tiles - 1 - w % a.n_tiles;  // causal: the longest sweeps first
+  const int b = bh / a.H, h = bh % a.H, hk = h / (a.H / a.Hkv);
+  const int n_qt = (a.Tq + 63) >> 6, n_kvt = (a.Tkv + 63) >> 6;
+  const int qt0 = kDsTiles * qb;
+  const int last = min(qt0 + kDsTiles, n_qt) - 1;  // the workgroup's last query tile
+  const int sel = wave >> 1, mq = wave & 1;
+  const int qt = qt0 + sel;
+  // kv tiles in a query tile's row of chunks, the sweep's, this wavefront's
+  auto n_j = [&](int q) { return a.causal ? min(q + 1, n_kvt) : n_kvt; };
+  const int n_kv = n_j(last);
+  const int my_kv = qt > last ? 0 : n_j(qt);
+  const T* kb = (const T*)a.k + b * a.sk_b + hk * a.sk_h;
+  const T* dsb = (const T*)a.ds + (int64_t)bh * a.ds_bh;
+  BtOffs<T, D> ko;
+  ko.init();
+  // B operand: transposing-read offsets of this wavefront's 32 chunk columns
+  // (BtOffs' table indexed by the run-time mq would be moved to LDS)
+  uint32_t so[2];
+  {
+    const int ts = lane & 15, th = (lane >> 4) & 1, r1 = 4 * g + (ts >> 2);
+#pragma unroll
+    for (int k = 0; k < 2; ++k)
+      so[k] = PS::off(r1 + 8 * k, 4 * mq + 2 * th + ((ts & 3) >> 1)) + (ts & 1) * 8;
+  }
+  BtDma1<T, D, kDsWaves> kdma;
+  kdma.init(a.sk_s, 0);
+  // chunk DMA: this wavefront fills LDS rows 8 wave .. + 7 of each chunk
+  // tile, lane -> row 8 wave + lane / 8, granule (lane % 8) ^ key(row)
+  static_assert(PS::DMAS == kDsWaves, "one DMA per wavefront per chunk");
+  uint32_t soff;
+  {
+    const int r = 8 * wave + (lane >> 3), c = (lane & 7) ^ PS::key(r);
+    soff = (uint32_t)(2 * (2048 * (r >> 5) + 512 * (c & 3) + 8 * (32 * (c >> 2) + (r & 31))));
+  }
+  constexpr int PERW = BtDma1<T, D, kDsWaves>::PER + kDsTiles;  // DMAs per wavefront per tile
+  // kv tile j: K, and chunk (q, j) of each query tile q, clamped to the
+  // tile's row (a tile past the workgroup's last, or a chunk past its row
+  // under the causal mask, is loaded but not multiplied)
+  auto issue = [&](int j) {
+    char* st = smem + (j % kDsStages) * STAGE;
+    kdma.issue_at(st, kb + (int64_t)(64 * j) * a.sk_s, a.sk_s, a.Tkv - 64 * j);
+#pragma unroll
+    for (int k = 0; k < kDsTiles; ++k) {
+      const int q = min(qt0 + k, last);
+      const T* src = dsb + (ds_row(a.causal, q, n_kvt) + min(j, n_j(q) - 1)) * 4096;
+      dma16s(src, soff,
+             __builtin_amdgcn_readfirstlane(lds_addr(st + PK::BYTES + k * PS::BYTES + wave * 1024)));
+    }
+  };
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) v4s lds_v4s;
+  f32x16 acc[MT];
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) acc[mt] = zero16();
+#pragma unroll
+  for (int j = 0; j < kDsStages - 1; ++j)
+    if (j < n_kv) issue(j);
+  for (int j = 0; j < n_kv; ++j) {
+    // tile j landed (the later tiles issued so far stay in flight)
+    if (j + kDsStages - 2 < n_kv) wait_vmcnt<(kDsStages - 2) * PERW>();
+    else wait_vmcnt<0>();
+    lds_barrier();  // ... for every wavefront; tile j - 1's stage is free
+    if (j + kDsStages - 1 < n_kv) issue(j + kDsStages - 1);
+    if (j < my_kv) {
+      const char* st = smem + (j % kDsStages) * STAGE;
+      const auto kbs = ko.tr_base(st);
+      uint32_t sx[2];
+#pragma unroll
+      for (int k = 0; k < 2; ++k) {
+        sx[k] = lds_addr(st + PK::BYTES + sel * PS::BYTES) + so[k];
+        asm("" : "+v"(sx[k]));
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const v4s lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4s*)(uintptr_t)(sx[0] + (uint32_t)(16 * t * PS::RB)));
+        const v4s hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (lds_v4s*)(uintptr_t)(sx[1] + (uint32_t)(16 * t * PS::RB)));
+        const V bs = __builtin_bit_cast(V, __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7));
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = M::mma(ko.rd_tr(kbs, 16 * t, mt), bs, acc[mt]);
+      }
+    }
+  }
+  if (qt <= last) {
+    const int qr = 64 * qt + ds_col_row(32 * mq + l32);
+    if (qr < a.Tq) {
+      T* out = (T*)a.dq + b * a.sdq_b + h * a.sdq_h + (int64_t)qr * a.sdq_s;
+      const float sc = a.scale;
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int d0 = 32 * mt + 8 * rr + 4 * g;
+          store4<T>(out + d0, acc[mt][4 * rr] * sc, acc[mt][4 * rr + 1] * sc,
+                    acc[mt][4 * rr + 2] * sc, acc[mt][4 * rr + 3] * sc);
+        }
       }
     }
   }
@@ -2535,10 +2757,31 @@ int fwd_simt(const FwdArgs& a, int64_t D, hipStream_t st) {
 #define TRI_ATTN_DQ_WAVES 4
 #endif
 
+// Stored-dS path (head_dim 128, no rope): delta, then dK/dV storing dS, then
+// dQ from the stored dS.
+template <typename T, int D>
+int bwd_ds(const BwdArgs& a, hipStream_t st) {
+  BwdArgs x = a;
+  const int64_t rows = (int64_t)a.B * a.H * a.Tq;
+  attn_bwd_delta_v<T, D><<<(unsigned)cdiv(rows, 128), 256, 0, st>>>(x);
+  if (int e = check_launch("attention backward (delta)")) return e;
+  x.n_tiles = (int)cdiv(a.Tkv, kPairBN);
+  const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;
+  attn_bwd_dkdv_pair<T, D, true><<<(unsigned)kv_blocks, 64 * kPairWaves, 0, st>>>(x);
+  if (int e = check_launch("attention backward (dk/dv storing ds, mfma pairs)")) return e;
+  x.n_tiles = (int)cdiv(cdiv(a.Tq, 64), kDsTiles);
+  const int64_t q_blocks = (int64_t)x.n_tiles * a.B * a.H;
+  attn_bwd_dq_ds<T, D><<<(unsigned)q_blocks, 64 * kDsWaves, 0, st>>>(x);
+  return check_launch("attention backward (dq from stored ds)");
+}
+
 // dQ first: it also computes delta, which the dK/dV kernel reads.
 template <typename T, int D>
 int bwd_v2(const BwdArgs& a, hipStream_t st) {
   constexpr int WK = TRI_ATTN_DKDV_WAVES, WQ = TRI_ATTN_DQ_WAVES;
+  if constexpr (D == 128) {
+    if (a.ds != nullptr) return bwd_ds<T, D>(a, st);
+  }
   BwdArgs x = a;
   x.n_tiles = (int)cdiv(a.Tq, 32 * WQ);
   const int64_t q_blocks = (int64_t)x.n_tiles * a.B * a.H;
@@ -2557,7 +2800,7 @@ int bwd_v2(const BwdArgs& a, hipStream_t st) {
   if constexpr (TRI_ATTN_DKDV_PAIR && D == 128) {
     x.n_tiles = (int)cdiv(a.Tkv, kPairBN);
     const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;
-    attn_bwd_dkdv_pair<T, D><<<(unsigned)kv_blocks, 64 * kPairWaves, 0, st>>>(x);
+    attn_bwd_dkdv_pair<T, D, false><<<(unsigned)kv_blocks, 64 * kPairWaves, 0, st>>>(x);
     return check_launch("attention backward (dk/dv, mfma pairs)");
   }
   x.n_tiles = (int)cdiv(a.Tkv, 32 * WK);
@@ -2668,11 +2911,20 @@ int attention_fwd(const void* q, const void* k, const void* v, void* o, float* l
   return TRI_OK;
 }
 
+// Bytes of the stored-dS workspace (0: the shape does not take that path).
+size_t ds_workspace_bytes(int64_t B, int64_t H, int64_t Tq, int64_t Tkv, int64_t D, int causal,
+                          int dtype) {
+  if (dtype == kF32 || D != 128 || B <= 0 || H <= 0 || Tq <= 0 || Tkv <= 0) return 0;
+  if (Tq >= ((int64_t)1 << 30) || Tkv >= ((int64_t)1 << 30)) return 0;
+  const int64_t per_bh = ds_row(causal != 0, (int)cdiv(Tq, 64), (int)cdiv(Tkv, 64)) * 4096;
+  return (size_t)(B * H) * (size_t)per_bh * 2;
+}
+
 int attention_bwd(const void* dout, const void* q, const void* k, const void* v, const void* o,
                   const float* lse, void* dq, void* dk, void* dv, float* delta, int64_t B,
                   int64_t H, int64_t Hkv, int64_t Tq, int64_t Tkv, int64_t D,
                   const int64_t* strides, int causal, int dtype, const RopeQ& rope, void* q_rot,
-                  void* stream) {
+                  void* ds_ws, size_t ds_bytes, void* stream) {
   if (int e = check_dims(B, H, Hkv, Tq, Tkv, D)) return e;
   if (B == 0 || Tq == 0 || Tkv == 0) return TRI_OK;
   BwdArgs a;
@@ -2692,6 +2944,8 @@ int attention_bwd(const void* dout, const void* q, const void* k, const void* v,
   a.scale = (float)(1.0 / sqrt((double)D));
   a.rope = rope;
   a.q_rot = q_rot;
+  a.ds = nullptr;
+  a.ds_bh = 0;
   const bool out_ok = [&] {
     const int64_t* s = strides + 15;
     for (int i = 0; i < 9; ++i)
@@ -2712,6 +2966,16 @@ int attention_bwd(const void* dout, const void* q, const void* k, const void* v,
                   (long long)D);
     if (q_rot == nullptr || !aligned16(q_rot))
       return fail(TRI_EINVAL, "attention backward with rope: q_rot workspace missing or unaligned");
+  }
+  if (ds_ws != nullptr && mfma && rope.cos == nullptr && TRI_ATTN_DKDV_PAIR) {
+    const size_t need = ds_workspace_bytes(B, H, Tq, Tkv, D, causal, dtype);
+    if (need > 0) {
+      if (ds_bytes < need || !aligned16(ds_ws))
+        return fail(TRI_EINVAL, "attention backward: dS workspace of %zu bytes (need %zu, "
+                    "16-byte aligned)", ds_bytes, need);
+      a.ds = ds_ws;
+      a.ds_bh = (int64_t)(need / 2 / (size_t)(B * H));
+    }
   }
   TRI_DISPATCH_FLOAT(dtype, T, return bwd_impl<T>(a, D, mfma, st));
   return TRI_OK;
@@ -2747,7 +3011,24 @@ extern "C" int tritium_attention_bwd(const void* dout, const void* q, const void
                                      const int64_t* strides, int causal, int dtype,
                                      void* stream) {
   return attention_bwd(dout, q, k, v, o, lse, dq, dk, dv, delta, B, H, Hkv, Tq, Tkv, D, strides,
-                       causal, dtype, RopeQ{}, nullptr, stream);
+                       causal, dtype, RopeQ{}, nullptr, nullptr, 0, stream);
+}
+
+extern "C" size_t tritium_attention_bwd_workspace_size(int64_t B, int64_t H, int64_t Tq,
+                                                       int64_t Tkv, int64_t D, int causal,
+                                                       int dtype) {
+  return ds_workspace_bytes(B, H, Tq, Tkv, D, causal, dtype);
+}
+
+extern "C" int tritium_attention_bwd_ws(const void* dout, const void* q, const void* k,
+                                        const void* v, const void* o, const float* lse, void* dq,
+                                        void* dk, void* dv, float* delta, void* workspace,
+                                        size_t workspace_bytes, int64_t B, int64_t H, int64_t Hkv,
+                                        int64_t Tq, int64_t Tkv, int64_t D,
+                                        const int64_t* strides, int causal, int dtype,
+                                        void* stream) {
+  return attention_bwd(dout, q, k, v, o, lse, dq, dk, dv, delta, B, H, Hkv, Tq, Tkv, D, strides,
+                       causal, dtype, RopeQ{}, nullptr, workspace, workspace_bytes, stream);
 }
 
 extern "C" int tritium_attention_fwd_rope(const void* q, const void* k, const void* v, void* o,
@@ -2776,7 +3057,7 @@ extern "C" int tritium_attention_bwd_rope(const void* dout, const void* q, const
   if (int e = rope_tables(cos_table, sin_table, position_ids, position_kind, max_position, r))
     return e;
   return attention_bwd(dout, q, k, v, o, lse, dq, dk, dv, delta, B, H, Hkv, Tq, Tkv, D, strides,
-                       causal, dtype, r, q_rot, stream);
+                       causal, dtype, r, q_rot, nullptr, 0, stream);
 }
 
 extern "C" size_t tritium_attention_decode_workspace_size(int64_t B, int64_t H, int64_t Hkv,

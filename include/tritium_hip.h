@@ -181,6 +181,25 @@ int tritium_attention_bwd(const void* dout, const void* q, const void* k, const 
                           int64_t Tkv, int64_t D, const int64_t* strides, int causal, int dtype,
                           void* stream);
 
+/* Bytes of the dS workspace that tritium_attention_bwd_ws takes for these
+ * arguments, 0 when the shape does not use one (head_dim other than 128,
+ * float32).  It grows with Tq * Tkv: B * H * (causal ? about n(n+1)/2 : n_q n_kv)
+ * 8 KiB chunks, n = Tq / 64 (2.2 GB at B 4, H 32, Tq = Tkv = 4096, causal). */
+size_t tritium_attention_bwd_workspace_size(int64_t B, int64_t H, int64_t Tq, int64_t Tkv,
+                                            int64_t D, int causal, int dtype);
+
+/* tritium_attention_bwd (same reference interface, attention.py:632-702) with
+ * a dS workspace of tritium_attention_bwd_workspace_size bytes (16-byte
+ * aligned; a smaller one is TRI_EINVAL): for head_dim 128 the dK/dV kernel
+ * then stores dS and dQ is formed from it, instead of a dQ kernel that
+ * recomputes S and dP.  Where the size is 0, or the tensors take the SIMT
+ * path, the workspace is not used. */
+int tritium_attention_bwd_ws(const void* dout, const void* q, const void* k, const void* v,
+                             const void* o, const float* lse, void* dq, void* dk, void* dv,
+                             float* delta, void* workspace, size_t workspace_bytes, int64_t B,
+                             int64_t H, int64_t Hkv, int64_t Tq, int64_t Tkv, int64_t D,
+                             const int64_t* strides, int causal, int dtype, void* stream);
+
 /* tritium_attention_fwd with RoPE applied to q as each row is loaded: q holds
  * the unrotated rows, k the rotated ones (tritium_rope_strided with a null q
  * rotates k alone).  No counterpart in the reference, which rotates q and k

@@ -6,6 +6,7 @@ lengths, q_len != kv_len and head_dim 128.  Tolerance: bf16/fp16 max-abs 2e-2
 
 from __future__ import annotations
 
+import importlib
 import numpy as np
 import pytest
 import torch
@@ -131,6 +132,38 @@ def test_attention_gqa_many_tiles_ragged(causal):
     # several kv and query workgroups per head, GQA group of 4, length not a tile multiple
     _check(torch.bfloat16, 1, 8, 2, 700, 700, 128, causal, seed=14)
     _check(torch.float16, 2, 4, 1, 333, 333, 64, causal, seed=15)
+
+
+# head_dim 128 backward: dK/dV store dS and dQ is formed from it (the default
+# where the workspace fits), or the dQ kernel recomputes S and dP (workspace
+# limit 0).  Both against the oracle: ragged tiles, Tq < Tkv and Tq > Tkv
+# (the causal mask is top-left), GQA, a single row.
+DS_SHAPES = [(1, 2, 2, 77, 77), (1, 2, 1, 50, 200), (1, 2, 1, 200, 50), (2, 4, 2, 333, 333),
+             (1, 2, 2, 64, 64), (1, 1, 1, 1, 1), (1, 2, 2, 129, 127), (1, 4, 4, 384, 384)]
+
+
+@pytest.mark.parametrize("stored", [True, False])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize(("b", "h", "hkv", "tq", "tkv"), DS_SHAPES)
+def test_attention_backward_stored_and_recomputed_ds(monkeypatch, stored, causal, b, h, hkv, tq,
+                                                     tkv):
+    A = importlib.import_module("helion_amd.attention")
+    if not stored:
+        monkeypatch.setattr(A, "DS_WORKSPACE_MAX_BYTES", 0)
+    _check(torch.bfloat16, b, h, hkv, tq, tkv, 128, causal, seed=31 + tq + tkv)
+
+
+def test_attention_stored_ds_deterministic_fp16():
+    q = randn((2, 4, 300, 128), torch.float16, 1).requires_grad_(True)
+    k = randn((2, 2, 300, 128), torch.float16, 2).requires_grad_(True)
+    v = randn((2, 2, 300, 128), torch.float16, 3).requires_grad_(True)
+    grads = []
+    for _ in range(2):
+        q.grad = k.grad = v.grad = None
+        tritium.attention(q, k, v).sum().backward()
+        grads.append((q.grad.clone(), k.grad.clone(), v.grad.clone()))
+    for a, b in zip(*grads):
+        assert torch.equal(a, b)
 
 
 def test_attention_invariants():

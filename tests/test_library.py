@@ -45,3 +45,25 @@ def test_argument_errors_come_back_as_messages():
     assert b"head_dim" in handle.tritium_last_error()
     with pytest.raises(RuntimeError, match="unsupported dtype"):
         L.call("tritium_swiglu_fwd", None, None, None, 16, 7, None)
+
+
+@pytest.mark.skipif(not os.path.exists(L.LIB_PATH), reason="library not built")
+def test_attention_bwd_workspace_size_and_rejection():
+    handle = L.lib()
+    size = handle.tritium_attention_bwd_workspace_size
+    # causal: query tile i sees min(i + 1, n_kv) 64 x 64 chunks of 2-byte dS
+    bf16, f16, f32 = 2, 1, 0
+    assert size(4, 32, 4096, 4096, 128, 1, bf16) == 4 * 32 * (64 * 65 // 2) * 8192
+    assert size(1, 2, 200, 50, 128, 1, bf16) == 2 * (1 + 1 + 1 + 1) * 8192
+    assert size(1, 2, 50, 200, 128, 1, bf16) == 2 * 1 * 8192
+    assert size(1, 2, 129, 127, 128, 0, f16) == 2 * 3 * 2 * 8192
+    assert size(1, 2, 128, 128, 64, 1, bf16) == 0   # head_dim 64: no stored dS
+    assert size(1, 2, 128, 128, 128, 1, f32) == 0
+    # an undersized workspace is rejected before any device work
+    strides = (ctypes.c_int64 * 24)(*([128] * 24))
+    p = ctypes.c_void_p(1 << 20)
+    rc = handle.tritium_attention_bwd_ws(p, p, p, p, p, p, p, p, p, p, p, 8192, 1, 2, 2, 128, 128,
+                                         128, strides, 1, bf16, None)
+    assert rc == 1
+    assert b"dS workspace" in handle.tritium_last_error()
+
