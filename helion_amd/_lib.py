@@ -97,6 +97,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _P,
          _I32, _I32, _P, _P, _P, _I32, _I64, _P],
     ),
+    "tritium_attention_bwd_rope_ws": (
+        _I32,
+        [_P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _SZ, _I64, _I64, _I64, _I64, _I64, _I64,
+         _P, _I32, _I32, _P, _P, _P, _I32, _I64, _P],
+    ),
     "tritium_attention_decode_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64]),
     "tritium_attention_decode": (
         _I32,

@@ -173,6 +173,16 @@ def _attention_forward(q, k, v, is_causal: bool):
     return o, lse
 
 
+def _ds_workspace(q, batch, n_heads, q_len, kv_len, head_dim, is_causal):
+    """The dS workspace of the backward (tensor, bytes), or (None, 0) where the
+    shape takes none or it would exceed DS_WORKSPACE_MAX_BYTES."""
+    n = _lib.lib().tritium_attention_bwd_workspace_size(
+        batch, n_heads, q_len, kv_len, head_dim, int(bool(is_causal)), _lib.dtype_code(q.dtype))
+    if not 0 < n <= DS_WORKSPACE_MAX_BYTES:
+        return None, 0
+    return torch.empty((n,), device=q.device, dtype=torch.uint8), n
+
+
 def _attention_backward_impl(do, q, k, v, o, lse, is_causal: bool):
     """attention.py:632-702, with correct strided outputs and no atomics."""
     batch, n_heads, n_kv_heads, q_len, kv_len, head_dim = _check_attention_inputs(q, k, v)
@@ -184,12 +194,7 @@ def _attention_backward_impl(do, q, k, v, o, lse, is_causal: bool):
         return dq.zero_(), dk.zero_(), dv.zero_()
     delta = torch.empty((batch * n_heads * q_len,), device=q.device, dtype=torch.float32)
     strides = _strides(q, k, v, o, do, dq, dk, dv)
-    code = _lib.dtype_code(q.dtype)
-    ws_bytes = _lib.lib().tritium_attention_bwd_workspace_size(
-        batch, n_heads, q_len, kv_len, head_dim, int(bool(is_causal)), code)
-    if not 0 < ws_bytes <= DS_WORKSPACE_MAX_BYTES:
-        ws_bytes = 0
-    ws = torch.empty((ws_bytes,), device=q.device, dtype=torch.uint8) if ws_bytes else None
+    ws, ws_bytes = _ds_workspace(q, batch, n_heads, q_len, kv_len, head_dim, is_causal)
     _lib.call(
         "tritium_attention_bwd_ws",
         do.data_ptr(),
@@ -342,10 +347,12 @@ def attention_rope_bwd(do, q, k, v, o, lse, cos, sin, position_ids, is_causal: b
     delta = torch.empty((batch * n_heads * q_len,), device=q.device, dtype=torch.float32)
     q_rot = torch.empty((batch, n_heads, q_len, head_dim), device=q.device, dtype=q.dtype)
     pos_ptr, kind = _pos_args(position_ids)
-    _lib.call("tritium_attention_bwd_rope", do.data_ptr(), q.data_ptr(), k.data_ptr(),
+    ws, ws_bytes = _ds_workspace(q, batch, n_heads, q_len, kv_len, head_dim, is_causal)
+    _lib.call("tritium_attention_bwd_rope_ws", do.data_ptr(), q.data_ptr(), k.data_ptr(),
               v.data_ptr(), o.data_ptr(), lse.data_ptr(), dq.data_ptr(), dk.data_ptr(),
-              dv.data_ptr(), delta.data_ptr(), q_rot.data_ptr(), batch, n_heads, n_kv_heads,
-              q_len, kv_len, head_dim, _strides(q, k, v, o, do, dq, dk, dv),
+              dv.data_ptr(), delta.data_ptr(), q_rot.data_ptr(),
+              ws.data_ptr() if ws is not None else None, ws_bytes, batch, n_heads,
+              n_kv_heads, q_len, kv_len, head_dim, _strides(q, k, v, o, do, dq, dk, dv),
               int(bool(is_causal)), _lib.dtype_code(q.dtype), cos.data_ptr(), sin.data_ptr(),
               pos_ptr, kind, cos.shape[0], _lib.stream_of(q))
     return dq, dk, dv

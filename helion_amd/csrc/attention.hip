@@ -1953,6 +1953,55 @@ attn_bwd_dkdv_pair(BwdArgs a) {
   }
 }
 
+// dQ of one query row from its MFMA accumulators (element d = 32 mt + 8 rr +
+// 4 g + j at dq[mt][4 rr + j]): scaled, with RoPE the inverse rotation (the
+// gradient of the unrotated q; d pairs with d + D/2 in dq[mt + MT/2]; NaN for
+// a position outside the tables), rounded once and stored.
+template <typename T, int D>
+__device__ __forceinline__ void store_dq_row(f32x16 (&dq)[D / 32], T* dqr, float sc,
+                                             const RopeQ& rp, bool rope, int64_t rpos,
+                                             bool rpos_ok, int g) {
+  constexpr int MT = D / 32;
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) dq[mt][r] *= sc;
+  if (rope) {
+    const float nan = __builtin_nanf("");
+#pragma unroll
+    for (int mt = 0; mt < MT / 2; ++mt) {
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const int d0 = 32 * mt + 8 * rr + 4 * g;
+        float c[4] = {}, s[4] = {};
+        if (rpos_ok) {
+#pragma unroll
+          for (int j = 0; j < 4; ++j) {
+            c[j] = rp.cos[rpos * (D / 2) + d0 + j];
+            s[j] = rp.sin[rpos * (D / 2) + d0 + j];
+          }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          float oa, ob;
+          rope_pair(dq[mt][4 * rr + j], dq[mt + MT / 2][4 * rr + j], c[j], -s[j], oa, ob);
+          dq[mt][4 * rr + j] = rpos_ok ? oa : nan;
+          dq[mt + MT / 2][4 * rr + j] = rpos_ok ? ob : nan;
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int mt = 0; mt < MT; ++mt) {
+#pragma unroll
+    for (int rr = 0; rr < 4; ++rr) {
+      const int d0 = 32 * mt + 8 * rr + 4 * g;
+      store4<T>(dqr + d0, dq[mt][4 * rr], dq[mt][4 * rr + 1], dq[mt][4 * rr + 2],
+                dq[mt][4 * rr + 3]);
+    }
+  }
+}
+
 // dQ: a workgroup owns 32 * WAVES query rows of one (batch, head), a
 // wavefront 32 of them (Q, dO fragments in registers, lane = query row),
 // and sweeps the 64-row K/V tiles it can see: S^T = K Q^T and
@@ -2074,50 +2123,9 @@ attn_bwd_dq_v2(BwdArgs a) {
     }
   }
 
-  if (qvalid) {
-    T* dqr = (T*)a.dq + b * a.sdq_b + h * a.sdq_h + (int64_t)qrow * a.sdq_s;
-    const float sc = a.scale;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) dq[mt][r] *= sc;
-    if (rope) {
-      // the gradient of the unrotated q: the inverse rotation of dq, element
-      // d = 32 mt + 8 rr + 4 g + j pairing with d + D/2 in dq[mt + MT/2]
-      const float nan = __builtin_nanf("");
-#pragma unroll
-      for (int mt = 0; mt < MT / 2; ++mt) {
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int d0 = 32 * mt + 8 * rr + 4 * g;
-          float c[4] = {}, s[4] = {};
-          if (rpos_ok) {
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-              c[j] = a.rope.cos[rpos * (D / 2) + d0 + j];
-              s[j] = a.rope.sin[rpos * (D / 2) + d0 + j];
-            }
-          }
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            float oa, ob;
-            rope_pair(dq[mt][4 * rr + j], dq[mt + MT / 2][4 * rr + j], c[j], -s[j], oa, ob);
-            dq[mt][4 * rr + j] = rpos_ok ? oa : nan;
-            dq[mt + MT / 2][4 * rr + j] = rpos_ok ? ob : nan;
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const int d0 = 32 * mt + 8 * rr + 4 * g;
-        store4<T>(dqr + d0, dq[mt][4 * rr], dq[mt][4 * rr + 1], dq[mt][4 * rr + 2],
-                  dq[mt][4 * rr + 3]);
-      }
-    }
-  }
+  if (qvalid)
+    store_dq_row<T, D>(dq, (T*)a.dq + b * a.sdq_b + h * a.sdq_h + (int64_t)qrow * a.sdq_s, a.scale,
+                       a.rope, rope, rpos, rpos_ok, g);
 }
 
 // --------------------------------------------- backward: stored-dS path --
@@ -2130,7 +2138,8 @@ attn_bwd_dq_v2(BwdArgs a) {
 
 // delta[bh][q] = sum_d dO[q][d] * O[q][d] (fp32), summed as the recomputing
 // dQ kernel sums it (two lanes a row, each over alternate 8-column granules
-// in column order, then their sum), so both paths give dK, dV bitwise alike.
+// in column order, then their sum); with RoPE also the rotated q rows
+// (q_rot, [B, H, Tq, D]) that the dK/dV kernel reads, as that kernel writes them.
 template <typename T, int D>
 __global__ void __launch_bounds__(256)
 attn_bwd_delta_v(BwdArgs a) {
@@ -2151,6 +2160,18 @@ attn_bwd_delta_v(BwdArgs a) {
       const auto of = ld8(orow + 16 * s + 8 * g);
 #pragma unroll
       for (int j = 0; j < 8; ++j) dl += (float)df[j] * (float)of[j];
+    }
+    if (a.rope.cos != nullptr) {  // the rotated q rows for the dK/dV kernel
+      typename Mfma<T>::V qf[KS];
+      const T* qrow = (const T*)a.q + b * a.sq_b + h * a.sq_h + (int64_t)q * a.sq_s;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) qf[s] = ld8(qrow + 16 * s + 8 * g);
+      int64_t pos = 0;
+      const bool ok = rope_position(a.rope, b, a.Tq, q, pos);
+      rope_q_frag<T, D>(qf, a.rope, pos, ok, g);
+      T* qr = (T*)a.q_rot + row * D;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) *reinterpret_cast<typename Mfma<T>::V*>(qr + 16 * s + 8 * g) = qf[s];
     }
   }
   dl += __shfl_xor(dl, 32, 64);
@@ -2272,17 +2293,11 @@ attn_bwd_dq_ds(BwdArgs a) {
   if (qt <= last) {
     const int qr = 64 * qt + ds_col_row(32 * mq + l32);
     if (qr < a.Tq) {
-      T* out = (T*)a.dq + b * a.sdq_b + h * a.sdq_h + (int64_t)qr * a.sdq_s;
-      const float sc = a.scale;
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int d0 = 32 * mt + 8 * rr + 4 * g;
-          store4<T>(out + d0, acc[mt][4 * rr] * sc, acc[mt][4 * rr + 1] * sc,
-                    acc[mt][4 * rr + 2] * sc, acc[mt][4 * rr + 3] * sc);
-        }
-      }
+      const bool rope = a.rope.cos != nullptr;
+      int64_t rpos = 0;
+      const bool rpos_ok = rope && rope_position(a.rope, b, a.Tq, qr, rpos);
+      store_dq_row<T, D>(acc, (T*)a.dq + b * a.sdq_b + h * a.sdq_h + (int64_t)qr * a.sdq_s,
+                         a.scale, a.rope, rope, rpos, rpos_ok, g);
     }
   }
 }
@@ -2757,18 +2772,31 @@ int fwd_simt(const FwdArgs& a, int64_t D, hipStream_t st) {
 #define TRI_ATTN_DQ_WAVES 4
 #endif
 
-// Stored-dS path (head_dim 128, no rope): delta, then dK/dV storing dS, then
-// dQ from the stored dS.
+// Stored-dS path (head_dim 128): delta (and with RoPE the rotated q), then
+// dK/dV storing dS, then dQ from the stored dS.  (At head_dim 64 the
+// recompute costs half as much and the stored path measured slower: GPT
+// config-5 layer 0.319 against 0.297 ms.)
 template <typename T, int D>
 int bwd_ds(const BwdArgs& a, hipStream_t st) {
   BwdArgs x = a;
   const int64_t rows = (int64_t)a.B * a.H * a.Tq;
   attn_bwd_delta_v<T, D><<<(unsigned)cdiv(rows, 128), 256, 0, st>>>(x);
   if (int e = check_launch("attention backward (delta)")) return e;
+  if (a.rope.cos != nullptr) {  // dK/dV take the rotated q
+    x.q = a.q_rot;
+    x.sq_s = D;
+    x.sq_h = (int64_t)a.Tq * D;
+    x.sq_b = (int64_t)a.H * a.Tq * D;
+  }
+  static_assert(D == 128, "stored-dS backward: head_dim 128");
   x.n_tiles = (int)cdiv(a.Tkv, kPairBN);
   const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;
   attn_bwd_dkdv_pair<T, D, true><<<(unsigned)kv_blocks, 64 * kPairWaves, 0, st>>>(x);
-  if (int e = check_launch("attention backward (dk/dv storing ds, mfma pairs)")) return e;
+  if (int e = check_launch("attention backward (dk/dv storing ds)")) return e;
+  x.q = a.q;  // dQ from dS reads K and dS only; the row strides of q stay the caller's
+  x.sq_s = a.sq_s;
+  x.sq_h = a.sq_h;
+  x.sq_b = a.sq_b;
   x.n_tiles = (int)cdiv(cdiv(a.Tq, 64), kDsTiles);
   const int64_t q_blocks = (int64_t)x.n_tiles * a.B * a.H;
   attn_bwd_dq_ds<T, D><<<(unsigned)q_blocks, 64 * kDsWaves, 0, st>>>(x);
@@ -2967,7 +2995,7 @@ int attention_bwd(const void* dout, const void* q, const void* k, const void* v,
     if (q_rot == nullptr || !aligned16(q_rot))
       return fail(TRI_EINVAL, "attention backward with rope: q_rot workspace missing or unaligned");
   }
-  if (ds_ws != nullptr && mfma && rope.cos == nullptr && TRI_ATTN_DKDV_PAIR) {
+  if (ds_ws != nullptr && mfma && TRI_ATTN_DKDV_PAIR) {
     const size_t need = ds_workspace_bytes(B, H, Tq, Tkv, D, causal, dtype);
     if (need > 0) {
       if (ds_bytes < need || !aligned16(ds_ws))
@@ -3058,6 +3086,20 @@ extern "C" int tritium_attention_bwd_rope(const void* dout, const void* q, const
     return e;
   return attention_bwd(dout, q, k, v, o, lse, dq, dk, dv, delta, B, H, Hkv, Tq, Tkv, D, strides,
                        causal, dtype, r, q_rot, nullptr, 0, stream);
+}
+
+extern "C" int tritium_attention_bwd_rope_ws(
+    const void* dout, const void* q, const void* k, const void* v, const void* o,
+    const float* lse, void* dq, void* dk, void* dv, float* delta, void* q_rot, void* workspace,
+    size_t workspace_bytes, int64_t B, int64_t H, int64_t Hkv, int64_t Tq, int64_t Tkv, int64_t D,
+    const int64_t* strides, int causal, int dtype, const float* cos_table,
+    const float* sin_table, const void* position_ids, int position_kind, int64_t max_position,
+    void* stream) {
+  RopeQ r{};
+  if (int e = rope_tables(cos_table, sin_table, position_ids, position_kind, max_position, r))
+    return e;
+  return attention_bwd(dout, q, k, v, o, lse, dq, dk, dv, delta, B, H, Hkv, Tq, Tkv, D, strides,
+                       causal, dtype, r, q_rot, workspace, workspace_bytes, stream);
 }
 
 extern "C" size_t tritium_attention_decode_workspace_size(int64_t B, int64_t H, int64_t Hkv,

@@ -181,10 +181,11 @@ int tritium_attention_bwd(const void* dout, const void* q, const void* k, const 
                           int64_t Tkv, int64_t D, const int64_t* strides, int causal, int dtype,
                           void* stream);
 
-/* Bytes of the dS workspace that tritium_attention_bwd_ws takes for these
- * arguments, 0 when the shape does not use one (head_dim other than 128,
- * float32).  It grows with Tq * Tkv: B * H * (causal ? about n(n+1)/2 : n_q n_kv)
- * 8 KiB chunks, n = Tq / 64 (2.2 GB at B 4, H 32, Tq = Tkv = 4096, causal). */
+/* Bytes of the dS workspace that tritium_attention_bwd_ws (and _bwd_rope_ws)
+ * take for these arguments, 0 when the shape does not use one (head_dim other
+ * than 128, float32).  It grows with Tq * Tkv: B * H * (causal ? about
+ * n(n+1)/2 : n_q n_kv) 8 KiB chunks, n = Tq / 64 (2.2 GB at B 4, H 32,
+ * Tq = Tkv = 4096, causal). */
 size_t tritium_attention_bwd_workspace_size(int64_t B, int64_t H, int64_t Tq, int64_t Tkv,
                                             int64_t D, int causal, int dtype);
 
@@ -230,6 +231,19 @@ int tritium_attention_bwd_rope(const void* dout, const void* q, const void* k, c
                                int causal, int dtype, const float* cos_table,
                                const float* sin_table, const void* position_ids,
                                int position_kind, int64_t max_position, void* stream);
+
+/* tritium_attention_bwd_rope with the dS workspace of tritium_attention_bwd_ws
+ * (no counterpart in the reference, as tritium_attention_fwd_rope): the
+ * rotated q for the dK/dV kernel is then written by the kernel that computes
+ * delta, and the dQ kernel applies the inverse rotation as it stores. */
+int tritium_attention_bwd_rope_ws(const void* dout, const void* q, const void* k, const void* v,
+                                  const void* o, const float* lse, void* dq, void* dk, void* dv,
+                                  float* delta, void* q_rot, void* workspace,
+                                  size_t workspace_bytes, int64_t B, int64_t H, int64_t Hkv,
+                                  int64_t Tq, int64_t Tkv, int64_t D, const int64_t* strides,
+                                  int causal, int dtype, const float* cos_table,
+                                  const float* sin_table, const void* position_ids,
+                                  int position_kind, int64_t max_position, void* stream);
 
 /* The attention forward for one query row per (batch, head) against a K/V
  * cache (the reference's decode branch, attention.py:144-217, 354-396:

@@ -142,15 +142,16 @@ DS_SHAPES = [(1, 2, 2, 77, 77), (1, 2, 1, 50, 200), (1, 2, 1, 200, 50), (2, 4, 2
              (1, 2, 2, 64, 64), (1, 1, 1, 1, 1), (1, 2, 2, 129, 127), (1, 4, 4, 384, 384)]
 
 
+@pytest.mark.parametrize("head_dim", [128])
 @pytest.mark.parametrize("stored", [True, False])
 @pytest.mark.parametrize("causal", [False, True])
 @pytest.mark.parametrize(("b", "h", "hkv", "tq", "tkv"), DS_SHAPES)
 def test_attention_backward_stored_and_recomputed_ds(monkeypatch, stored, causal, b, h, hkv, tq,
-                                                     tkv):
+                                                     tkv, head_dim):
     A = importlib.import_module("helion_amd.attention")
     if not stored:
         monkeypatch.setattr(A, "DS_WORKSPACE_MAX_BYTES", 0)
-    _check(torch.bfloat16, b, h, hkv, tq, tkv, 128, causal, seed=31 + tq + tkv)
+    _check(torch.bfloat16, b, h, hkv, tq, tkv, head_dim, causal, seed=31 + tq + tkv)
 
 
 def test_attention_stored_ds_deterministic_fp16():

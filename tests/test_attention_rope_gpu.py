@@ -2,9 +2,8 @@
 tritium_attention_fwd_rope / tritium_attention_bwd_rope) against the
 reference's sequence -- rope on q and k, then attention (helion/nn.py:196-220)
 -- run two ways: this library's rope kernel followed by its attention (the
-forward and dK/dV must match bitwise, since the rotation rounds alike; the
-composition's backward is held to the same recomputing-dQ kernels, as the
-head_dim-128 stored-dS backward forms delta with other instructions), and
+forward and dK/dV must match bitwise, since the rotation rounds alike; both
+take the stored-dS backward, or both the recomputing one), and
 the float64 oracle (oracle.rope, then oracle.attention; dq through the
 inverse rotation).  Tolerance as the attention tests: max-abs 2e-2 + 2e-2
 relative for 16-bit."""
@@ -75,12 +74,7 @@ def _run(dtype, b, h, hkv, t, d, kind, seed=0, oracle_check=True):
     q_rot = _rope_tokens(q, cos, sin, pos_arg)
     qc, kc, vc = (x.detach().requires_grad_(True) for x in (q_rot, k_rot, v))
     oc = tritium.attention(qc, kc, vc, is_causal=True)
-    A = importlib.import_module("helion_amd.attention")
-    limit, A.DS_WORKSPACE_MAX_BYTES = A.DS_WORKSPACE_MAX_BYTES, 0
-    try:
-        oc.backward(do)
-    finally:
-        A.DS_WORKSPACE_MAX_BYTES = limit
+    oc.backward(do)
     assert torch.equal(o, oc), "forward differs from rope + attention"
     assert torch.equal(ks.grad, kc.grad) and torch.equal(vs.grad, vc.grad), "dk/dv differ"
     # dq: the fused path un-rotates fp32 accumulators and rounds once; the composition
@@ -107,15 +101,24 @@ def _run(dtype, b, h, hkv, t, d, kind, seed=0, oracle_check=True):
     assert_close(vs.grad, edv, TOL, TOL, "dv")
 
 
+@pytest.mark.parametrize("stored", [True, False])
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("head_dim", [64, 128])
 @pytest.mark.parametrize("pos_kind", [0, 1, 2])
-def test_attention_rope_q_matches_rope_then_attention(dtype, head_dim, pos_kind):
+def test_attention_rope_q_matches_rope_then_attention(monkeypatch, dtype, head_dim, pos_kind,
+                                                      stored):
+    if not stored:  # the recomputing backward (no dS workspace)
+        monkeypatch.setattr(importlib.import_module("helion_amd.attention"),
+                            "DS_WORKSPACE_MAX_BYTES", 0)
     _run(dtype, 2, 4, 4, 130, head_dim, pos_kind, seed=head_dim + pos_kind)
 
 
+@pytest.mark.parametrize("stored", [True, False])
 @pytest.mark.parametrize("head_dim", [64, 128])
-def test_attention_rope_q_grouped_query_ragged(head_dim):
+def test_attention_rope_q_grouped_query_ragged(monkeypatch, head_dim, stored):
+    if not stored:
+        monkeypatch.setattr(importlib.import_module("helion_amd.attention"),
+                            "DS_WORKSPACE_MAX_BYTES", 0)
     _run(torch.bfloat16, 1, 8, 2, 77, head_dim, 2, seed=3)
 
 
