@@ -27,8 +27,11 @@
 // 1024 / RB rows; each lane picks which 16-byte granule it fetches so that the rows
 // land XOR-swizzled (granule c of row r at slot c ^ swz_key(r)), and the MFMA
 // fragment reads of consecutive rows hit distinct 16-byte bank groups.
-// One barrier per K tile: at step kt the wave waits for tile kt, syncs, issues
-// tile kt + STAGES - 1 into the buffer read at step kt - 1, then computes.
+// One barrier per K tile.  16-bit types run the cross-tile loop (xt_loop):
+// the barrier that publishes tile kt + 1 sits before the MFMAs of tile kt's
+// last 16-deep step and tile kt + 1's first fragments are read under them;
+// the other loops wait for tile kt, sync, issue tile kt + STAGES - 1 into
+// the buffer read at step kt - 1, then compute.
 // Rows past M (N) re-read the last valid row (their results are never
 // stored); a partial last K tile is zero-filled through registers and done
 // first, so the pipelined loop has no bounds checks.
@@ -603,6 +606,101 @@ __device__ __forceinline__ void planned_loop(const DmaPlan<C, T, TA, TB>& plan, 
 #define TRI_GEMM_PLAN 1
 #endif
 
+// Cross-tile pipelined 2-stage loop.  The loop above starts every K tile
+// with barrier -> step-0 fragment reads -> MFMAs, so all eight wavefronts
+// wait out one LDS read latency per tile with the MFMA pipe empty.  Here the
+// barrier that publishes tile kt + 1 sits before the MFMAs of tile kt's
+// last 16-deep step, and tile kt + 1's step-0 fragments are read under
+// those MFMAs.  Every wavefront has finished reading tile kt's stage when it
+// passes that barrier (its last reads were issued a step earlier and
+// lds_barrier waits for them), so the first TRI_GEMM_XT_EARLY of its DMAs of
+// tile kt + 2 go into that stage right after the last step's MFMAs, and the
+// rest after the next tile's first step: the last DMAs of a tile then have
+// two steps of MFMAs to land behind before the barrier waits for them, as in
+// the loop above.
+#ifndef TRI_GEMM_XTILE
+#define TRI_GEMM_XTILE 1
+#endif
+#ifndef TRI_GEMM_XT_EARLY
+#define TRI_GEMM_XT_EARLY -1  // -1: half of each wavefront's DMAs
+#endif
+template <class C>
+constexpr int xt_early() {
+  return TRI_GEMM_XT_EARLY < 0 ? C::DMA_PER_WAVE / 2
+         : (TRI_GEMM_XT_EARLY > C::DMA_PER_WAVE ? C::DMA_PER_WAVE : TRI_GEMM_XT_EARLY);
+}
+
+template <class C, bool TA, bool TB, class V>
+__device__ __forceinline__ void read_step(const char* stage, int wm, int wn, int S, V (&a)[C::MT],
+                                          V (&b)[C::NT]) {
+  const char* As = stage;
+  const char* Bs = stage + C::BM * C::RB;
+#pragma unroll
+  for (int i = 0; i < C::MT; ++i) a[i] = frag_a<C, TA, V>(As, wm, i, S);
+#pragma unroll
+  for (int j = 0; j < C::NT; ++j) b[j] = frag_b<C, TB, V>(Bs, wn, j, S);
+}
+
+// 16-deep step S (and the ones after it) of K tile kt, held in stage `cur`.
+// NEXT: tile kt + 1 exists (published by the barrier before the last step,
+// its step-0 fragments read under the last step's MFMAs, its remaining DMAs
+// issued after step 0); NEXT2: tile kt + 2 exists (its first DMAs follow
+// the last step's MFMAs, into stage `cur`).  Compile-time flags: a run-time
+// branch around the barrier makes the compiler merge the LDS counters of
+// both paths and wait for the next tile's reads before the last MFMAs.
+template <class C, typename T, bool TA, bool TB, bool NEXT, bool NEXT2, int S = 0, class V>
+__device__ __forceinline__ void xt_tile(const DmaPlan<C, T, TA, TB>& plan, char* smem, int cur,
+                                        int64_t kt, Acc<C>& acc, int wm, int wn,
+                                        V (&a)[2][C::MT], V (&b)[2][C::NT]) {
+  constexpr int KS = C::RB / 32;
+  constexpr int H = xt_early<C>();
+  static_assert(KS % 2 == 0, "the next tile's step 0 lands in fragment buffer 0");
+  if constexpr (S < KS) {
+    if constexpr (S + 1 < KS) {
+      read_step<C, TA, TB>(smem + cur * C::STAGE_BYTES, wm, wn, S + 1, a[(S + 1) & 1],
+                           b[(S + 1) & 1]);
+    } else if constexpr (NEXT) {
+      wait_vmcnt<0>();
+      lds_barrier();
+      read_step<C, TA, TB>(smem + (cur ^ 1) * C::STAGE_BYTES, wm, wn, 0, a[0], b[0]);
+    }
+    fence();
+#pragma unroll
+    for (int i = 0; i < C::MT; ++i)
+#pragma unroll
+      for (int j = 0; j < C::NT; ++j) acc.t[i][j] = mma(a[S & 1][i], b[S & 1][j], acc.t[i][j]);
+    if constexpr (S == 0 && NEXT) plan.template issue_range<H, C::DMA_PER_WAVE>(cur ^ 1, kt + 1);
+    if constexpr (S + 1 == KS && NEXT2) plan.template issue_range<0, H>(cur, kt + 2);
+    fence();
+    xt_tile<C, T, TA, TB, NEXT, NEXT2, S + 1>(plan, smem, cur, kt, acc, wm, wn, a, b);
+  }
+}
+
+// The cross-tile loop over nfull >= 1 full K tiles (the caller tests for
+// none: an early return in here kept extra copies of the accumulators alive
+// and spilled them).
+template <class C, typename T, bool TA, bool TB>
+__device__ __forceinline__ void xt_loop(const DmaPlan<C, T, TA, TB>& plan, char* smem,
+                                        Acc<C>& acc, int wm, int wn, int64_t nfull) {
+  typedef typename FragOf<T>::V V;
+  constexpr int H = xt_early<C>();
+  V a[2][C::MT], b[2][C::NT];
+  plan.template issue_range<0, C::DMA_PER_WAVE>(0, 0);
+  wait_vmcnt<0>();
+  lds_barrier();
+  read_step<C, TA, TB>(smem, wm, wn, 0, a[0], b[0]);
+  if (nfull > 1) plan.template issue_range<0, H>(1, 1);
+  fence();
+  int64_t kt = 0;
+  for (; kt + 2 < nfull; ++kt)
+    xt_tile<C, T, TA, TB, true, true>(plan, smem, (int)(kt & 1), kt, acc, wm, wn, a, b);
+  if (kt + 1 < nfull) {
+    xt_tile<C, T, TA, TB, true, false>(plan, smem, (int)(kt & 1), kt, acc, wm, wn, a, b);
+    ++kt;
+  }
+  xt_tile<C, T, TA, TB, false, false>(plan, smem, (int)(kt & 1), kt, acc, wm, wn, a, b);
+}
+
 // Accumulate the (tm, tn) tile of A * B^T over all of K (A, B in the
 // layouts TA, TB select).  `smem` holds C::SMEM_BYTES of LDS (1 KiB aligned).
 template <class C, typename T, bool TA = false, bool TB = false>
@@ -648,6 +746,10 @@ __device__ __forceinline__ void mainloop(const Problem& p, int tm, int tn, char*
       __syncthreads();
       compute_tile<C, T>(smem + (int)((nfull - 1) & 1) * C::STAGE_BYTES, acc, wm, wn);
     }
+  } else if constexpr (C::STAGES == 2 && TRI_GEMM_PLAN && TRI_GEMM_XTILE && sizeof(T) == 2) {
+    DmaPlan<C, T, TA, TB> plan;
+    plan.init(p, m0, n0, smem);
+    if (nfull > 0) xt_loop<C, T, TA, TB>(plan, smem, acc, wm, wn, nfull);
   } else if constexpr (C::STAGES == 2 && TRI_GEMM_PLAN) {
     // branch-free steady state: wait for tile kt, sync, prefetch tile kt + 1
     // into the buffer read at step kt - 1, compute tile kt
