@@ -318,10 +318,82 @@ dw_finish_kernel(const A* __restrict__ sums, int64_t n_groups, int hidden, T* __
   dw[col] = from_f32<T>((float)s);
 }
 
-// Two-level column sum of n_part partial rows into dw; `sums` holds
-// cdiv(n_part, kDwGroup) rows.
+// Column sums of the partial rows in one launch (hidden a multiple of the
+// 16-byte vector): block b owns kDwCols columns; thread t takes the 16-byte
+// column group t % kDwCg of rows s, s + kDwSlices, s + 2 kDwSlices, ...
+// (s = t / kDwCg, rows added in increasing order, eight loads in flight),
+// and the kDwSlices slice sums of each column are added through LDS in two
+// fixed-order levels (16 slices, then the 4 group sums).  The order depends
+// on n_part and hidden only, so dweight is deterministic.  Replaces two
+// launches (group sums, then their sum) whose launch and tail time was most
+// of the reduction's 9 us at 512 partial rows.
+#ifndef TRI_RMS_DW_ONE
+#define TRI_RMS_DW_ONE 1
+#endif
+constexpr int kDwCg = 4;                  // 16-byte column groups per block
+constexpr int kDwSlices = 256 / kDwCg;    // row slices (64)
+
+template <typename T, typename A>
+__global__ void __launch_bounds__(256)
+dw_reduce_kernel(const A* __restrict__ partial, int64_t n_part, int hidden, T* __restrict__ dw) {
+  constexpr int VA = 16 / (int)sizeof(A);
+  constexpr int COLS = kDwCg * VA;
+  constexpr int U = 8;
+  __shared__ A red[kDwSlices][COLS];
+  __shared__ A red2[4][COLS];
+  const int cg = threadIdx.x % kDwCg, s = threadIdx.x / kDwCg;
+  const int c0 = blockIdx.x * COLS + cg * VA;
+  A acc[VA];
+#pragma unroll
+  for (int i = 0; i < VA; ++i) acc[i] = 0;
+  if (c0 < hidden) {
+    int64_t p = s;
+    for (; p + (U - 1) * kDwSlices < n_part; p += U * kDwSlices) {
+      Pack<A, VA> v[U];
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+        v[u] = *reinterpret_cast<const Pack<A, VA>*>(partial + (p + u * kDwSlices) * hidden + c0);
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int i = 0; i < VA; ++i) acc[i] += v[u].v[i];
+    }
+    for (; p < n_part; p += kDwSlices) {
+      const Pack<A, VA> v = *reinterpret_cast<const Pack<A, VA>*>(partial + p * hidden + c0);
+#pragma unroll
+      for (int i = 0; i < VA; ++i) acc[i] += v.v[i];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < VA; ++i) red[s][cg * VA + i] = acc[i];
+  __syncthreads();
+  if (threadIdx.x < 4 * COLS) {
+    const int col = threadIdx.x % COLS, q = threadIdx.x / COLS;
+    A t = 0;
+#pragma unroll
+    for (int k = 0; k < kDwSlices / 4; ++k) t += red[q * (kDwSlices / 4) + k][col];
+    red2[q][col] = t;
+  }
+  __syncthreads();
+  if (threadIdx.x < COLS) {
+    const int col = blockIdx.x * COLS + threadIdx.x;
+    const A t = (red2[0][threadIdx.x] + red2[1][threadIdx.x]) +
+                (red2[2][threadIdx.x] + red2[3][threadIdx.x]);
+    if (col < hidden) dw[col] = from_f32<T>((float)t);
+  }
+}
+
+// Column sum of n_part partial rows into dw: one launch when hidden is a
+// multiple of the 16-byte vector, else two levels through `sums`
+// (cdiv(n_part, kDwGroup) rows).
 template <typename T, typename A>
 int dw_reduce(const A* partial, int64_t n_part, int hidden, A* sums, T* dw, hipStream_t stream) {
+  constexpr int VA = 16 / (int)sizeof(A);
+  if (TRI_RMS_DW_ONE && hidden % VA == 0 && aligned16(partial)) {
+    dw_reduce_kernel<T, A><<<(unsigned)cdiv(hidden, kDwCg * VA), 256, 0, stream>>>(
+        partial, n_part, hidden, dw);
+    return check_launch("rmsnorm dweight reduce");
+  }
   const int64_t n_groups = cdiv(n_part, kDwGroup);
   dw_sum_groups_kernel<A><<<dim3((unsigned)cdiv(hidden, 256), (unsigned)n_groups), 256, 0,
                             stream>>>(partial, n_part, hidden, sums);
