@@ -26,13 +26,24 @@ namespace {
 
 constexpr int kBlock = 256;
 #ifndef TRI_ADAMW_VEC_PER_THREAD
-#define TRI_ADAMW_VEC_PER_THREAD 2
+#define TRI_ADAMW_VEC_PER_THREAD 1
 #endif
 constexpr int kVecPerThread = TRI_ADAMW_VEC_PER_THREAD;
-constexpr int64_t kChunk = (int64_t)kBlock * kVecPerThread * 8;  // 4096 elements
+constexpr int64_t kChunk = (int64_t)kBlock * kVecPerThread * 8;  // 2048 elements
 // The mixed-precision kernel (four fp32 and two 16-bit streams per element)
 // streams best with four 8-element steps per lane: 820 vs 839 us per GPT
 // step with two, 860 with eight; the fp32 kernels are fastest at kChunk.
+// A lane issues its 16-byte loads stream by stream (all of its p vectors,
+// then g, m, v) and its stores likewise (m, v, p), rather than the four
+// streams of one vector together: config-2 step 611-614 -> 599-607 us
+// (loads alone 606-609), on the same boxes; with one vector per lane per
+// stream (the chunk of 2048 fp32 elements above) rather than two, 599-601.
+#ifndef TRI_ADAMW_STREAM_MAJOR
+#define TRI_ADAMW_STREAM_MAJOR 1
+#endif
+#ifndef TRI_ADAMW_STORE_MAJOR
+#define TRI_ADAMW_STORE_MAJOR 1
+#endif
 #ifndef TRI_ADAMW_MIXED_STEPS
 #define TRI_ADAMW_MIXED_STEPS 4
 #endif
@@ -67,6 +78,28 @@ __device__ __forceinline__ void adam_chunk(T* __restrict__ p, const T* __restric
     const int64_t vec_end = start + ((end - start) / VEC) * VEC;
     constexpr int NVEC = (int)(kChunk / VEC / kBlock);
     float pv[NVEC][VEC], gv[NVEC][VEC], mv[NVEC][VEC], vv[NVEC][VEC];
+#if TRI_ADAMW_STREAM_MAJOR
+#pragma unroll
+    for (int u = 0; u < NVEC; ++u) {
+      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
+      if (e < vec_end) load_stream<T, VEC>(p + e, pv[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < NVEC; ++u) {
+      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
+      if (e < vec_end) load_stream<T, VEC>(g + e, gv[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < NVEC; ++u) {
+      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
+      if (e < vec_end) load_stream<float, VEC>(m + e, mv[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < NVEC; ++u) {
+      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
+      if (e < vec_end) load_stream<float, VEC>(v + e, vv[u]);
+    }
+#else
 #pragma unroll
     for (int u = 0; u < NVEC; ++u) {
       const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
@@ -77,6 +110,28 @@ __device__ __forceinline__ void adam_chunk(T* __restrict__ p, const T* __restric
         load_stream<float, VEC>(v + e, vv[u]);
       }
     }
+#endif
+#if TRI_ADAMW_STORE_MAJOR
+#pragma unroll
+    for (int u = 0; u < NVEC; ++u)
+#pragma unroll
+      for (int i = 0; i < VEC; ++i) adam_update(pv[u][i], gv[u][i], mv[u][i], vv[u][i], h, lr_wd, step_size);
+#pragma unroll
+    for (int u = 0; u < NVEC; ++u) {
+      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
+      if (e < vec_end) store_stream<float, VEC>(m + e, mv[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < NVEC; ++u) {
+      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
+      if (e < vec_end) store_stream<float, VEC>(v + e, vv[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < NVEC; ++u) {
+      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
+      if (e < vec_end) store_stream<T, VEC>(p + e, pv[u]);
+    }
+#else
 #pragma unroll
     for (int u = 0; u < NVEC; ++u) {
       const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
@@ -88,6 +143,7 @@ __device__ __forceinline__ void adam_chunk(T* __restrict__ p, const T* __restric
         store_stream<T, VEC>(p + e, pv[u]);
       }
     }
+#endif
     for (int64_t e = vec_end + threadIdx.x; e < end; e += kBlock) {
       float pp = to_f32(p[e]), mm = m[e], vv2 = v[e];
       adam_update(pp, to_f32(g[e]), mm, vv2, h, lr_wd, step_size);
