@@ -17,7 +17,17 @@ namespace tri {
 namespace {
 
 constexpr int kBlock = 256;
-constexpr int kUnroll = 4;
+#ifndef TRI_SWIGLU_UNROLL
+#define TRI_SWIGLU_UNROLL 4
+#endif
+constexpr int kUnroll = TRI_SWIGLU_UNROLL;
+// 1: a lane issues its loads operand by operand (all U vectors of x, then of
+// gate, ...) and its stores likewise, instead of the operands of one vector
+// together (config 2 fwd+bwd 473-475 -> 471 us; unrolling 2 instead of 4:
+// 478 us).
+#ifndef TRI_SWIGLU_STREAM_MAJOR
+#define TRI_SWIGLU_STREAM_MAJOR 1
+#endif
 
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
@@ -28,12 +38,25 @@ swiglu_fwd_kernel(const T* __restrict__ x, const T* __restrict__ g, T* __restric
   const int64_t nvec = n / VEC;
   const int64_t first = (int64_t)blockIdx.x * kBlock * U + threadIdx.x;
   float xv[U][VEC], gv[U][VEC];
+  if constexpr (TRI_SWIGLU_STREAM_MAJOR) {
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int64_t iv = first + (int64_t)u * kBlock;
-    if (iv < nvec) {
-      load_stream<T, VEC>(x + iv * VEC, xv[u]);
-      load_stream<T, VEC>(g + iv * VEC, gv[u]);
+    for (int u = 0; u < U; ++u) {
+      const int64_t iv = first + (int64_t)u * kBlock;
+      if (iv < nvec) load_stream<T, VEC>(x + iv * VEC, xv[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t iv = first + (int64_t)u * kBlock;
+      if (iv < nvec) load_stream<T, VEC>(g + iv * VEC, gv[u]);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t iv = first + (int64_t)u * kBlock;
+      if (iv < nvec) {
+        load_stream<T, VEC>(x + iv * VEC, xv[u]);
+        load_stream<T, VEC>(g + iv * VEC, gv[u]);
+      }
     }
   }
 #pragma unroll
@@ -61,30 +84,58 @@ swiglu_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x, const T* __
   const int64_t nvec = n / VEC;
   const int64_t first = (int64_t)blockIdx.x * kBlock * U + threadIdx.x;
   float dv[U][VEC], xv[U][VEC], gv[U][VEC];
+  if constexpr (TRI_SWIGLU_STREAM_MAJOR) {
+    const T* src[3] = {dy, x, g};
+    float (*dst[3])[VEC] = {dv, xv, gv};
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int64_t iv = first + (int64_t)u * kBlock;
-    if (iv < nvec) {
-      load_stream<T, VEC>(dy + iv * VEC, dv[u]);
-      load_stream<T, VEC>(x + iv * VEC, xv[u]);
-      load_stream<T, VEC>(g + iv * VEC, gv[u]);
+    for (int o = 0; o < 3; ++o)
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        const int64_t iv = first + (int64_t)u * kBlock;
+        if (iv < nvec) load_stream<T, VEC>(src[o] + iv * VEC, dst[o][u]);
+      }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t iv = first + (int64_t)u * kBlock;
+      if (iv < nvec) {
+        load_stream<T, VEC>(dy + iv * VEC, dv[u]);
+        load_stream<T, VEC>(x + iv * VEC, xv[u]);
+        load_stream<T, VEC>(g + iv * VEC, gv[u]);
+      }
     }
   }
+  // gradients in place: dv becomes dx, xv becomes dgate
 #pragma unroll
-  for (int u = 0; u < U; ++u) {
-    const int64_t iv = first + (int64_t)u * kBlock;
-    if (iv < nvec) {
-      float ox[VEC], og[VEC];
+  for (int u = 0; u < U; ++u)
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) {
-        const float s = sigmoid_f32(xv[u][i]);
-        const float silu = xv[u][i] * s;
-        const float dsilu = s * (1.0f + xv[u][i] * (1.0f - s));
-        ox[i] = dv[u][i] * gv[u][i] * dsilu;
-        og[i] = dv[u][i] * silu;
+    for (int i = 0; i < VEC; ++i) {
+      const float s = sigmoid_f32(xv[u][i]);
+      const float silu = xv[u][i] * s;
+      const float dsilu = s * (1.0f + xv[u][i] * (1.0f - s));
+      const float d = dv[u][i];
+      dv[u][i] = d * gv[u][i] * dsilu;
+      xv[u][i] = d * silu;
+    }
+  if constexpr (TRI_SWIGLU_STREAM_MAJOR) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t iv = first + (int64_t)u * kBlock;
+      if (iv < nvec) store_stream<T, VEC>(dx + iv * VEC, dv[u]);
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t iv = first + (int64_t)u * kBlock;
+      if (iv < nvec) store_stream<T, VEC>(dg + iv * VEC, xv[u]);
+    }
+  } else {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int64_t iv = first + (int64_t)u * kBlock;
+      if (iv < nvec) {
+        store_stream<T, VEC>(dx + iv * VEC, dv[u]);
+        store_stream<T, VEC>(dg + iv * VEC, xv[u]);
       }
-      store_stream<T, VEC>(dx + iv * VEC, ox);
-      store_stream<T, VEC>(dg + iv * VEC, og);
     }
   }
   if (VEC > 1 && blockIdx.x == gridDim.x - 1) {
