@@ -22,6 +22,12 @@
 namespace tri {
 namespace {
 
+// The backward's row prefetch issues all of a lane's x vectors, then its dy
+// vectors (config 2: 69.8 -> 68.7 us), rather than the two of each vector
+// together.
+#ifndef TRI_RMS_STREAM_MAJOR
+#define TRI_RMS_STREAM_MAJOR 1
+#endif
 #ifndef TRI_RMS_BWD_BLOCKS
 #define TRI_RMS_BWD_BLOCKS 512
 #endif
@@ -179,6 +185,18 @@ rmsnorm_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x,
   float rs_next = 0.f;
   auto fetch = [&](int64_t row, u32x4 (&xb)[NV], u32x4 (&gb)[NV], float& rsb) {
     if (row >= n_rows) return;
+#if TRI_RMS_STREAM_MAJOR
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int vi = lt + j * TPR;
+      if (vi < nvec) xb[j] = ld16_nt(x + row * hidden + (int64_t)vi * VEC);
+    }
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+      const int vi = lt + j * TPR;
+      if (vi < nvec) gb[j] = ld16_nt(dy + row * hidden + (int64_t)vi * VEC);
+    }
+#else
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int vi = lt + j * TPR;
@@ -187,6 +205,7 @@ rmsnorm_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x,
         gb[j] = ld16_nt(dy + row * hidden + (int64_t)vi * VEC);
       }
     }
+#endif
     if (rstd_in != nullptr) rsb = rstd_in[row];
   };
   fetch(first + g, xr, gr, rs_next);
