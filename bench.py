@@ -17,7 +17,10 @@ reference PyTorch CPU path timed on this host's cores (``cpu_baseline``; the
 attention, linear-CE and GPT legs carry their own).
 
 Kernel times are measured with HIP events recorded on the stream every kernel
-is launched on (torch's current stream).
+is launched on (torch's current stream), two per measured span: the headline
+spans K whole steps, each op of the breakdown K back-to-back calls of that op
+(an event recorded between two kernels leaves the GPU idle for a few
+microseconds while it drains the queue for the timestamp).
 """
 
 from __future__ import annotations
@@ -148,33 +151,41 @@ def row_leg(torch, tritium, steps: int, warmup: int):
     vs = [torch.zeros(s, device=dev) for s in shapes]
     n_params = sum(p.numel() for p in params)
 
-    timer = Timer(torch)
     step_no = [0]
 
-    def step():
-        timer.start("rmsnorm")
+    # each op's forward+backward (AdamW: one update); the gradients are cleared
+    # so that the next call does not accumulate into them
+    def op_rmsnorm():
         y = tritium.rmsnorm(x, w, 1e-6)
         torch.autograd.backward(y, dy)
-        timer.stop("rmsnorm")
-        timer.start("rope")
+        x.grad = w.grad = None
+
+    def op_rope():
         qo, ko = tritium.rope(q, k, cos, sin, position_ids=pos)
         torch.autograd.backward((qo, ko), (dq, dk))
-        timer.stop("rope")
-        timer.start("swiglu")
+        q.grad = k.grad = None
+
+    def op_swiglu():
         out = tritium.swiglu(sx, sg)
         torch.autograd.backward(out, sdy)
-        timer.stop("swiglu")
+        sx.grad = sg.grad = None
+
+    def op_adamw():
         step_no[0] += 1
-        timer.start("adamw")
         tritium.adamw_step_multi(params, grads, ms, vs, step=step_no[0], **ADAMW_HP)
-        timer.stop("adamw")
-        # grads accumulate across steps; clear them outside the timed kernels' events
-        x.grad = w.grad = q.grad = k.grad = sx.grad = sg.grad = None
+
+    op_fns = {"rmsnorm": op_rmsnorm, "rope": op_rope, "swiglu": op_swiglu, "adamw": op_adamw}
+
+    def step():
+        for f in op_fns.values():
+            f()
 
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
-    timer.reset()
+    # the headline: K whole steps between two events and nothing else on the
+    # stream (an event recorded between two kernels leaves the GPU idle for
+    # about 5 us while it drains the queue for the timestamp)
     t0 = time.perf_counter()
     ev0 = torch.cuda.Event(enable_timing=True)
     ev1 = torch.cuda.Event(enable_timing=True)
@@ -185,6 +196,18 @@ def row_leg(torch, tritium, steps: int, warmup: int):
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     step_ms = ev0.elapsed_time(ev1) / steps
+    # the per-op breakdown: each op K times back to back between two events
+    op_ms = {}
+    for name, f in op_fns.items():
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(steps):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        op_ms[name] = e0.elapsed_time(e1) / steps
 
     rb = rmsnorm_bytes(n_rows, ROWS_D)
     ropeb = rope_bytes(n_rows, ROPE_H, ROPE_HD, ROWS_T)
@@ -194,7 +217,7 @@ def row_leg(torch, tritium, steps: int, warmup: int):
     total_bytes = sum(per_op_bytes.values())
     ops = {}
     for name, nbytes in per_op_bytes.items():
-        t = timer.mean_ms(name)
+        t = op_ms[name]
         gbs = nbytes / (t * 1e-3) / 1e9
         ops[name] = {"ms": round(t, 4), "bytes": nbytes, "GB/s": round(gbs, 1),
                      "frac_hbm_peak": round(gbs / HBM_PEAK_GBS, 4)}
@@ -206,7 +229,7 @@ def row_leg(torch, tritium, steps: int, warmup: int):
         "total_bytes": total_bytes,
         "ops": ops,
         "n_params": n_params,
-        "adamw_ms": timer.mean_ms("adamw"),
+        "adamw_ms": op_ms["adamw"],
         "adamw_bytes": ab,
     }
 
@@ -221,21 +244,34 @@ def attention_leg(torch, tritium, iters: int = 5, warmup: int = 2,
 
     q, k, v = (rn((b, h, t, d)).requires_grad_(True) for _ in range(3))
     do = rn((b, h, t, d))
-    timer = Timer(torch)
-    for i in range(warmup + iters):
-        if i == warmup:
-            torch.cuda.synchronize()
-            timer.reset()
-        timer.start("fwd")
+
+    def fwd_bwd():
         o = tritium.attention(q, k, v, is_causal=True)
-        timer.stop("fwd")
-        timer.start("bwd")
         o.backward(do)
-        timer.stop("bwd")
         q.grad = k.grad = v.grad = None
-    torch.cuda.synchronize()
+
+    def fwd():
+        tritium.attention(q, k, v, is_causal=True)
+
+    for _ in range(warmup):
+        fwd_bwd()
+    # forward+backward over `iters` passes between two events (events between
+    # the kernels would leave the GPU idle for their timestamps), then the
+    # forward alone the same way; the backward is the difference
+    spans = {}
+    for name, f in (("fwd_bwd", fwd_bwd), ("fwd", fwd)):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(iters):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        spans[name] = e0.elapsed_time(e1) / iters
     ff, fb = attention_flops(b, h, t, d)
-    fwd_ms, bwd_ms = timer.mean_ms("fwd"), timer.mean_ms("bwd")
+    fwd_ms = spans["fwd"]
+    bwd_ms = spans["fwd_bwd"] - fwd_ms
     tot = (ff + fb) / ((fwd_ms + bwd_ms) * 1e-3) / 1e12
     return {
         "shape": [b, h, t, d],
