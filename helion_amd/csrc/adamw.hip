@@ -24,12 +24,17 @@
 namespace tri {
 namespace {
 
-constexpr int kBlock = 256;
+// One wavefront per workgroup: config-2 update 612-618 -> 586-595 us against
+// 256 lanes (128: 607-617, 512: 620-623, 1024: 651-653), on the same boxes.
+#ifndef TRI_ADAMW_BLOCK
+#define TRI_ADAMW_BLOCK 64
+#endif
+constexpr int kBlock = TRI_ADAMW_BLOCK;
 #ifndef TRI_ADAMW_VEC_PER_THREAD
 #define TRI_ADAMW_VEC_PER_THREAD 1
 #endif
 constexpr int kVecPerThread = TRI_ADAMW_VEC_PER_THREAD;
-constexpr int64_t kChunk = (int64_t)kBlock * kVecPerThread * 8;  // 2048 elements
+constexpr int64_t kChunk = (int64_t)kBlock * kVecPerThread * 8;  // 512 elements
 // The mixed-precision kernel (four fp32 and two 16-bit streams per element)
 // streams best with four 8-element steps per lane: 820 vs 839 us per GPT
 // step with two, 860 with eight; the fp32 kernels are fastest at kChunk.
@@ -37,7 +42,7 @@ constexpr int64_t kChunk = (int64_t)kBlock * kVecPerThread * 8;  // 2048 element
 // then g, m, v) and its stores likewise (m, v, p), rather than the four
 // streams of one vector together: config-2 step 611-614 -> 599-607 us
 // (loads alone 606-609), on the same boxes; with one vector per lane per
-// stream (the chunk of 2048 fp32 elements above) rather than two, 599-601.
+// stream rather than two, 599-601.
 #ifndef TRI_ADAMW_STREAM_MAJOR
 #define TRI_ADAMW_STREAM_MAJOR 1
 #endif
@@ -47,7 +52,7 @@ constexpr int64_t kChunk = (int64_t)kBlock * kVecPerThread * 8;  // 2048 element
 #ifndef TRI_ADAMW_MIXED_STEPS
 #define TRI_ADAMW_MIXED_STEPS 4
 #endif
-constexpr int64_t kChunkMixed = (int64_t)kBlock * TRI_ADAMW_MIXED_STEPS * 8;  // 8192 elements
+constexpr int64_t kChunkMixed = (int64_t)kBlock * TRI_ADAMW_MIXED_STEPS * 8;  // 2048 elements
 
 struct Hyper {
   float lr, beta1, beta2, eps, weight_decay, bc1, bc2;
