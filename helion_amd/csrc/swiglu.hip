@@ -6,7 +6,7 @@
 // Pure streaming kernels: each lane moves U 16-byte vectors per operand, the
 // U loads of a lane are issued before any math so a wavefront keeps
 // U * (#operands) * 1 KiB in flight; a block covers one contiguous
-// 256 * U * VEC element span, so every access is fully coalesced.  Every
+// kBlock * U * VEC element span, so every access is fully coalesced.  Every
 // operand is touched once: loads and stores carry the nontemporal hint.
 #include "common.h"
 #include "../../include/tritium_hip.h"
@@ -16,15 +16,20 @@
 namespace tri {
 namespace {
 
-constexpr int kBlock = 256;
+// One wavefront per workgroup, two vectors per lane per operand: config-2
+// fwd+bwd 463-464 -> 448-449 us on one box (64 lanes with four vectors:
+// 456.5; 128 lanes: 465-466).
+#ifndef TRI_SWIGLU_BLOCK
+#define TRI_SWIGLU_BLOCK 64
+#endif
+constexpr int kBlock = TRI_SWIGLU_BLOCK;
 #ifndef TRI_SWIGLU_UNROLL
-#define TRI_SWIGLU_UNROLL 4
+#define TRI_SWIGLU_UNROLL 2
 #endif
 constexpr int kUnroll = TRI_SWIGLU_UNROLL;
 // 1: a lane issues its loads operand by operand (all U vectors of x, then of
 // gate, ...) and its stores likewise, instead of the operands of one vector
-// together (config 2 fwd+bwd 473-475 -> 471 us; unrolling 2 instead of 4:
-// 478 us).
+// together (config 2 fwd+bwd 473-475 -> 471 us with 256-lane workgroups).
 #ifndef TRI_SWIGLU_STREAM_MAJOR
 #define TRI_SWIGLU_STREAM_MAJOR 1
 #endif
