@@ -612,6 +612,55 @@ def cpu_baseline(budget_s: float = 12.0):
     }
 
 
+def config1_cpu(torch=None, tritium=None, budget_s: float = 5.0):
+    """Config 1: RMSNorm fwd+bwd on the reference's PyTorch formulas on this host's
+    cores (tests/tritium/test_rmsnorm.py:12-48, restated in oracle/torch_ref.py):
+    x [4096, 768] fp32 ~N(0,1), w = 1 + 0.02 N(0,1), eps 1e-6, dy ~N(0,1), drawn in
+    that order from a CPU generator seeded 0.  Produces y, dx and dw; their time
+    (median after a warm-up run) and checksums, and, when a GPU is given, the
+    max-abs difference of this library's kernels on the same inputs."""
+    import torch as _torch
+
+    from oracle import torch_ref
+
+    cores = len(os.sched_getaffinity(0))
+    _torch.set_num_threads(cores)
+    g = _torch.Generator().manual_seed(0)
+    n, d, eps = 4096, 768, 1e-6
+    x = _torch.randn((n, d), generator=g)
+    w = 1 + 0.02 * _torch.randn((d,), generator=g)
+    dy = _torch.randn((n, d), generator=g)
+    out = {}
+
+    def one():
+        out["y"] = torch_ref.rmsnorm(x, w, eps)
+        out["dx"], out["dw"] = torch_ref.rmsnorm_backward(dy, x, w, eps)
+
+    med, runs = _time_cpu(one, budget_s, min_runs=3, max_runs=50)
+    fwd, bwd = rmsnorm_bytes(n, d, esz=4)
+    res = {
+        "workload": "RMSNorm fwd+bwd, x [4096,768] fp32, w = 1+N(0,0.02), eps 1e-6, seed 0",
+        "ms": round(med * 1e3, 3),
+        "GB/s": round((fwd + bwd) / med / 1e9, 3),
+        "runs": runs,
+        "cores": cores,
+        "cpu_model": _cpu_model(),
+        "kind": "port",
+        "checksums": {k: round(float(v.double().sum()), 6) for k, v in out.items()},
+    }
+    if torch is not None and tritium is not None and torch.cuda.is_available():
+        xg = x.cuda().requires_grad_(True)
+        wg = w.cuda().requires_grad_(True)
+        yg = tritium.rmsnorm(xg, wg, eps)
+        yg.backward(dy.cuda())
+        res["max_abs_diff_vs_hip"] = {
+            "y": float((yg.detach().cpu() - out["y"]).abs().max()),
+            "dx": float((xg.grad.cpu() - out["dx"]).abs().max()),
+            "dw": float((wg.grad.cpu() - out["dw"]).abs().max()),
+        }
+    return res
+
+
 def _cpu_model() -> str:
     try:
         with open("/proc/cpuinfo") as f:
@@ -749,40 +798,63 @@ def mfma_roofline(kernels: str, flops: float, ms: float, counters: str) -> dict:
 
 
 def stream_probe(torch, tritium, reps: int = 10):
-    """GB/s of the plain streaming patterns of ``tritium_stream_probe`` (nontemporal
-    16-byte accesses, persistent grids of 2048-16384 workgroups): read 1 GiB, copy
-    1 GiB, fill 1 GiB, and the AdamW-shaped in-place update over 124,439,808 fp32
-    elements (4 streams read, 3 written).  Median of ``reps`` event-timed launches."""
+    """GB/s of plain HBM streaming patterns (``helion_amd/probe/stream_probe.hip``,
+    its own library ``libtritium_probe.so``; nontemporal 16-byte accesses): read,
+    copy and fill of 1 GiB as persistent grids of 2048-16384 workgroups (4 vectors
+    per lane in flight) and as grid-covering launches (one vector per lane), two
+    streams read and one written (the RMSNorm-backward shape), and the AdamW-shaped
+    in-place update over 124,439,808 fp32 elements (4 streams read, 3 written).
+    Median of ``reps`` event-timed launches after one warm-up."""
+    import ctypes
     import statistics
 
-    from helion_amd import _lib
+    from helion_amd import _build, _lib
+
+    _lib.lib()  # binds torch's HIP runtime first, as every library call does
+    if not os.path.exists(_build.PROBE_PATH):
+        raise RuntimeError(f"{_build.PROBE_PATH} is not built (python -m helion_amd._build)")
+    probe = ctypes.CDLL(_build.PROBE_PATH)
+    probe.tritium_stream_probe.restype = ctypes.c_int
+    probe.tritium_stream_probe.argtypes = [ctypes.c_int] + [ctypes.c_void_p] * 4 + [
+        ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    probe.tritium_probe_last_error.restype = ctypes.c_char_p
 
     dev = torch.device("cuda")
     n = 1 << 26  # 16-byte vectors: 1 GiB
     a = torch.ones(n * 4, device=dev)
     b = torch.empty(n * 4, device=dev)
+    c = torch.empty(n * 4, device=dev)
     sink = torch.zeros(256, device=dev)
     npar = 124439808 // 4 * 4
     p, g, m, v = (torch.rand(npar, device=dev) for _ in range(4))
-    cases = [("read 1 GiB", 0, (a, sink, None, None), n, 1 << 30),
-             ("copy 1 GiB", 1, (a, b, None, None), n, 2 << 30),
-             ("fill 1 GiB", 2, (b, None, None, None), n, 1 << 30),
-             ("adamw-shaped 4 read + 3 write", 3, (p, g, m, v), npar // 4, 28 * npar)]
+    persistent = (2048, 4096, 8192, 16384)
+    cases = [("read 1 GiB, persistent", 0, (a, sink, None, None), n, 1 << 30, persistent),
+             ("copy 1 GiB, persistent", 1, (a, b, None, None), n, 2 << 30, persistent),
+             ("fill 1 GiB, persistent", 2, (b, None, None, None), n, 1 << 30, persistent),
+             ("adamw-shaped 4 read + 3 write, persistent", 3, (p, g, m, v), npar // 4,
+              28 * npar, persistent),
+             ("read 1 GiB, grid-covering", 4, (a, sink, None, None), n, 1 << 30, (0,)),
+             ("copy 1 GiB, grid-covering", 5, (a, b, None, None), n, 2 << 30, (0,)),
+             ("fill 1 GiB, grid-covering", 6, (b, None, None, None), n, 1 << 30, (0,)),
+             ("2 read + 1 write of 1 GiB, grid-covering", 7, (a, b, c, None), n, 3 << 30, (0,))]
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     out = []
-    for name, pat, bufs, nv, nbytes in cases:
+    for name, pat, bufs, nv, nbytes, grids in cases:
         row = {"pattern": name, "bytes": nbytes}
-        for blocks in (2048, 4096, 8192, 16384):
+        for blocks in grids:
             ptrs = [None if x is None else x.data_ptr() for x in bufs]
             times = []
             for _ in range(reps + 1):
                 s.record()
-                _lib.call("tritium_stream_probe", pat, *ptrs, nv, blocks, _lib.stream_of(a))
+                rc = probe.tritium_stream_probe(pat, *ptrs, nv, max(blocks, 1), _lib.stream_of(a))
+                if rc != 0:
+                    raise RuntimeError(probe.tritium_probe_last_error().decode())
                 e.record()
                 torch.cuda.synchronize()
                 times.append(s.elapsed_time(e))
             ms = statistics.median(times[1:])
-            row[f"GB/s b{blocks}"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+            key = f"GB/s b{blocks}" if blocks else "GB/s"
+            row[key] = round(nbytes / (ms * 1e-3) / 1e9, 1)
         row["best_frac_of_8TB/s"] = round(max(vv for k, vv in row.items() if k.startswith("GB/s"))
                                           / HBM_PEAK_GBS, 4)
         out.append(row)
@@ -893,6 +965,7 @@ def main(argv=None) -> int:
         "algorithmic_bytes_per_launch": rows["adamw_bytes"],
     }
     cpu = None if args.no_cpu else cpu_baseline()
+    cpu_config1 = None if args.no_cpu else config1_cpu(torch, tritium)
     if not args.no_cpu:
         # the other legs' reference PyTorch paths on the same host cores
         for key, fn in (("attention_fwd_bwd", attention_cpu_baseline),
@@ -925,6 +998,7 @@ def main(argv=None) -> int:
         "ops": ops,
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "cpu_config1": cpu_config1,
     }
     print(json.dumps(line), flush=True)
     return 0

@@ -27,6 +27,9 @@ SRC_DIR = os.path.join(PKG_DIR, "csrc")
 OBJ_DIR = os.path.join(PKG_DIR, "_build")
 REPO_DIR = os.path.dirname(PKG_DIR)
 LIB_PATH = os.path.join(PKG_DIR, "libtritium_hip.so")
+# measurement-only probes (HBM streaming ceilings), loaded by bench.py alone
+PROBE_SRC = os.path.join(PKG_DIR, "probe", "stream_probe.hip")
+PROBE_PATH = os.path.join(PKG_DIR, "libtritium_probe.so")
 
 HIPCC = os.environ.get("HIPCC") or shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 
@@ -88,6 +91,21 @@ def build(jobs: int | None = None, verbose: bool = False, out: str = LIB_PATH,
     return out
 
 
+def build_probe() -> str:
+    """Compile the streaming probes into their own library (not the product's)."""
+    os.makedirs(OBJ_DIR, exist_ok=True)
+    obj_dir = os.path.join(OBJ_DIR, "probe")
+    os.makedirs(obj_dir, exist_ok=True)
+    obj, _ = _compile(PROBE_SRC, obj_dir)
+    tmp = PROBE_PATH + ".tmp"
+    cmd = [HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp, obj]
+    proc = subprocess.run(cmd, capture_output=True, text=True)
+    if proc.returncode != 0:
+        raise RuntimeError(f"link failed:\n{' '.join(cmd)}\n{proc.stdout}{proc.stderr}")
+    os.replace(tmp, PROBE_PATH)
+    return PROBE_PATH
+
+
 def main(argv: list[str] | None = None) -> int:
     ap = argparse.ArgumentParser(description=__doc__)
     ap.add_argument("--jobs", type=int, default=None)
@@ -96,6 +114,8 @@ def main(argv: list[str] | None = None) -> int:
     ap.add_argument("-D", dest="defines", action="append", default=[], help="preprocessor macro")
     args = ap.parse_args(argv)
     print(build(args.jobs, args.verbose, args.out, tuple(args.defines)))
+    if args.out == LIB_PATH:
+        print(build_probe())
     return 0
 
 

@@ -112,7 +112,6 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I32,
         [_P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I32, _P],
     ),
-    "tritium_stream_probe": (_I32, [_I32, _P, _P, _P, _P, _I64, _I32, _P]),
     "tritium_embedding_bwd_workspace_size": (_SZ, [_I64, _I64, _I64]),
     "tritium_embedding_bwd": (
         _I32, [_P, _I32, _I64, _P, _I64, _P, _P, _I64, _I64, _P, _SZ, _I32, _P],
@@ -131,7 +130,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         _I32,
         [_P, _I32, _I64, _F32, _F32, _F32, _F32, _F32, _F64, _F64, _P],
     ),
-    "tritium_cross_entropy_fwd": (_I32, [_P, _P, _I32, _P, _P, _P, _I64, _I64, _I32, _P]),
+    "tritium_cross_entropy_fwd_ws": (_I32, [_P, _P, _I32, _P, _P, _P, _SZ, _I64, _I64, _I32, _P]),
     "tritium_cross_entropy_fwd_workspace_size": (_SZ, [_I64, _I64, _I32]),
     "tritium_cross_entropy_bwd": (
         _I32, [_P, _P, _P, _I32, _P, _P, _I64, _I64, _F64, _I32, _P],

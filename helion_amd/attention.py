@@ -21,6 +21,7 @@ Differences:
 
 from __future__ import annotations
 
+import collections
 import ctypes
 from typing import Any
 
@@ -112,7 +113,12 @@ def _strides(*ts: torch.Tensor):
 # Decode workspaces, one per (device, stream), grown on demand: calls on one
 # stream never overlap, so each reuses its stream's buffer instead of
 # allocating one per call (the partials are written before they are read).
-_DECODE_WS: dict[tuple[int, int], torch.Tensor] = {}
+# Only the _DECODE_WS_KEEP most recently used streams keep theirs: a caller
+# that makes a stream per request retains at most that many buffers, each the
+# size of the largest call seen on its stream.  An evicted buffer goes back to
+# torch's caching allocator, ordered on the stream it was allocated on.
+_DECODE_WS: "collections.OrderedDict[tuple[int, int], torch.Tensor]" = collections.OrderedDict()
+_DECODE_WS_KEEP = 4
 
 
 def _decode_workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tensor:
@@ -124,6 +130,9 @@ def _decode_workspace(dev: torch.device, stream: int, nbytes: int) -> torch.Tens
     if buf is None or buf.numel() < n:
         buf = torch.empty((n,), device=dev, dtype=torch.float32)
         _DECODE_WS[key] = buf
+    _DECODE_WS.move_to_end(key)
+    while len(_DECODE_WS) > _DECODE_WS_KEEP:
+        _DECODE_WS.popitem(last=False)
     return buf
 
 

@@ -83,9 +83,9 @@ def _cross_entropy_forward(logits: torch.Tensor, target: torch.Tensor):
     ws_bytes = _lib.lib().tritium_cross_entropy_fwd_workspace_size(n_rows, vocab_size, code)
     work = torch.empty((max(1, -(-ws_bytes // 4)),), device=dev, dtype=torch.float32)
     _lib.call(
-        "tritium_cross_entropy_fwd", logits.data_ptr(), target.data_ptr(), _target_kind(target),
-        loss.data_ptr(), lse.data_ptr(), work.data_ptr(), n_rows, vocab_size, code,
-        _lib.stream_of(logits),
+        "tritium_cross_entropy_fwd_ws", logits.data_ptr(), target.data_ptr(),
+        _target_kind(target), loss.data_ptr(), lse.data_ptr(), work.data_ptr(),
+        work.numel() * 4, n_rows, vocab_size, code, _lib.stream_of(logits),
     )
     return loss, lse
 

@@ -301,20 +301,24 @@ extern "C" size_t tritium_cross_entropy_fwd_workspace_size(int64_t n_rows, int64
   return chunks > 1 ? (size_t)(n_rows * chunks) * sizeof(float2) : (size_t)n_rows * sizeof(float);
 }
 
-extern "C" int tritium_cross_entropy_fwd(const void* logits, const void* target, int target_kind,
-                                         float* loss, float* lse, float* work, int64_t n_rows,
-                                         int64_t vocab, int dtype, void* stream) {
+extern "C" int tritium_cross_entropy_fwd_ws(const void* logits, const void* target,
+                                            int target_kind, float* loss, float* lse, void* work,
+                                            size_t work_bytes, int64_t n_rows, int64_t vocab,
+                                            int dtype, void* stream) {
   if (n_rows < 0 || vocab <= 0) return fail(TRI_EINVAL, "cross_entropy: bad sizes");
   if (n_rows >= ((int64_t)1 << 31)) return fail(TRI_EINVAL, "cross_entropy: too many rows");
   hipStream_t st = (hipStream_t)stream;
   if (n_rows == 0) return TRI_OK;
+  const size_t need = tritium_cross_entropy_fwd_workspace_size(n_rows, vocab, dtype);
+  if (work == nullptr || work_bytes < need)
+    return fail(TRI_EINVAL, "cross_entropy: workspace of %zu bytes, %zu needed", work_bytes, need);
+  if ((reinterpret_cast<uintptr_t>(work) & 7u) != 0)
+    return fail(TRI_EINVAL, "cross_entropy: workspace must be 8-byte aligned");
   const int vec_ok = rows_vec_ok(logits, vocab, dtype);
   int chunks;
   int64_t span;
   span_split(n_rows, vocab, chunks, span);
   if (chunks > 1) {
-    if ((reinterpret_cast<uintptr_t>(work) & 7u) != 0)
-      return fail(TRI_EINVAL, "cross_entropy: workspace must be 8-byte aligned");
     float2* part = reinterpret_cast<float2*>(work);
     TRI_DISPATCH_INDEX(target_kind, TT,
       TRI_DISPATCH_FLOAT(dtype, T, {
@@ -326,7 +330,7 @@ extern "C" int tritium_cross_entropy_fwd(const void* logits, const void* target,
       }));
     return check_launch("cross_entropy_finish");
   }
-  float* nll = work;
+  float* nll = reinterpret_cast<float*>(work);
   TRI_DISPATCH_INDEX(target_kind, TT,
     TRI_DISPATCH_FLOAT(dtype, T, {
       if (vocab >= kWideRow) {

@@ -369,12 +369,14 @@ int tritium_sum_splits(const float* src, void* dst, int64_t n_splits, int64_t n,
  * targets, lse[row] = logsumexp(logits[row]) in fp32, nll[row] = lse[row] -
  * logits[row, target[row]] (NaN for a target outside [0, vocab)), and
  * loss[0] = mean(nll) summed in a fixed order.  `work` is caller-provided
- * scratch (8-byte aligned) of tritium_cross_entropy_fwd_workspace_size bytes:
- * the n_rows nll values, or, for fewer rows than the GPU has room for blocks
- * of long rows, a (max, sum) pair per span of each row. */
-int tritium_cross_entropy_fwd(const void* logits, const void* target, int target_kind,
-                              float* loss, float* lse, float* work, int64_t n_rows, int64_t vocab,
-                              int dtype, void* stream);
+ * scratch (8-byte aligned) of `work_bytes` bytes, at least
+ * tritium_cross_entropy_fwd_workspace_size(n_rows, vocab, dtype): the n_rows
+ * nll values, or, for fewer rows than the GPU has room for blocks of long
+ * rows, a (max, sum) pair per span of each row.  A smaller or misaligned
+ * buffer is rejected with TRI_EINVAL before anything is launched. */
+int tritium_cross_entropy_fwd_ws(const void* logits, const void* target, int target_kind,
+                                 float* loss, float* lse, void* work, size_t work_bytes,
+                                 int64_t n_rows, int64_t vocab, int dtype, void* stream);
 size_t tritium_cross_entropy_fwd_workspace_size(int64_t n_rows, int64_t vocab, int dtype);
 
 /* tritium.cross_entropy_backward (cross_entropy.py:71-100
@@ -384,15 +386,6 @@ size_t tritium_cross_entropy_fwd_workspace_size(int64_t n_rows, int64_t vocab, i
 int tritium_cross_entropy_bwd(const float* grad_out, const void* logits, const void* target,
                               int target_kind, const float* lse, void* dlogits, int64_t n_rows,
                               int64_t vocab, double grad_denominator, int dtype, void* stream);
-
-/* ---- measurement ---------------------------------------------------------
- * HBM streaming probes for bench.py --stream-probe (no counterpart in the
- * reference; measurement only): pattern 0 reads n_vec4 16-byte vectors of a
- * (b: a 1 KB scratch sink), 1 copies a to b, 2 fills a, 3 runs an AdamW-shaped
- * update reading a, b, c, d and writing a, c, d in place -- all with
- * nontemporal 16-byte accesses from `blocks` 256-lane workgroups. */
-int tritium_stream_probe(int pattern, void* a, void* b, void* c, void* d, int64_t n_vec4,
-                         int blocks, void* stream);
 
 #ifdef __cplusplus
 }

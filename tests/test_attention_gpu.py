@@ -123,6 +123,27 @@ def test_attention_decode_grads_through_general_backward():
     assert_close(v.grad, edv, 2e-2, 2e-2, "dv")
 
 
+def test_attention_decode_workspace_cache_is_bounded():
+    # one workspace per (device, stream), only the most recent few streams keep theirs;
+    # each stream's decode still matches the oracle
+    att = importlib.import_module("helion_amd.attention")
+    b, h, hkv, kv_len, d = 1, 4, 2, 700, 64
+    q = randn((b, h, 1, d), torch.bfloat16, 11)
+    k = randn((b, hkv, kv_len, d), torch.bfloat16, 12)
+    v = randn((b, hkv, kv_len, d), torch.bfloat16, 13)
+    eo, _ = oracle.attention.forward(np32(q), np32(k), np32(v), False)
+    streams = [torch.cuda.Stream() for _ in range(att._DECODE_WS_KEEP + 3)]
+    for st in streams:
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            o = tritium.attention(q, k, v, is_causal=False)
+        torch.cuda.current_stream().wait_stream(st)
+        assert_close(o, eo, 2e-2, 2e-2, "o")
+        assert len(att._DECODE_WS) <= att._DECODE_WS_KEEP
+    keys = list(att._DECODE_WS)
+    assert keys[-1][1] == streams[-1].cuda_stream
+
+
 def test_attention_large_head_bf16_t1024():
     _check(torch.bfloat16, 1, 2, 2, 1024, 1024, 128, True, seed=13)
 

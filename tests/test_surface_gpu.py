@@ -40,9 +40,12 @@ def _close(actual, expected, dtype=None, tol=None):
 
 # ------------------------------------------------------------- cross_entropy
 CE_SHAPES = [(1, 10), (7, 100), (64, 1000), (33, 8191), (16, 8192), (8, 50304), (3, 131072),
-             (5, 12345), (300, 257),
-             # the one-launch path (<= 128 rows of <= 128 16-byte vectors) and its edges
-             (128, 1024), (129, 1024), (128, 1032), (16, 512), (1, 8)]
+             (5, 12345), (300, 257), (128, 1024), (16, 512), (1, 8),
+             # dispatch edges of the forward: rows of >= 8192 elements are cut into spans
+             # (a (max, sum) pair per span, merged in span order) when there are fewer rows
+             # than two workgroups per compute unit (512 on a 256-CU part), otherwise a
+             # 256-lane block per row; shorter rows get one wavefront each
+             (511, 8192), (512, 8192), (513, 8192), (511, 8191), (2, 16384), (2, 16376)]
 
 
 def _targets(n, v, seed, dtype=torch.int64):
@@ -109,6 +112,31 @@ def test_cross_entropy_edge_cases():
     bad = torch.tensor([3, 16], device="cuda")
     assert math.isnan(float(tritium.cross_entropy(logits, bad)))
     assert not tritium.cross_entropy(logits, torch.tensor([3, 15], device="cuda")).isnan()
+
+
+def test_cross_entropy_forward_rejects_small_workspace():
+    # The C entry takes the workspace size and refuses a buffer smaller than
+    # tritium_cross_entropy_fwd_workspace_size before launching anything.
+    lib = importlib.import_module("helion_amd._lib")
+    n, v = 16, 32768  # few long rows: one (max, sum) pair per span
+    logits = randn((n, v), torch.bfloat16, seed=5)
+    target = _targets(n, v, seed=6)
+    code = lib.dtype_code(logits.dtype)
+    need = lib.lib().tritium_cross_entropy_fwd_workspace_size(n, v, code)
+    assert need > n * 4
+    loss = torch.empty((), device="cuda")
+    lse = torch.empty((n,), device="cuda")
+    work = torch.empty((need // 4 + 1,), device="cuda")
+    with pytest.raises(RuntimeError, match="workspace"):
+        lib.call("tritium_cross_entropy_fwd_ws", logits.data_ptr(), target.data_ptr(), 2,
+                 loss.data_ptr(), lse.data_ptr(), work.data_ptr(), n * 4, n, v, code,
+                 lib.stream_of(logits))
+    lib.call("tritium_cross_entropy_fwd_ws", logits.data_ptr(), target.data_ptr(), 2,
+             loss.data_ptr(), lse.data_ptr(), work.data_ptr(), need, n, v, code,
+             lib.stream_of(logits))
+    ref_loss, ref_lse, _ = _ce_ref(logits, target)
+    _close(loss, ref_loss, tol=1e-5)
+    _close(lse, ref_lse, tol=1e-5)
 
 
 def test_cross_entropy_no_autograd_when_not_needed():
