@@ -948,7 +948,7 @@ def main(argv=None) -> int:
 
     adamw_gbs = rows["adamw_bytes"] / (rows["adamw_ms"] * 1e-3) / 1e9
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "adamw_multi_config2_traffic.txt")
+    tpath = os.path.join(ROOT, "profiles", "row_ops_config2_traffic.txt")
     if os.path.exists(tpath):
         with open(tpath) as f:
             for line in f:
