@@ -285,6 +285,63 @@ def attention_leg(torch, tritium, iters: int = 5, warmup: int = 2,
     }
 
 
+def attention_gpt_leg(torch, tritium, iters: int = 20, warmup: int = 3,
+                      b=16, t=1024, h=12, d=64):
+    """Causal attention at the config-5 GPT block's shape, timed alone (outside the
+    training step, where the projection GEMMs run beside it on a second stream):
+    the block's own call, RoPE on q and k over the fused q/k/v projection
+    [b, t, 3, h, d] (``_QKVRopeAttention`` in helion_amd/gpt.py: k rotated once,
+    q rotated as the attention kernels load it), forward and forward+backward."""
+    from helion_amd.gpt import _QKVRopeAttention
+
+    dev = torch.device("cuda")
+    g = torch.Generator().manual_seed(0)
+    qkv = torch.randn((b, t, 3, h, d), generator=g).to(torch.bfloat16).to(dev)
+    qkv.requires_grad_(True)
+    do = torch.randn((b, t, h, d), generator=g).to(torch.bfloat16).to(dev)
+    half = d // 2
+    inv_freq = 1.0 / (10000.0 ** (torch.arange(half, dtype=torch.float32) / half))
+    freqs = torch.outer(torch.arange(t, dtype=torch.float32), inv_freq)
+    cos, sin = freqs.cos().to(dev), freqs.sin().to(dev)
+    pos = torch.arange(t, dtype=torch.int64).repeat(b).to(dev)
+
+    def fwd_bwd():
+        o = _QKVRopeAttention.apply(qkv, cos, sin, pos)
+        o.backward(do)
+        qkv.grad = None
+
+    def fwd():
+        with torch.no_grad():
+            _QKVRopeAttention.apply(qkv, cos, sin, pos)
+
+    for _ in range(warmup):
+        fwd_bwd()
+    spans = {}
+    for name, f in (("fwd_bwd", fwd_bwd), ("fwd", fwd)):
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record()
+        for _ in range(iters):
+            f()
+        e1.record()
+        torch.cuda.synchronize()
+        spans[name] = e0.elapsed_time(e1) / iters
+    ff, fb = attention_flops(b, h, t, d)
+    fwd_ms = spans["fwd"]
+    bwd_ms = spans["fwd_bwd"] - fwd_ms
+    tot = (ff + fb) / ((fwd_ms + bwd_ms) * 1e-3) / 1e12
+    return {
+        "shape": [b, h, t, d], "rope": "q on load, k once", "layout": "fused qkv [b, t, 3, h, d]",
+        "fwd_ms": round(fwd_ms, 4), "bwd_ms": round(bwd_ms, 4),
+        "fwd_TFLOP/s": round(ff / (fwd_ms * 1e-3) / 1e12, 1),
+        "bwd_TFLOP/s": round(fb / (bwd_ms * 1e-3) / 1e12, 1),
+        "TFLOP/s": round(tot, 1),
+        "frac_mfma_peak": round(tot / MFMA_BF16_PEAK_TFLOPS, 4),
+        "flops_basis": "FA2 convention, 14*D per visible pair (T^2/2 pairs per head)",
+    }
+
+
 def lce_leg(torch, tritium, iters: int = 3, warmup: int = 1, n=8192, d=4096, v=128256):
     if not hasattr(tritium, "linear_cross_entropy"):
         return None
@@ -867,9 +924,10 @@ def main(argv=None) -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--legs", default="rows,attention,lce,gpt,refbench,decode",
-                    help="comma list of rows,attention,lce,gpt,refbench (rows is the headline; "
-                         "refbench reruns the reference's published benchmark rows)")
+    ap.add_argument("--legs", default="rows,attention,attngpt,lce,gpt,refbench,decode",
+                    help="comma list of rows,attention,attngpt,lce,gpt,refbench,decode (rows is "
+                         "the headline; attngpt is attention at the GPT block's shape; refbench "
+                         "reruns the reference's published benchmark rows)")
     ap.add_argument("--stream-probe", action="store_true",
                     help="only time the HBM streaming probes (read, copy, fill, AdamW-shaped "
                          "update; tritium_stream_probe) that set the row kernels' ceilings")
@@ -911,6 +969,9 @@ def main(argv=None) -> int:
         if "attention" in legs:
             ops["attention_fwd_bwd"] = attention_leg(torch, tritium, iters=args.steps,
                                                      warmup=args.warmup)
+        if "attngpt" in legs:
+            ops["attention_gpt_shape"] = attention_gpt_leg(torch, tritium, iters=args.steps,
+                                                           warmup=args.warmup)
         if "lce" in legs:
             ops["linear_ce_fwd_bwd"] = lce_leg(torch, tritium, iters=args.steps,
                                                warmup=args.warmup)
@@ -928,6 +989,10 @@ def main(argv=None) -> int:
     if "attention" in legs:
         ops["attention_fwd_bwd"] = attention_leg(torch, tritium)
         print(f"[bench] attention: {ops['attention_fwd_bwd']}", file=sys.stderr, flush=True)
+    if "attngpt" in legs:
+        ops["attention_gpt_shape"] = attention_gpt_leg(torch, tritium)
+        print(f"[bench] attention (GPT shape): {ops['attention_gpt_shape']}", file=sys.stderr,
+              flush=True)
     if "lce" in legs:
         res = lce_leg(torch, tritium)
         if res is not None:

@@ -1,4 +1,5 @@
-"""``attention`` on gfx950 HIP kernels (bf16/fp16 MFMA; fp32 SIMT).
+"""``attention`` on gfx950 HIP kernels (bf16/fp16 MFMA for head_dim 16-256;
+fp32, and 16-bit head_dims 512 and 1024, on a SIMT path).
 
 Drop-in for alkinun/helion ``tritium/ops/attention.py``: same signature
 (``attention(q, k, v, *, is_causal=True)`` 739-757), validation and messages

@@ -461,14 +461,14 @@ attn_fwd_mfma(FwdArgs a) {
 //     bit 2 for 128-byte rows, differ between rows of one parity).
 template <int D>
 struct BTile {
-  static_assert(D == 64 || D == 128, "head_dim");
+  static_assert(D == 64 || D == 128 || D == 256, "head_dim");
   static constexpr int RB = 2 * D;              // bytes per row
   static constexpr int GR = RB / 16;            // granules per row
   static constexpr int BYTES = 64 * RB;         // one 64-row tile
   static constexpr int DMA_ROWS = 1024 / RB;    // rows per wave-wide DMA
   static constexpr int DMAS = BYTES / 1024;     // wave-wide DMAs per tile
   static __device__ __forceinline__ int key(int r) {
-    if constexpr (GR == 16) return ((r & 3) << 2) | ((r >> 2) & 3);
+    if constexpr (GR >= 16) return ((r & 3) << 2) | ((r >> 2) & 3);
     else return (((r >> 1) & 1) << 2) | ((r >> 2) & 3);
   }
   static __device__ __forceinline__ int off(int r, int c) { return r * RB + ((c ^ key(r)) << 4); }
@@ -724,7 +724,7 @@ constexpr int kRing = TRI_ATTN_RING;  // MFMA operands in flight ahead of use
 constexpr int kF2Stages = TRI_ATTN_FWD_STAGES;  // K/V tiles in the LDS ring
 
 template <typename T, int D>
-__global__ void __launch_bounds__(64 * kF2Waves, 8 / kF2Waves)  // 2 wavefronts per SIMD
+__global__ void __launch_bounds__(64 * kF2Waves, D > 128 ? 1 : 8 / kF2Waves)  // 2 wavefronts per SIMD (1 at D = 256)
 attn_fwd_v2(FwdArgs a) {
   typedef Mfma<T> M;
   typedef typename M::V V;
@@ -1456,9 +1456,13 @@ attn_bwd_dq_mfma(BwdArgs a) {
 // sweeps the 64-row query tiles of every query head of the GQA group that
 // can see them: S = Q K^T and dP = dO V^T from row reads of the Q / dO
 // tiles, dV^T += dO^T P and dK^T += Q^T dS from transposing reads.
-template <typename T, int D, int WAVES>
+template <typename T, int D, int WAVES, int PASS = 0>
 __global__ void __launch_bounds__(64 * WAVES)
 attn_bwd_dkdv_v2(BwdArgs a) {
+  // PASS 0: dK and dV; 1: dV alone; 2: dK alone (head_dim 256, where the K
+  // and V fragments and both accumulators of 32 kv rows would not fit one
+  // wavefront's 512 registers: two launches, S formed in each)
+  constexpr bool DO_DV = PASS != 2, DO_DK = PASS != 1;
   typedef Mfma<T> M;
   typedef typename M::V V;
   typedef BTile<D> P;
@@ -1488,7 +1492,7 @@ attn_bwd_dkdv_v2(BwdArgs a) {
 #pragma unroll
   for (int s = 0; s < KS; ++s) {
     kf[s] = kvvalid ? ld8(kp + (int64_t)kvw * a.sk_s + 16 * s + 8 * g) : zero8<T>();
-    vf[s] = kvvalid ? ld8(vp + (int64_t)kvw * a.sv_s + 16 * s + 8 * g) : zero8<T>();
+    vf[s] = kvvalid && DO_DK ? ld8(vp + (int64_t)kvw * a.sv_s + 16 * s + 8 * g) : zero8<T>();
   }
   f32x16 dv[MT], dk[MT];
 #pragma unroll
@@ -1519,12 +1523,20 @@ attn_bwd_dkdv_v2(BwdArgs a) {
     // (MFMA operands), VGPRs left to the softmax; 8 wavefronts: 256, VGPRs
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      if constexpr (WAVES <= 4) { pin_agpr(dv[mt]); pin_agpr(dk[mt]); }
-      else { pin_vgpr(dv[mt]); pin_vgpr(dk[mt]); }
+      if constexpr (WAVES <= 4) {
+        if constexpr (DO_DV) pin_agpr(dv[mt]);
+        if constexpr (DO_DK) pin_agpr(dk[mt]);
+      } else {
+        if constexpr (DO_DV) pin_vgpr(dv[mt]);
+        if constexpr (DO_DK) pin_vgpr(dk[mt]);
+      }
     }
     if constexpr (WAVES <= 4) {
 #pragma unroll
-      for (int st = 0; st < KS; ++st) { pin_agpr(kf[st]); pin_agpr(vf[st]); }
+      for (int st = 0; st < KS; ++st) {
+        pin_agpr(kf[st]);
+        if constexpr (DO_DK) pin_agpr(vf[st]);
+      }
     }
     wait_vmcnt<0>();
     __syncthreads();
@@ -1546,7 +1558,7 @@ attn_bwd_dkdv_v2(BwdArgs a) {
 #pragma unroll
       for (int st = 0; st < KS; ++st) {
         s = M::mma(bt_row<T, D>(Qs, 32 * mq, st), kf[st], s);
-        dp = M::mma(bt_row<T, D>(dOs, 32 * mq, st), vf[st], dp);
+        if constexpr (DO_DK) dp = M::mma(bt_row<T, D>(dOs, 32 * mq, st), vf[st], dp);
       }
       __builtin_amdgcn_s_setprio(0);
       // phases are fenced so that no more than one phase's LDS fragments
@@ -1587,8 +1599,8 @@ attn_bwd_dkdv_v2(BwdArgs a) {
         }
 #pragma unroll
         for (int mt = 0; mt < MT; ++mt) {
-          dv[mt] = M::mma(bt_tr<T, D>(dOs, 32 * mq + 16 * t, mt), pb, dv[mt]);
-          dk[mt] = M::mma(bt_tr<T, D>(Qs, 32 * mq + 16 * t, mt), db, dk[mt]);
+          if constexpr (DO_DV) dv[mt] = M::mma(bt_tr<T, D>(dOs, 32 * mq + 16 * t, mt), pb, dv[mt]);
+          if constexpr (DO_DK) dk[mt] = M::mma(bt_tr<T, D>(Qs, 32 * mq + 16 * t, mt), db, dk[mt]);
         }
       }
       __builtin_amdgcn_s_setprio(0);
@@ -1605,10 +1617,12 @@ attn_bwd_dkdv_v2(BwdArgs a) {
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
         const int d0 = 32 * mt + 8 * rr + 4 * g;
-        store4<T>(dkr + d0, dk[mt][4 * rr] * sc, dk[mt][4 * rr + 1] * sc,
-                  dk[mt][4 * rr + 2] * sc, dk[mt][4 * rr + 3] * sc);
-        store4<T>(dvr + d0, dv[mt][4 * rr], dv[mt][4 * rr + 1], dv[mt][4 * rr + 2],
-                  dv[mt][4 * rr + 3]);
+        if constexpr (DO_DK)
+          store4<T>(dkr + d0, dk[mt][4 * rr] * sc, dk[mt][4 * rr + 1] * sc,
+                    dk[mt][4 * rr + 2] * sc, dk[mt][4 * rr + 3] * sc);
+        if constexpr (DO_DV)
+          store4<T>(dvr + d0, dv[mt][4 * rr], dv[mt][4 * rr + 1], dv[mt][4 * rr + 2],
+                    dv[mt][4 * rr + 3]);
       }
     }
   }
@@ -2007,7 +2021,7 @@ __device__ __forceinline__ void store_dq_row(f32x16 (&dq)[D / 32], T* dqr, float
 // and sweeps the 64-row K/V tiles it can see: S^T = K Q^T and
 // dP^T = V dO^T from row reads, dQ^T += K^T dS^T from transposing reads.
 template <typename T, int D, int WAVES>
-__global__ void __launch_bounds__(64 * WAVES, 8 / WAVES)  // 2 wavefronts per SIMD
+__global__ void __launch_bounds__(64 * WAVES, D > 128 ? 1 : 8 / WAVES)  // 2 wavefronts per SIMD (1 at D = 256)
 attn_bwd_dq_v2(BwdArgs a) {
   typedef Mfma<T> M;
   typedef typename M::V V;
@@ -2079,8 +2093,13 @@ attn_bwd_dq_v2(BwdArgs a) {
   if (n_kv > 0) dma.issue(smem, kp, a.sk_s, vp, a.sv_s, 0, a.Tkv);
   for (int it = 0; it < n_kv; ++it) {
     const int kv0 = it * 64;
+    // accumulators in VGPRs (the softmax needs the rest); at head_dim 256
+    // they take the AGPRs, beside Q and dO in VGPRs
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) pin_vgpr(dq[mt]);
+    for (int mt = 0; mt < MT; ++mt) {
+      if constexpr (D > 128) pin_agpr(dq[mt]);
+      else pin_vgpr(dq[mt]);
+    }
     wait_vmcnt<0>();
     __syncthreads();
     if (it + 1 < n_kv)
@@ -2090,7 +2109,7 @@ attn_bwd_dq_v2(BwdArgs a) {
     const char* Vs = Ks + P::BYTES;
     const bool need_mask = kv0 + 64 > a.Tkv || (a.causal && kv0 + 63 > qw0);
 
-    f32x16 ds[2];
+    V dsb[4];  // dS^T rounded to T as formed: operand t holds rows 16t + 4g + {0..3}, 16t + 8 + ...
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       f32x16 s = zero16(), dp = zero16();
@@ -2110,16 +2129,13 @@ attn_bwd_dq_v2(BwdArgs a) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float p = fast_exp2(fmaf(s[r], sl2, -lse2));
-        ds[u][r] = p * (dp[r] - dl);
+        dsb[2 * u + (r >> 3)][r & 7] = (T)(p * (dp[r] - dl));
       }
     }
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-      V db;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) db[j] = (T)ds[t >> 1][8 * (t & 1) + j];
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) dq[mt] = M::mma(bt_tr<T, D>(Ks, 16 * t, mt), db, dq[mt]);
+      for (int mt = 0; mt < MT; ++mt) dq[mt] = M::mma(bt_tr<T, D>(Ks, 16 * t, mt), dsb[t], dq[mt]);
     }
   }
 
@@ -2702,7 +2718,7 @@ attn_bwd_dkdv_simt(BwdArgs a, int D) {
 }
 
 // ------------------------------------------------------------- host side --
-bool mfma_head_dim(int64_t d) { return d == 16 || d == 32 || d == 64 || d == 128; }
+bool mfma_head_dim(int64_t d) { return d == 16 || d == 32 || d == 64 || d == 128 || d == 256; }
 
 int simt_per_lane(int64_t d) {
   int pl = 1;
@@ -2743,11 +2759,13 @@ int fwd_mfma(const FwdArgs& a, int64_t D, hipStream_t st) {
     }
   }
 #endif
-  if (D == 64 || D == 128) {
+  if (D == 64 || D == 128 || D == 256) {
     FwdArgs x = a;
     x.n_tiles = (int)cdiv(a.Tq, kF2BM);
     const int64_t blocks = (int64_t)x.n_tiles * a.B * a.H;
-    if (D == 128)
+    if (D == 256)
+      attn_fwd_v2<T, 256><<<(unsigned)blocks, 64 * kF2Waves, 0, st>>>(x);
+    else if (D == 128)
       attn_fwd_v2<T, 128><<<(unsigned)blocks, 64 * kF2Waves, 0, st>>>(x);
     else
       attn_fwd_v2<T, 64><<<(unsigned)blocks, 64 * kF2Waves, 0, st>>>(x);
@@ -2842,8 +2860,15 @@ int bwd_v2(const BwdArgs& a, hipStream_t st) {
   }
   x.n_tiles = (int)cdiv(a.Tkv, 32 * WK);
   const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;
-  attn_bwd_dkdv_v2<T, D, WK><<<(unsigned)kv_blocks, 64 * WK, 0, st>>>(x);
-  return check_launch("attention backward (dk/dv, mfma)");
+  if constexpr (D == 256) {  // dV, then dK: one pass does not fit the registers
+    attn_bwd_dkdv_v2<T, D, WK, 1><<<(unsigned)kv_blocks, 64 * WK, 0, st>>>(x);
+    if (int e = check_launch("attention backward (dv, mfma)")) return e;
+    attn_bwd_dkdv_v2<T, D, WK, 2><<<(unsigned)kv_blocks, 64 * WK, 0, st>>>(x);
+    return check_launch("attention backward (dk, mfma)");
+  } else {
+    attn_bwd_dkdv_v2<T, D, WK><<<(unsigned)kv_blocks, 64 * WK, 0, st>>>(x);
+    return check_launch("attention backward (dk/dv, mfma)");
+  }
 }
 
 template <typename T>
@@ -2866,6 +2891,7 @@ int bwd_mfma(const BwdArgs& a, int64_t D, hipStream_t st) {
 template <typename T>
 int bwd_impl(const BwdArgs& a, int64_t D, bool mfma, hipStream_t st) {
   if constexpr (!std::is_same<T, float>::value) {
+    if (mfma && D == 256) return bwd_v2<T, 256>(a, st);
     if (mfma && D == 128) return bwd_v2<T, 128>(a, st);
     if (mfma && D == 64) return bwd_v2<T, 64>(a, st);
   }

@@ -165,8 +165,10 @@ int tritium_adamw_step_mixed(const int64_t* table, int n_tensors, int64_t total_
  * {q_b, q_h, q_s, k_b, k_h, k_s, v_b, v_h, v_s, o_b, o_h, o_s} (host array).
  * lse: [B, H, Tq] float32, natural-log logsumexp of the scaled scores.
  * causal != 0 applies the top-left mask q_pos >= kv_pos; scale = D^-0.5.
- * bf16/fp16 with D in {16, 32, 64, 128} run on MFMA, anything else on the
- * SIMT path (D <= 1024). */
+ * bf16/fp16 with D in {16, 32, 64, 128, 256} run on MFMA, anything else on
+ * the SIMT path (D <= 1024).  (At D = 256 the backward's dK/dV runs as two
+ * launches, dV then dK, each forming S again: the fragments and accumulators
+ * of one pass would not fit a wavefront's registers.) */
 int tritium_attention_fwd(const void* q, const void* k, const void* v, void* o, float* lse,
                           int64_t B, int64_t H, int64_t Hkv, int64_t Tq, int64_t Tkv, int64_t D,
                           const int64_t* strides, int causal, int dtype, void* stream);

@@ -49,6 +49,16 @@ def test_attention_forward_backward(dtype, head_dim, batch, n_heads, seq):
     _check(dtype, batch, n_heads, n_heads, seq, seq, head_dim, True)
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("causal", [True, False])
+def test_attention_head_dim_256(dtype, causal):
+    # the MFMA path at head_dim 256 (forward kernel with one wavefront per SIMD,
+    # dQ kernel, dV and dK as two passes): several tiles, GQA, ragged lengths
+    _check(dtype, 2, 4, 4, 192, 192, 256, causal, seed=21)
+    _check(dtype, 1, 4, 2, 77, 130, 256, causal, seed=22)
+    _check(dtype, 1, 2, 2, 130, 70, 256, causal, seed=23, layout="bthd")
+
+
 @pytest.mark.parametrize("dtype", DTYPES)
 def test_attention_grouped_query(dtype):
     _check(dtype, 2, 8, 2, 128, 128, 64, True, seed=4)
