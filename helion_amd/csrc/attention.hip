@@ -1654,26 +1654,29 @@ constexpr int kDkvPPStages = 3;
 #endif
 constexpr int kDkvRing = TRI_ATTN_DKDV_RING;  // MFMA operands in flight ahead of use
 
+template <int D>
+struct PairLds {
+  static constexpr int STAGE = 2 * BTile<D>::BYTES + 512;  // Q, dO, lse[64], delta[64]
+  static constexpr int XCH = 2 * 4 * 64 * 16;  // per pair: 2 query halves x [4][64 lanes][4 fp32]
+};
+
+// The work of one (batch * kv head, kv tile) item; smem and xch_all are the
+// workgroup's LDS (PairLds sizes).
 template <typename T, int D, bool DS>
-__global__ void __launch_bounds__(64 * kPairWaves, 1)  // 2 wavefronts per SIMD
-attn_bwd_dkdv_pair(BwdArgs a) {
+__device__ __forceinline__ void dkdv_pair_item(const BwdArgs& a, char* smem, char* xch_all,
+                                               int bhk, int kt) {
   typedef Mfma<T> M;
   typedef typename M::V V;
   typedef BTile<D> P;
   constexpr int KS = D / 16;
   constexpr int MT = D / 32;
-  constexpr int STAGE = 2 * P::BYTES + 512;  // Q, dO, lse[64], delta[64]
-  constexpr int XCH = 2 * 4 * 64 * 16;       // per pair: 2 query halves x [4][64 lanes][4 fp32]
-  __shared__ __attribute__((aligned(1024))) char smem[kDkvPPStages * STAGE];
-  __shared__ __attribute__((aligned(16))) char xch_all[4 * XCH];
+  constexpr int STAGE = PairLds<D>::STAGE;
+  constexpr int XCH = PairLds<D>::XCH;
 
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int l32 = lane & 31, g = lane >> 5;
   const int pair = wave & 3;
   const bool role_b = wave >= 4;  // wave-uniform
-  const int w = xcd_remap(blockIdx.x, gridDim.x);
-  const int bhk = w / a.n_tiles;
-  const int kt = w % a.n_tiles;  // kt = 0 sees the most queries: heaviest first
   const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
   const int group = a.H / a.Hkv;
   const int kv0 = kt * kPairBN;
@@ -1964,6 +1967,39 @@ attn_bwd_dkdv_pair(BwdArgs a) {
                   acc[mt][4 * rr + 2] * sc, acc[mt][4 * rr + 3] * sc);
       }
     }
+  }
+}
+
+// dK, dV (and with DS the stored dS) over (batch * kv head, kv tile) items.
+// PERSIST: one workgroup per compute unit walks a fixed list of items
+// instead of one workgroup per item (a workgroup's turnaround on its compute
+// unit measured about 8 us, 10% of the config-3 kernel at 16 items per CU).
+// Each XCD (workgroups b with b % 8 == x) owns a contiguous eighth of the
+// (batch, kv head)s, so their Q / dO tiles stay in that XCD's L2; its
+// workgroups take the XCD's items round-robin, ordered head by head with the
+// kv-tile order reversed every other head, so that with as many workgroups
+// per XCD as kv tiles every workgroup pairs tile t with tile n - 1 - t and
+// all carry the same number of steps under the causal mask.
+template <typename T, int D, bool DS, bool PERSIST>
+__global__ void __launch_bounds__(64 * kPairWaves, 1)  // 2 wavefronts per SIMD
+attn_bwd_dkdv_pair(BwdArgs a) {
+  __shared__ __attribute__((aligned(1024))) char smem[kDkvPPStages * PairLds<D>::STAGE];
+  __shared__ __attribute__((aligned(16))) char xch_all[4 * PairLds<D>::XCH];
+  if constexpr (PERSIST) {
+    const int per = a.B * a.Hkv / kXcds;  // the host checks divisibility
+    const int slots = (int)gridDim.x / kXcds;
+    const int x = (int)blockIdx.x % kXcds, slot = (int)blockIdx.x / kXcds;
+    const int n_items = per * a.n_tiles;
+    for (int it = slot; it < n_items; it += slots) {
+      const int j = it / a.n_tiles, kk = it % a.n_tiles;
+      const int kt = (j & 1) ? a.n_tiles - 1 - kk : kk;
+      dkdv_pair_item<T, D, DS>(a, smem, xch_all, x * per + j, kt);
+      lds_barrier();  // every wavefront is done with the LDS before the next item's DMAs
+    }
+  } else {
+    const int w = xcd_remap(blockIdx.x, gridDim.x);
+    // kt = 0 sees the most queries: heaviest first
+    dkdv_pair_item<T, D, DS>(a, smem, xch_all, w / a.n_tiles, w % a.n_tiles);
   }
 }
 
@@ -2799,6 +2835,27 @@ int fwd_simt(const FwdArgs& a, int64_t D, hipStream_t st) {
 #define TRI_ATTN_DQ_WAVES 4
 #endif
 
+#ifndef TRI_ATTN_DKDV_PERSIST
+#define TRI_ATTN_DKDV_PERSIST 1
+#endif
+
+// The dK/dV pair kernel over x.n_tiles kv tiles of every (batch, kv head):
+// persistent (one workgroup per compute unit) when the (batch, kv head)s
+// split evenly over the XCDs and there are at least two items per compute
+// unit, else one workgroup per item.
+template <typename T, int D, bool DS>
+int launch_dkdv_pair(const BwdArgs& x, hipStream_t st) {
+  const int64_t n_bhk = (int64_t)x.B * x.Hkv;
+  const int64_t items = n_bhk * x.n_tiles;
+  const int cus = cu_count();
+  if (TRI_ATTN_DKDV_PERSIST && n_bhk % kXcds == 0 && cus % kXcds == 0 && items >= 2 * (int64_t)cus)
+    attn_bwd_dkdv_pair<T, D, DS, true><<<(unsigned)cus, 64 * kPairWaves, 0, st>>>(x);
+  else
+    attn_bwd_dkdv_pair<T, D, DS, false><<<(unsigned)items, 64 * kPairWaves, 0, st>>>(x);
+  return check_launch(DS ? "attention backward (dk/dv storing ds)"
+                         : "attention backward (dk/dv, mfma pairs)");
+}
+
 // Stored-dS path (head_dim 128): delta (and with RoPE the rotated q), then
 // dK/dV storing dS, then dQ from the stored dS.  (At head_dim 64 the
 // recompute costs half as much and the stored path measured slower: GPT
@@ -2817,9 +2874,7 @@ int bwd_ds(const BwdArgs& a, hipStream_t st) {
   }
   static_assert(D == 128, "stored-dS backward: head_dim 128");
   x.n_tiles = (int)cdiv(a.Tkv, kPairBN);
-  const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;
-  attn_bwd_dkdv_pair<T, D, true><<<(unsigned)kv_blocks, 64 * kPairWaves, 0, st>>>(x);
-  if (int e = check_launch("attention backward (dk/dv storing ds)")) return e;
+  if (int e = launch_dkdv_pair<T, D, true>(x, st)) return e;
   x.q = a.q;  // dQ from dS reads K and dS only; the row strides of q stay the caller's
   x.sq_s = a.sq_s;
   x.sq_h = a.sq_h;
@@ -2854,9 +2909,7 @@ int bwd_v2(const BwdArgs& a, hipStream_t st) {
   // 0.30 ms at [16, 12, 1024, 64], 1.35 vs 1.60 ms at [4, 32, 4096, 64])
   if constexpr (TRI_ATTN_DKDV_PAIR && D == 128) {
     x.n_tiles = (int)cdiv(a.Tkv, kPairBN);
-    const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;
-    attn_bwd_dkdv_pair<T, D, false><<<(unsigned)kv_blocks, 64 * kPairWaves, 0, st>>>(x);
-    return check_launch("attention backward (dk/dv, mfma pairs)");
+    return launch_dkdv_pair<T, D, false>(x, st);
   }
   x.n_tiles = (int)cdiv(a.Tkv, 32 * WK);
   const int64_t kv_blocks = (int64_t)x.n_tiles * a.B * a.Hkv;
