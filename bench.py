@@ -893,7 +893,9 @@ def stream_probe(torch, tritium, reps: int = 10):
              ("read 1 GiB, grid-covering", 4, (a, sink, None, None), n, 1 << 30, (0,)),
              ("copy 1 GiB, grid-covering", 5, (a, b, None, None), n, 2 << 30, (0,)),
              ("fill 1 GiB, grid-covering", 6, (b, None, None, None), n, 1 << 30, (0,)),
-             ("2 read + 1 write of 1 GiB, grid-covering", 7, (a, b, c, None), n, 3 << 30, (0,))]
+             ("2 read + 1 write of 1 GiB, grid-covering", 7, (a, b, c, None), n, 3 << 30, (0,)),
+             ("adamw-shaped 4 read + 3 write, grid-covering (workgroup lanes)", 8, (p, g, m, v),
+              npar // 4, 28 * npar, (64, 256))]
     s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     out = []
     for name, pat, bufs, nv, nbytes, grids in cases:
@@ -910,7 +912,7 @@ def stream_probe(torch, tritium, reps: int = 10):
                 torch.cuda.synchronize()
                 times.append(s.elapsed_time(e))
             ms = statistics.median(times[1:])
-            key = f"GB/s b{blocks}" if blocks else "GB/s"
+            key = (f"GB/s {blocks} lanes" if pat == 8 else f"GB/s b{blocks}") if blocks else "GB/s"
             row[key] = round(nbytes / (ms * 1e-3) / 1e9, 1)
         row["best_frac_of_8TB/s"] = round(max(vv for k, vv in row.items() if k.startswith("GB/s"))
                                           / HBM_PEAK_GBS, 4)

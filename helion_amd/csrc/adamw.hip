@@ -26,33 +26,15 @@ namespace {
 
 // One wavefront per workgroup: config-2 update 612-618 -> 586-595 us against
 // 256 lanes (128: 607-617, 512: 620-623, 1024: 651-653), on the same boxes.
-#ifndef TRI_ADAMW_BLOCK
-#define TRI_ADAMW_BLOCK 64
-#endif
-constexpr int kBlock = TRI_ADAMW_BLOCK;
-#ifndef TRI_ADAMW_VEC_PER_THREAD
-#define TRI_ADAMW_VEC_PER_THREAD 1
-#endif
-constexpr int kVecPerThread = TRI_ADAMW_VEC_PER_THREAD;
-constexpr int64_t kChunk = (int64_t)kBlock * kVecPerThread * 8;  // 512 elements
+constexpr int kBlock = 64;
+// 512 elements per workgroup (two groups of 4 per lane): 256 and 1024
+// measured the same or slower (0.560-0.586 and 0.567 ms against 0.566 ms
+// for the config-2 update, same box).
+constexpr int64_t kChunk = 512;
 // The mixed-precision kernel (four fp32 and two 16-bit streams per element)
 // streams best with four 8-element steps per lane: 820 vs 839 us per GPT
-// step with two, 860 with eight; the fp32 kernels are fastest at kChunk.
-// A lane issues its 16-byte loads stream by stream (all of its p vectors,
-// then g, m, v) and its stores likewise (m, v, p), rather than the four
-// streams of one vector together: config-2 step 611-614 -> 599-607 us
-// (loads alone 606-609), on the same boxes; with one vector per lane per
-// stream rather than two, 599-601.
-#ifndef TRI_ADAMW_STREAM_MAJOR
-#define TRI_ADAMW_STREAM_MAJOR 1
-#endif
-#ifndef TRI_ADAMW_STORE_MAJOR
-#define TRI_ADAMW_STORE_MAJOR 1
-#endif
-#ifndef TRI_ADAMW_MIXED_STEPS
-#define TRI_ADAMW_MIXED_STEPS 4
-#endif
-constexpr int64_t kChunkMixed = (int64_t)kBlock * TRI_ADAMW_MIXED_STEPS * 8;  // 2048 elements
+// step with two, 860 with eight.
+constexpr int64_t kChunkMixed = (int64_t)kBlock * 4 * 8;  // 2048 elements
 
 struct Hyper {
   float lr, beta1, beta2, eps, weight_decay, bc1, bc2;
@@ -67,7 +49,38 @@ __device__ __forceinline__ void adam_update(float& p, float g, float& m, float& 
   p = p - step_size * m / denom;
 }
 
+// Four consecutive elements of T as fp32, and back: one 16-byte access for
+// fp32, 8 bytes for 16-bit types, both with the nontemporal hint.
+template <typename T>
+__device__ __forceinline__ void load4_nt(const T* __restrict__ p, float (&f)[4]) {
+  if constexpr (sizeof(T) == 4) {
+    unpack<float>(ld16_nt(p), f);
+  } else {
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    const u32x2 u = __builtin_nontemporal_load(reinterpret_cast<const u32x2*>(p));
+    const Pack<T, 4> pk = __builtin_bit_cast(Pack<T, 4>, u);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) f[i] = to_f32(pk.v[i]);
+  }
+}
+template <typename T>
+__device__ __forceinline__ void store4_nt(T* __restrict__ p, const float (&f)[4]) {
+  if constexpr (sizeof(T) == 4) {
+    st16_nt(p, pack<float>(f));
+  } else {
+    Pack<T, 4> pk;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) pk.v[i] = from_f32<T>(f[i]);
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    __builtin_nontemporal_store(__builtin_bit_cast(u32x2, pk), reinterpret_cast<u32x2*>(p));
+  }
+}
+
 // Update elements [start, start + kChunk) of one tensor (clipped to n).
+// With 16-byte aligned tensors each lane owns kSteps groups of 4 consecutive
+// elements, kBlock groups apart, and issues its loads stream by stream (its
+// p groups, then g, m, v) and its stores likewise (m, v, p); elements past
+// the last whole group of 4 go one per lane.
 template <typename T>
 __device__ __forceinline__ void adam_chunk(T* __restrict__ p, const T* __restrict__ g,
                                            float* __restrict__ m, float* __restrict__ v,
@@ -75,95 +88,47 @@ __device__ __forceinline__ void adam_chunk(T* __restrict__ p, const T* __restric
                                            const Hyper& h) {
   const float lr_wd = h.lr * h.weight_decay;
   const float step_size = h.lr / h.bc1;
-  constexpr int VEC = 16 / sizeof(T);
   const int64_t end = min(start + kChunk, n);
+  int64_t tail = start;
   if (vec_ok) {
-    // chunk starts are multiples of kChunk, hence of VEC; only the last chunk
-    // of a tensor can end inside a vector (handled element-wise below)
-    const int64_t vec_end = start + ((end - start) / VEC) * VEC;
-    constexpr int NVEC = (int)(kChunk / VEC / kBlock);
-    float pv[NVEC][VEC], gv[NVEC][VEC], mv[NVEC][VEC], vv[NVEC][VEC];
-#if TRI_ADAMW_STREAM_MAJOR
+    constexpr int NS = (int)(kChunk / (4 * kBlock));
+    static_assert(NS * 4 * kBlock == kChunk, "chunk = whole groups of 4 per lane");
+    const int64_t vec_end = start + ((end - start) / 4) * 4;
+    float pv[NS][4], gv[NS][4], mv[NS][4], vv[NS][4];
+    auto elem = [&](int u) { return start + ((int64_t)u * kBlock + threadIdx.x) * 4; };
 #pragma unroll
-    for (int u = 0; u < NVEC; ++u) {
-      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
-      if (e < vec_end) load_stream<T, VEC>(p + e, pv[u]);
-    }
+    for (int u = 0; u < NS; ++u)
+      if (elem(u) < vec_end) load4_nt<T>(p + elem(u), pv[u]);
 #pragma unroll
-    for (int u = 0; u < NVEC; ++u) {
-      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
-      if (e < vec_end) load_stream<T, VEC>(g + e, gv[u]);
-    }
+    for (int u = 0; u < NS; ++u)
+      if (elem(u) < vec_end) load4_nt<T>(g + elem(u), gv[u]);
 #pragma unroll
-    for (int u = 0; u < NVEC; ++u) {
-      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
-      if (e < vec_end) load_stream<float, VEC>(m + e, mv[u]);
-    }
+    for (int u = 0; u < NS; ++u)
+      if (elem(u) < vec_end) load4_nt<float>(m + elem(u), mv[u]);
 #pragma unroll
-    for (int u = 0; u < NVEC; ++u) {
-      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
-      if (e < vec_end) load_stream<float, VEC>(v + e, vv[u]);
-    }
-#else
+    for (int u = 0; u < NS; ++u)
+      if (elem(u) < vec_end) load4_nt<float>(v + elem(u), vv[u]);
 #pragma unroll
-    for (int u = 0; u < NVEC; ++u) {
-      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
-      if (e < vec_end) {
-        load_stream<T, VEC>(p + e, pv[u]);
-        load_stream<T, VEC>(g + e, gv[u]);
-        load_stream<float, VEC>(m + e, mv[u]);
-        load_stream<float, VEC>(v + e, vv[u]);
-      }
-    }
-#endif
-#if TRI_ADAMW_STORE_MAJOR
+    for (int u = 0; u < NS; ++u)
 #pragma unroll
-    for (int u = 0; u < NVEC; ++u)
+      for (int i = 0; i < 4; ++i) adam_update(pv[u][i], gv[u][i], mv[u][i], vv[u][i], h, lr_wd, step_size);
 #pragma unroll
-      for (int i = 0; i < VEC; ++i) adam_update(pv[u][i], gv[u][i], mv[u][i], vv[u][i], h, lr_wd, step_size);
+    for (int u = 0; u < NS; ++u)
+      if (elem(u) < vec_end) store4_nt<float>(m + elem(u), mv[u]);
 #pragma unroll
-    for (int u = 0; u < NVEC; ++u) {
-      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
-      if (e < vec_end) store_stream<float, VEC>(m + e, mv[u]);
-    }
+    for (int u = 0; u < NS; ++u)
+      if (elem(u) < vec_end) store4_nt<float>(v + elem(u), vv[u]);
 #pragma unroll
-    for (int u = 0; u < NVEC; ++u) {
-      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
-      if (e < vec_end) store_stream<float, VEC>(v + e, vv[u]);
-    }
-#pragma unroll
-    for (int u = 0; u < NVEC; ++u) {
-      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
-      if (e < vec_end) store_stream<T, VEC>(p + e, pv[u]);
-    }
-#else
-#pragma unroll
-    for (int u = 0; u < NVEC; ++u) {
-      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * VEC;
-      if (e < vec_end) {
-#pragma unroll
-        for (int i = 0; i < VEC; ++i) adam_update(pv[u][i], gv[u][i], mv[u][i], vv[u][i], h, lr_wd, step_size);
-        store_stream<float, VEC>(m + e, mv[u]);
-        store_stream<float, VEC>(v + e, vv[u]);
-        store_stream<T, VEC>(p + e, pv[u]);
-      }
-    }
-#endif
-    for (int64_t e = vec_end + threadIdx.x; e < end; e += kBlock) {
-      float pp = to_f32(p[e]), mm = m[e], vv2 = v[e];
-      adam_update(pp, to_f32(g[e]), mm, vv2, h, lr_wd, step_size);
-      m[e] = mm;
-      v[e] = vv2;
-      p[e] = from_f32<T>(pp);
-    }
-  } else {
-    for (int64_t e = start + threadIdx.x; e < end; e += kBlock) {
-      float pp = to_f32(p[e]), mm = m[e], vv2 = v[e];
-      adam_update(pp, to_f32(g[e]), mm, vv2, h, lr_wd, step_size);
-      m[e] = mm;
-      v[e] = vv2;
-      p[e] = from_f32<T>(pp);
-    }
+    for (int u = 0; u < NS; ++u)
+      if (elem(u) < vec_end) store4_nt<T>(p + elem(u), pv[u]);
+    tail = vec_end;
+  }
+  for (int64_t e = tail + threadIdx.x; e < end; e += kBlock) {
+    float pp = to_f32(p[e]), mm = m[e], vv2 = v[e];
+    adam_update(pp, to_f32(g[e]), mm, vv2, h, lr_wd, step_size);
+    m[e] = mm;
+    v[e] = vv2;
+    p[e] = from_f32<T>(pp);
   }
 }
 

@@ -708,20 +708,13 @@ struct BtOffs {
 // global_load_lds_dwordx4 into two LDS stages (the next tile streams in
 // while the current one is multiplied); rows are XOR-swizzled per tile so
 // that both the 16-byte K reads and the transposing V reads are conflict-free.
-#ifndef TRI_ATTN_FWD_WAVES
-#define TRI_ATTN_FWD_WAVES 4
-#endif
-constexpr int kF2Waves = TRI_ATTN_FWD_WAVES;
+constexpr int kF2Waves = 4;
 constexpr int kF2BM = 32 * kF2Waves;  // query rows per workgroup
 constexpr int kF2BN = 64;             // K/V rows per tile
-#ifndef TRI_ATTN_RING
-#define TRI_ATTN_RING 4
-#endif
-constexpr int kRing = TRI_ATTN_RING;  // MFMA operands in flight ahead of use
-#ifndef TRI_ATTN_FWD_STAGES
-#define TRI_ATTN_FWD_STAGES 2
-#endif
-constexpr int kF2Stages = TRI_ATTN_FWD_STAGES;  // K/V tiles in the LDS ring
+// MFMA operands in flight ahead of use (8 measured within 2% at head_dim 64)
+constexpr int kRing = 4;
+// K/V tiles in the LDS ring (3 measured 9% slower at the GPT block's shape)
+constexpr int kF2Stages = 2;
 
 template <typename T, int D>
 __global__ void __launch_bounds__(64 * kF2Waves, D > 128 ? 1 : 8 / kF2Waves)  // 2 wavefronts per SIMD (1 at D = 256)
@@ -911,15 +904,9 @@ attn_fwd_v2(FwdArgs a) {
 // flight across them.  Each wavefront owns 32 query rows; the two groups
 // take alternate 32-row blocks so that near the causal diagonal both stop
 // within a tile of each other.
-#ifndef TRI_ATTN_FWD_PP
-#define TRI_ATTN_FWD_PP 1
-#endif
 constexpr int kPPWaves = 8;
 constexpr int kPPBM = 32 * kPPWaves;  // query rows per workgroup
 constexpr int kPPStages = 4;          // tile j + 2 streams in during iteration j
-#ifndef TRI_ATTN_PP_PRIO
-#define TRI_ATTN_PP_PRIO 1
-#endif
 
 // MFMA phase of the ping-pong forward: O^T += V^T P^T over the previous
 // tile (DPV; MFMA i = MT t + mt, t the 16-row slice of the tile), then
@@ -1051,15 +1038,11 @@ attn_fwd_pp(FwdArgs a) {
     if (grp == 1) lds_barrier();
     for (int j = 0; j <= n_kv; ++j) {
       f32x16 s[2];
-#if TRI_ATTN_PP_PRIO
       __builtin_amdgcn_s_setprio(1);
-#endif
       pp_mfma<T, D>(j >= 1 && j <= n_w, j < n_w,
                     smem + ((j + kPPStages - 1) % kPPStages) * STAGE + P::BYTES,
                     smem + (j % kPPStages) * STAGE, fo, qf, pb, rb, s, o);
-#if TRI_ATTN_PP_PRIO
       __builtin_amdgcn_s_setprio(0);
-#endif
       lds_barrier();
 
       if (j + 2 < n_kv) dma.issue(slot0 + ((j + 2) % kPPStages) * STAGE, xp, sx, (j + 2) * 64, a.Tkv);
@@ -1447,9 +1430,6 @@ attn_bwd_dq_mfma(BwdArgs a) {
   }
 }
 
-#ifndef TRI_DKDV_FENCES
-#define TRI_DKDV_FENCES 0
-#endif
 
 // dK, dV: a workgroup owns 32 * WAVES kv rows of one (batch, kv head), a
 // wavefront 32 of them (K, V fragments in registers, lane = kv row), and
@@ -1563,7 +1543,6 @@ attn_bwd_dkdv_v2(BwdArgs a) {
       __builtin_amdgcn_s_setprio(0);
       // phases are fenced so that no more than one phase's LDS fragments
       // are live at a time (the wavefront's registers hold K, V, dK, dV)
-      if (TRI_DKDV_FENCES) sched_fence();
       // s[r] = S[q0 + 32mq + 8(r/4) + 4g + r%4][kvw]; masked scores -> -inf (p = 0)
       if (need_mask) {
 #pragma unroll
@@ -1587,7 +1566,6 @@ attn_bwd_dkdv_v2(BwdArgs a) {
           dp[r] = p * (dp[r] - dlv[j]);
         }
       }
-      if (TRI_DKDV_FENCES) sched_fence();
       __builtin_amdgcn_s_setprio(1);
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -1604,7 +1582,6 @@ attn_bwd_dkdv_v2(BwdArgs a) {
         }
       }
       __builtin_amdgcn_s_setprio(0);
-      if (TRI_DKDV_FENCES) sched_fence();
     }
   }
 
@@ -1649,10 +1626,7 @@ attn_bwd_dkdv_v2(BwdArgs a) {
 constexpr int kPairWaves = 8;
 constexpr int kPairBN = 128;
 constexpr int kDkvPPStages = 3;
-#ifndef TRI_ATTN_DKDV_RING
-#define TRI_ATTN_DKDV_RING 8
-#endif
-constexpr int kDkvRing = TRI_ATTN_DKDV_RING;  // MFMA operands in flight ahead of use
+constexpr int kDkvRing = 8;  // MFMA operands in flight ahead of use
 
 template <int D>
 struct PairLds {
@@ -1838,13 +1812,9 @@ __device__ __forceinline__ void dkdv_pair_item(const BwdArgs& a, char* smem, cha
       const bool inter = nxt && prev && ld_fast();
       if (nxt && !inter) issue_all();
       if (inter) issue_stats();
-#if TRI_ATTN_PP_PRIO
       __builtin_amdgcn_s_setprio(1);
-#endif
       mfma_phase(prev, cur, inter, fo.tr_base(smem + sp * STAGE + P::BYTES), stc, op, x);
-#if TRI_ATTN_PP_PRIO
       __builtin_amdgcn_s_setprio(0);
-#endif
       if (nxt) advance();
       lds_barrier();
       // half-step 2s + 1: P_s (lse_s scaled by log2 e in half-step 2s)
@@ -1938,13 +1908,9 @@ __device__ __forceinline__ void dkdv_pair_item(const BwdArgs& a, char* smem, cha
       }
       lds_barrier();
       // half-step 2s + 1: dK^T += Q_{s-1}^T dS_{s-1}, dP_s = dO_s V^T
-#if TRI_ATTN_PP_PRIO
       __builtin_amdgcn_s_setprio(1);
-#endif
       mfma_phase(prev, cur, false, qb, stc + P::BYTES, op, x);
-#if TRI_ATTN_PP_PRIO
       __builtin_amdgcn_s_setprio(0);
-#endif
       lds_barrier();
       q0p = q0c;
       hp = hc;
@@ -2248,10 +2214,7 @@ attn_bwd_delta_v(BwdArgs a) {
 // reads (k = kv rows).
 constexpr int kDsWaves = 8;
 constexpr int kDsTiles = 4;  // query tiles per workgroup
-#ifndef TRI_ATTN_DQDS_STAGES
-#define TRI_ATTN_DQDS_STAGES 3
-#endif
-constexpr int kDsStages = TRI_ATTN_DQDS_STAGES;
+constexpr int kDsStages = 3;  // 2 measured 0.670 against 0.545 ms at config 3
 
 template <typename T, int D>
 __global__ void __launch_bounds__(64 * kDsWaves, 1)
@@ -2779,7 +2742,6 @@ int simt_per_lane(int64_t d) {
 
 template <typename T>
 int fwd_mfma(const FwdArgs& a, int64_t D, hipStream_t st) {
-#if TRI_ATTN_FWD_PP
   // The ping-pong kernel (one 8-wavefront workgroup per CU, two 256-row
   // query tiles each) measured faster than attn_fwd_v2 only for D = 128
   // with at least 4 workgroups per CU; with fewer the CUs run out of
@@ -2794,7 +2756,6 @@ int fwd_mfma(const FwdArgs& a, int64_t D, hipStream_t st) {
       return check_launch("attention forward (mfma)");
     }
   }
-#endif
   if (D == 64 || D == 128 || D == 256) {
     FwdArgs x = a;
     x.n_tiles = (int)cdiv(a.Tq, kF2BM);
@@ -2825,19 +2786,9 @@ int fwd_simt(const FwdArgs& a, int64_t D, hipStream_t st) {
   return check_launch("attention forward (simt)");
 }
 
-#ifndef TRI_ATTN_DKDV_WAVES
-#define TRI_ATTN_DKDV_WAVES 4
-#endif
-#ifndef TRI_ATTN_DKDV_PAIR
-#define TRI_ATTN_DKDV_PAIR 1
-#endif
-#ifndef TRI_ATTN_DQ_WAVES
-#define TRI_ATTN_DQ_WAVES 4
-#endif
-
-#ifndef TRI_ATTN_DKDV_PERSIST
-#define TRI_ATTN_DKDV_PERSIST 1
-#endif
+// Wavefronts per workgroup of the one-role dK/dV and the dQ kernels (8
+// measured no faster at the GPT block's shape; dQ 7% slower).
+constexpr int kDkvWaves = 4, kDqWaves = 4;
 
 // The dK/dV pair kernel over x.n_tiles kv tiles of every (batch, kv head):
 // persistent (one workgroup per compute unit) when the (batch, kv head)s
@@ -2848,7 +2799,7 @@ int launch_dkdv_pair(const BwdArgs& x, hipStream_t st) {
   const int64_t n_bhk = (int64_t)x.B * x.Hkv;
   const int64_t items = n_bhk * x.n_tiles;
   const int cus = cu_count();
-  if (TRI_ATTN_DKDV_PERSIST && n_bhk % kXcds == 0 && cus % kXcds == 0 && items >= 2 * (int64_t)cus)
+  if (n_bhk % kXcds == 0 && cus % kXcds == 0 && items >= 2 * (int64_t)cus)
     attn_bwd_dkdv_pair<T, D, DS, true><<<(unsigned)cus, 64 * kPairWaves, 0, st>>>(x);
   else
     attn_bwd_dkdv_pair<T, D, DS, false><<<(unsigned)items, 64 * kPairWaves, 0, st>>>(x);
@@ -2888,7 +2839,7 @@ int bwd_ds(const BwdArgs& a, hipStream_t st) {
 // dQ first: it also computes delta, which the dK/dV kernel reads.
 template <typename T, int D>
 int bwd_v2(const BwdArgs& a, hipStream_t st) {
-  constexpr int WK = TRI_ATTN_DKDV_WAVES, WQ = TRI_ATTN_DQ_WAVES;
+  constexpr int WK = kDkvWaves, WQ = kDqWaves;
   if constexpr (D == 128) {
     if (a.ds != nullptr) return bwd_ds<T, D>(a, st);
   }
@@ -2907,7 +2858,7 @@ int bwd_v2(const BwdArgs& a, hipStream_t st) {
   // for the same VALU work, and one wavefront doing both roles with its
   // K and V fragments (attn_bwd_dkdv_v2) measured faster there (0.27 vs
   // 0.30 ms at [16, 12, 1024, 64], 1.35 vs 1.60 ms at [4, 32, 4096, 64])
-  if constexpr (TRI_ATTN_DKDV_PAIR && D == 128) {
+  if constexpr (D == 128) {
     x.n_tiles = (int)cdiv(a.Tkv, kPairBN);
     return launch_dkdv_pair<T, D, false>(x, st);
   }
@@ -3083,7 +3034,7 @@ int attention_bwd(const void* dout, const void* q, const void* k, const void* v,
     if (q_rot == nullptr || !aligned16(q_rot))
       return fail(TRI_EINVAL, "attention backward with rope: q_rot workspace missing or unaligned");
   }
-  if (ds_ws != nullptr && mfma && TRI_ATTN_DKDV_PAIR) {
+  if (ds_ws != nullptr && mfma) {
     const size_t need = ds_workspace_bytes(B, H, Tq, Tkv, D, causal, dtype);
     if (need > 0) {
       if (ds_bytes < need || !aligned16(ds_ws))

@@ -21,7 +21,7 @@
 // the C layout of v_mfma_f32_32x32x16_{bf16,f16}.
 //
 // Pipeline: K is walked in tiles of RB bytes per row (64 or 128: 32 or 64
-// 16-bit elements) through STAGES LDS buffers.  Tiles are fetched with
+// 16-bit elements) through two LDS buffers.  Tiles are fetched with
 // global_load_lds_dwordx4 (straight into LDS, no staging registers): lane i
 // of an instruction fills bytes [16 i, 16 i + 16) of a 1 KiB run, which covers
 // 1024 / RB rows; each lane picks which 16-byte granule it fetches so that the rows
@@ -30,8 +30,8 @@
 // One barrier per K tile.  16-bit types run the cross-tile loop (xt_loop):
 // the barrier that publishes tile kt + 1 sits before the MFMAs of tile kt's
 // last 16-deep step and tile kt + 1's first fragments are read under them;
-// the other loops wait for tile kt, sync, issue tile kt + STAGES - 1 into
-// the buffer read at step kt - 1, then compute.
+// fp32 (planned_loop) waits for tile kt, syncs, issues tile kt + 1 into the
+// buffer read at step kt - 1, then computes.
 // Rows past M (N) re-read the last valid row (their results are never
 // stored); a partial last K tile is zero-filled through registers and done
 // first, so the pipelined loop has no bounds checks.
@@ -142,70 +142,6 @@ struct Problem {
   int64_t M, N, K;
 };
 
-// Source of the 16 bytes that land at byte 16 * lane of 1 KiB run `run` of
-// an operand tile (K-contiguous: DMA_ROWS rows of RB bytes; MN-contiguous:
-// 1024 / (2 X) k-rows of X elements).
-template <class C, typename T, bool TR, int X>
-__device__ __forceinline__ const T* run_src(const void* base, int64_t ld, int64_t x0, int64_t xn,
-                                            int64_t k0, int run, int lane) {
-  constexpr int VE = vec<T>();
-  if constexpr (!TR) {
-    const int trow = run * C::DMA_ROWS + lane / C::GRAN;
-    const int c = (lane % C::GRAN) ^ swz_key<C>(trow);
-    return (const T*)base + imin(x0 + trow, xn - 1) * ld + k0 + c * VE;
-  } else {
-    constexpr int XG = X / 8;  // granules per k-row
-    static_assert(XG <= 64 && 64 % XG == 0, "k-rows of at most 1 KiB");
-    const int krow = run * (64 / XG) + lane / XG;
-    const int c = (lane % XG) ^ tkey(krow);
-    const int64_t last = ((xn + 7) & ~(int64_t)7) - 8;  // last granule of round_up(xn, 8)
-    return (const T*)base + (k0 + krow) * ld + imin(x0 + c * VE, last);
-  }
-}
-
-// DMA q of this wavefront's share of K tile k0 into one LDS stage: every
-// wavefront issues PA runs of the A tile, then PB runs of the B tile, so the
-// operand of each DMA is known at compile time (no branch, and no per-lane
-// select between the operands' pointers, which the compiler had routed
-// through a stack array).
-template <class C, typename T, int Q, bool TA, bool TB>
-__device__ __forceinline__ void dma_one(char* stage, const Problem& p, int64_t m0, int64_t n0,
-                                        int64_t k0, int lane, int wave) {
-  constexpr int W = C::WM * C::WN;
-  constexpr int RUNS_A = C::BM / C::DMA_ROWS, RUNS_B = C::BN / C::DMA_ROWS;
-  constexpr int PA = RUNS_A / W, PB = RUNS_B / W;
-  static_assert(PA * W == RUNS_A && PB * W == RUNS_B && PA + PB == C::DMA_PER_WAVE,
-                "each operand's runs split evenly over the wavefronts");
-  if constexpr (Q < PA) {
-    const int run = wave * PA + Q;
-    const T* src = run_src<C, T, TA, C::BM>(p.a, p.lda, m0, p.M, k0, run, lane);
-    dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(stage + run * 1024)));
-  } else {
-    const int run = wave * PB + (Q - PA);
-    const T* src = run_src<C, T, TB, C::BN>(p.b, p.ldb, n0, p.N, k0, run, lane);
-    dma16(src, __builtin_amdgcn_readfirstlane(lds_addr(stage + (RUNS_A + run) * 1024)));
-  }
-}
-
-template <class C, typename T, int Q, int Q1, bool TA, bool TB>
-__device__ __forceinline__ void dma_range(char* stage, const Problem& p, int64_t m0, int64_t n0,
-                                          int64_t k0, int lane, int wave) {
-  if constexpr (Q < Q1) {
-    dma_one<C, T, Q, TA, TB>(stage, p, m0, n0, k0, lane, wave);
-    dma_range<C, T, Q + 1, Q1, TA, TB>(stage, p, m0, n0, k0, lane, wave);
-  }
-}
-
-// Issue DMAs [Q0, Q1) of this wavefront's share of K tile k0 (both
-// operands) into one LDS stage; dma_tile issues all of them.
-template <class C, typename T, int Q0 = 0, int Q1 = C::DMA_PER_WAVE, bool TA = false,
-          bool TB = false>
-__device__ __forceinline__ void dma_tile(char* stage, const Problem& p, int64_t m0, int64_t n0,
-                                         int64_t k0) {
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  dma_range<C, T, Q0, Q1, TA, TB>(stage, p, m0, n0, k0, lane, wave);
-}
-
 // One operand of the partial last K tile, MN-contiguous: k-rows past K are
 // zero, columns clamped like the DMA's.
 template <class C, typename T, int X>
@@ -260,41 +196,6 @@ __device__ __forceinline__ void reg_tile(char* stage, const Problem& p, int64_t 
 #pragma unroll
     for (int e = 0; e < VE; ++e) pk.v[e] = (k + e < p.K) ? src[k + e] : (T)0.f;
     *reinterpret_cast<Pack<T, VE>*>(stage + swz<C>(row, c)) = pk;
-  }
-}
-
-// Register-staged copy of one K tile: global loads into VGPRs (issued early),
-// LDS stores later (after the MFMAs of the current tile).
-template <class C>
-struct Stage {
-  static constexpr int N = (C::BM + C::BN) * C::GRAN / C::THREADS;
-  uint4 v[N];
-};
-
-template <class C, typename T>
-__device__ __forceinline__ void stage_load(Stage<C>& st, const Problem& p, int64_t m0, int64_t n0,
-                                           int64_t k0) {
-  constexpr int VE = vec<T>();
-#pragma unroll
-  for (int q = 0; q < Stage<C>::N; ++q) {
-    const int idx = q * C::THREADS + threadIdx.x;
-    const int row = idx / C::GRAN, c = idx % C::GRAN;  // row-uniform per 8 or 4 lanes
-    const T* src;
-    if (row < C::BM) {
-      src = (const T*)p.a + imin(m0 + row, p.M - 1) * p.lda;
-    } else {
-      src = (const T*)p.b + imin(n0 + row - C::BM, p.N - 1) * p.ldb;
-    }
-    st.v[q] = *reinterpret_cast<const uint4*>(src + k0 + c * VE);
-  }
-}
-
-template <class C>
-__device__ __forceinline__ void stage_store(const Stage<C>& st, char* stage) {
-#pragma unroll
-  for (int q = 0; q < Stage<C>::N; ++q) {
-    const int idx = q * C::THREADS + threadIdx.x;
-    *reinterpret_cast<uint4*>(stage + swz<C>(idx / C::GRAN, idx % C::GRAN)) = st.v[q];
   }
 }
 
@@ -421,10 +322,8 @@ __device__ __forceinline__ void compute_tile(const char* stage, Acc<C>& acc, int
 // dealt round-robin to the 8 XCDs; each XCD gets a contiguous range of work
 // items, walked in groups of GROUP_M row tiles column by column so that the
 // blocks resident on one XCD share A and B tiles in its L2.
-#ifndef TRI_GEMM_GROUP_M
-#define TRI_GEMM_GROUP_M 4
-#endif
-template <int GROUP_M = TRI_GEMM_GROUP_M>
+// (groups of 2 or 8 row tiles measured 1-3% slower on config 4's linear-CE)
+template <int GROUP_M = 4>
 __device__ __forceinline__ void tile_of(int64_t bid, int64_t n_blocks, int tiles_m, int tiles_n,
                                         int& tm, int& tn) {
   int64_t w = bid;
@@ -438,46 +337,13 @@ __device__ __forceinline__ void tile_of(int64_t bid, int64_t n_blocks, int tiles
   tn = (int)(in_group / gsize);
 }
 
-#ifndef TRI_GEMM_DMA
-#define TRI_GEMM_DMA 1
-#endif
-
-// compute_tile hook: DMAs of the next K tile, DMA_PER_WAVE / KS of them
-// after each 16-deep step
-// How many of a wavefront's DMAs follow each 16-deep step, as decimal digits
-// of TRI_GEMM_SPREAD read from the first step; the remaining DMAs follow the
-// last step.  4400 (four after each of the first two steps) measured 3.5%
-// faster than 2222 and 1.7% faster than 8000 on config 4's linear-CE: the
-// last DMAs of the next tile then have half a tile of MFMAs to land behind.
-#ifndef TRI_GEMM_SPREAD
-#define TRI_GEMM_SPREAD 4400
-#endif
-constexpr int spread_digit(int s, int ks) {
-  int v = TRI_GEMM_SPREAD;
-  for (int i = 0; i < ks - 1 - s; ++i) v /= 10;
-  return v % 10;
-}
-template <class C>
-constexpr int spread_first(int s) {
-  int q = 0;
-  for (int i = 0; i < s; ++i) q += spread_digit(i, C::RB / 32);
-  return q < C::DMA_PER_WAVE ? q : C::DMA_PER_WAVE;
-}
-
-template <class C, typename T, bool TA = false, bool TB = false>
-struct DmaSpread {
-  char* st;
-  const Problem* p;
-  int64_t m0, n0, k0;
-  template <int S>
-  __device__ __forceinline__ void step() const {
-    constexpr int KS = C::RB / 32;
-    constexpr int Q0 = spread_first<C>(S);
-    constexpr int Q1 = S + 1 == KS ? C::DMA_PER_WAVE : spread_first<C>(S + 1);
-    if constexpr (Q0 < Q1) dma_tile<C, T, Q0, Q1, TA, TB>(st, *p, m0, n0, k0);
-  }
-};
-
+// DMA pattern of the fp32 loop (planned_loop): how many of a wavefront's
+// DMAs follow each 16-deep step, as decimal digits read from the first step;
+// 4400 (four after each of the first two steps) measured 3.5% faster than
+// 2222 and 1.7% faster than 8000 on config 4's linear-CE in that loop's
+// 16-bit form: the next tile's last DMAs have half a tile of MFMAs to land
+// behind.
+constexpr int kSpread = 4400;
 
 // DMA plan of the 2-stage loop for one output tile: each of this
 // wavefront's DMA_PER_WAVE runs (PA of A, then PB of B, as in dma_one) gets
@@ -602,10 +468,6 @@ __device__ __forceinline__ void planned_loop(const DmaPlan<C, T, TA, TB>& plan, 
   }
 }
 
-#ifndef TRI_GEMM_PLAN
-#define TRI_GEMM_PLAN 1
-#endif
-
 // Cross-tile pipelined 2-stage loop.  The loop above starts every K tile
 // with barrier -> step-0 fragment reads -> MFMAs, so all eight wavefronts
 // wait out one LDS read latency per tile with the MFMA pipe empty.  Here the
@@ -613,21 +475,14 @@ __device__ __forceinline__ void planned_loop(const DmaPlan<C, T, TA, TB>& plan, 
 // last 16-deep step, and tile kt + 1's step-0 fragments are read under
 // those MFMAs.  Every wavefront has finished reading tile kt's stage when it
 // passes that barrier (its last reads were issued a step earlier and
-// lds_barrier waits for them), so the first TRI_GEMM_XT_EARLY of its DMAs of
+// lds_barrier waits for them), so the first half of its DMAs of
 // tile kt + 2 go into that stage right after the last step's MFMAs, and the
 // rest after the next tile's first step: the last DMAs of a tile then have
 // two steps of MFMAs to land behind before the barrier waits for them, as in
 // the loop above.
-#ifndef TRI_GEMM_XTILE
-#define TRI_GEMM_XTILE 1
-#endif
-#ifndef TRI_GEMM_XT_EARLY
-#define TRI_GEMM_XT_EARLY -1  // -1: half of each wavefront's DMAs
-#endif
 template <class C>
 constexpr int xt_early() {
-  return TRI_GEMM_XT_EARLY < 0 ? C::DMA_PER_WAVE / 2
-         : (TRI_GEMM_XT_EARLY > C::DMA_PER_WAVE ? C::DMA_PER_WAVE : TRI_GEMM_XT_EARLY);
+  return C::DMA_PER_WAVE / 2;
 }
 
 template <class C, bool TA, bool TB, class V>
@@ -706,7 +561,7 @@ __device__ __forceinline__ void xt_loop(const DmaPlan<C, T, TA, TB>& plan, char*
 template <class C, typename T, bool TA = false, bool TB = false>
 __device__ __forceinline__ void mainloop(const Problem& p, int tm, int tn, char* smem,
                                          Acc<C>& acc) {
-  static_assert(!(TA || TB) || C::STAGES == 2, "MN-contiguous operands: the 2-stage DMA loop");
+  static_assert(C::STAGES == 2, "the 2-stage DMA loops");
   // the wavefront index stays a per-lane value here: it is part of every
   // fragment's LDS address, which then folds into one VGPR base plus
   // immediate offsets (a scalar index costs an add per read: -12% measured)
@@ -726,76 +581,20 @@ __device__ __forceinline__ void mainloop(const Problem& p, int tm, int tn, char*
     compute_tile<C, T, NoHook, TA, TB>(smem, acc, wm, wn);
     __syncthreads();
   }
-  if constexpr (C::STAGES == 2 && !TRI_GEMM_DMA) {
-    static_assert(!TA && !TB, "register-staged loop: K-contiguous operands only");
-    // register-staged double buffer: at step kt the global loads of tile
-    // kt + 1 are in flight while tile kt is multiplied, then land in the
-    // buffer read at step kt - 1
-    Stage<C> st;
-    if (nfull > 0) {
-      stage_load<C, T>(st, p, m0, n0, 0);
-      stage_store<C>(st, smem);
-    }
-    for (int64_t kt = 0; kt + 1 < nfull; ++kt) {
-      __syncthreads();
-      stage_load<C, T>(st, p, m0, n0, (kt + 1) * BK);
-      compute_tile<C, T>(smem + (int)(kt & 1) * C::STAGE_BYTES, acc, wm, wn);
-      stage_store<C>(st, smem + (int)((kt + 1) & 1) * C::STAGE_BYTES);
-    }
-    if (nfull > 0) {
-      __syncthreads();
-      compute_tile<C, T>(smem + (int)((nfull - 1) & 1) * C::STAGE_BYTES, acc, wm, wn);
-    }
-  } else if constexpr (C::STAGES == 2 && TRI_GEMM_PLAN && TRI_GEMM_XTILE && sizeof(T) == 2) {
-    DmaPlan<C, T, TA, TB> plan;
-    plan.init(p, m0, n0, smem);
+  DmaPlan<C, T, TA, TB> plan;
+  plan.init(p, m0, n0, smem);
+  if constexpr (sizeof(T) == 2) {
     if (nfull > 0) xt_loop<C, T, TA, TB>(plan, smem, acc, wm, wn, nfull);
-  } else if constexpr (C::STAGES == 2 && TRI_GEMM_PLAN) {
+  } else {
     // branch-free steady state: wait for tile kt, sync, prefetch tile kt + 1
     // into the buffer read at step kt - 1, compute tile kt
-    DmaPlan<C, T, TA, TB> plan;
-    plan.init(p, m0, n0, smem);
     if (nfull > 0) plan.template issue_range<0, C::DMA_PER_WAVE>(0, 0);
-    planned_loop<C, T, TA, TB, TRI_GEMM_SPREAD>(plan, smem, acc, wm, wn, nfull);
+    planned_loop<C, T, TA, TB, kSpread>(plan, smem, acc, wm, wn, nfull);
     if (nfull > 0) {
       wait_vmcnt<0>();
       __syncthreads();
       compute_tile<C, T, NoHook, TA, TB>(smem + (int)((nfull - 1) & 1) * C::STAGE_BYTES, acc, wm,
                                          wn);
-    }
-  } else if constexpr (C::STAGES == 2) {
-    if (nfull > 0) dma_tile<C, T, 0, C::DMA_PER_WAVE, TA, TB>(smem, p, m0, n0, 0);
-    for (int64_t kt = 0; kt + 1 < nfull; ++kt) {
-      wait_vmcnt<0>();
-      __syncthreads();
-      // the next tile's DMAs, spread over the 16-deep steps
-      const DmaSpread<C, T, TA, TB> spread{smem + (int)((kt + 1) & 1) * C::STAGE_BYTES, &p, m0,
-                                           n0, (kt + 1) * BK};
-      compute_tile<C, T, DmaSpread<C, T, TA, TB>, TA, TB>(smem + (int)(kt & 1) * C::STAGE_BYTES,
-                                                          acc, wm, wn, spread);
-    }
-    if (nfull > 0) {
-      wait_vmcnt<0>();
-      __syncthreads();
-      compute_tile<C, T, NoHook, TA, TB>(smem + (int)((nfull - 1) & 1) * C::STAGE_BYTES, acc, wm,
-                                         wn);
-    }
-  } else {
-#pragma unroll
-    for (int s = 0; s < C::STAGES - 1; ++s)
-      if (s < nfull) dma_tile<C, T>(smem + s * C::STAGE_BYTES, p, m0, n0, (int64_t)s * BK);
-    for (int64_t kt = 0; kt < nfull; ++kt) {
-      if (kt + C::STAGES - 2 < nfull)
-        wait_vmcnt<(C::STAGES - 2) * C::DMA_PER_WAVE>();
-      else
-        wait_vmcnt<0>();
-      // LDS-only barrier: __syncthreads would also wait for the younger
-      // tiles' DMAs, leaving one tile of lead whatever STAGES is
-      lds_barrier();
-      const int64_t next = kt + C::STAGES - 1;
-      if (next < nfull)
-        dma_tile<C, T>(smem + (int)(next % C::STAGES) * C::STAGE_BYTES, p, m0, n0, next * BK);
-      compute_tile<C, T>(smem + (int)(kt % C::STAGES) * C::STAGE_BYTES, acc, wm, wn);
     }
   }
   __syncthreads();
@@ -804,10 +603,7 @@ __device__ __forceinline__ void mainloop(const Problem& p, int tm, int tn, char*
 // Configurations: 16-bit types run 256 x 256 tiles on 8 wavefronts (2 per
 // SIMD, 128 x 64 each), double-buffered 128-byte K rows; fp32 (exact SIMT
 // arithmetic) runs 128 x 128 tiles on 4 wavefronts.
-#ifndef TRI_GEMM16_CFG
-#define TRI_GEMM16_CFG 256, 256, 2, 4, 2, 128
-#endif
-template <typename T> struct CfgOf { typedef Cfg<TRI_GEMM16_CFG> type; };
+template <typename T> struct CfgOf { typedef Cfg<256, 256, 2, 4, 2, 128> type; };
 template <> struct CfgOf<float> { typedef Cfg<128, 128, 2, 2, 2> type; };
 
 }  // namespace gemm

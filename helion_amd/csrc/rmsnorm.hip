@@ -22,16 +22,9 @@
 namespace tri {
 namespace {
 
-// The backward's row prefetch issues all of a lane's x vectors, then its dy
-// vectors (config 2: 69.8 -> 68.7 us), rather than the two of each vector
-// together.
-#ifndef TRI_RMS_STREAM_MAJOR
-#define TRI_RMS_STREAM_MAJOR 1
-#endif
-#ifndef TRI_RMS_BWD_BLOCKS
-#define TRI_RMS_BWD_BLOCKS 512
-#endif
-constexpr int kMaxPartialRows = TRI_RMS_BWD_BLOCKS;  // fast-path backward grid = dweight partial rows
+// Fast-path backward grid = dweight partial rows (1024 or 2048 measured
+// slower, with a longer reduction).
+constexpr int kMaxPartialRows = 512;
 constexpr int kGenericBlock = 256;
 constexpr int kStage1Rows = 128;       // streaming-path rows per dweight partial
 
@@ -185,7 +178,8 @@ rmsnorm_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x,
   float rs_next = 0.f;
   auto fetch = [&](int64_t row, u32x4 (&xb)[NV], u32x4 (&gb)[NV], float& rsb) {
     if (row >= n_rows) return;
-#if TRI_RMS_STREAM_MAJOR
+    // all of a lane's x vectors, then its dy vectors (config 2: 69.8 -> 68.7
+    // us against the two of each vector together)
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
       const int vi = lt + j * TPR;
@@ -196,16 +190,6 @@ rmsnorm_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x,
       const int vi = lt + j * TPR;
       if (vi < nvec) gb[j] = ld16_nt(dy + row * hidden + (int64_t)vi * VEC);
     }
-#else
-#pragma unroll
-    for (int j = 0; j < NV; ++j) {
-      const int vi = lt + j * TPR;
-      if (vi < nvec) {
-        xb[j] = ld16_nt(x + row * hidden + (int64_t)vi * VEC);
-        gb[j] = ld16_nt(dy + row * hidden + (int64_t)vi * VEC);
-      }
-    }
-#endif
     if (rstd_in != nullptr) rsb = rstd_in[row];
   };
   fetch(first + g, xr, gr, rs_next);
@@ -338,19 +322,17 @@ dw_finish_kernel(const A* __restrict__ sums, int64_t n_groups, int hidden, T* __
 }
 
 // Column sums of the partial rows in one launch (hidden a multiple of the
-// 16-byte vector): block b owns kDwCols columns; thread t takes the 16-byte
-// column group t % kDwCg of rows s, s + kDwSlices, s + 2 kDwSlices, ...
+// 16-byte vector): block b owns kDwCg 16-byte column groups (128 bytes of
+// every partial row, so no two blocks fetch one cache line); thread t takes
+// the column group t % kDwCg of rows s, s + kDwSlices, s + 2 kDwSlices, ...
 // (s = t / kDwCg, rows added in increasing order, eight loads in flight),
 // and the kDwSlices slice sums of each column are added through LDS in two
-// fixed-order levels (16 slices, then the 4 group sums).  The order depends
-// on n_part and hidden only, so dweight is deterministic.  Replaces two
-// launches (group sums, then their sum) whose launch and tail time was most
-// of the reduction's 9 us at 512 partial rows.
-#ifndef TRI_RMS_DW_ONE
-#define TRI_RMS_DW_ONE 1
-#endif
-constexpr int kDwCg = 4;                  // 16-byte column groups per block
-constexpr int kDwSlices = 256 / kDwCg;    // row slices (64)
+// fixed-order levels (a quarter of the slices each, then the 4 group sums).
+// The order depends on n_part and hidden only, so dweight is deterministic.
+// Replaces two launches (group sums, then their sum) whose launch and tail
+// time was most of the reduction's 9 us at 512 partial rows.
+constexpr int kDwCg = 8;                  // 16-byte column groups per block
+constexpr int kDwSlices = 256 / kDwCg;    // row slices (32)
 
 template <typename T, typename A>
 __global__ void __launch_bounds__(256)
@@ -408,7 +390,7 @@ dw_reduce_kernel(const A* __restrict__ partial, int64_t n_part, int hidden, T* _
 template <typename T, typename A>
 int dw_reduce(const A* partial, int64_t n_part, int hidden, A* sums, T* dw, hipStream_t stream) {
   constexpr int VA = 16 / (int)sizeof(A);
-  if (TRI_RMS_DW_ONE && hidden % VA == 0 && aligned16(partial)) {
+  if (hidden % VA == 0 && aligned16(partial)) {
     dw_reduce_kernel<T, A><<<(unsigned)cdiv(hidden, kDwCg * VA), 256, 0, stream>>>(
         partial, n_part, hidden, dw);
     return check_launch("rmsnorm dweight reduce");
@@ -532,18 +514,13 @@ FastCfg pick_fast(int64_t hidden, int vec, int max_nv) {
     default: return fail(TRI_EINVAL, "rmsnorm: no kernel for tpr=%d nv=%d", cfg.tpr, cfg.nv); \
   }
 
-#ifndef TRI_RMS_FWD_MAX_NV
-#define TRI_RMS_FWD_MAX_NV 1
-#endif
-#ifndef TRI_RMS_FWD_BLOCKS
-#define TRI_RMS_FWD_BLOCKS 8192
-#endif
-constexpr int kFwdMaxNV = TRI_RMS_FWD_MAX_NV;
-constexpr int64_t kFwdBlocks = TRI_RMS_FWD_BLOCKS;  // persistent forward grid (rows loop inside)
-#ifndef TRI_RMS_BWD_MAX_NV
-#define TRI_RMS_BWD_MAX_NV 4
-#endif
-constexpr int kBwdMaxNV = TRI_RMS_BWD_MAX_NV;
+// Forward: one vector per lane (rows of up to 1024 vectors on the fast
+// path), a persistent grid of 8192 workgroups (2 rows each at config 2; 1024
+// to 4096 workgroups or two vectors per lane measured slower); backward: up
+// to 4 vectors per lane.
+constexpr int kFwdMaxNV = 1;
+constexpr int64_t kFwdBlocks = 8192;
+constexpr int kBwdMaxNV = 4;
 
 template <typename T>
 int fwd_impl(const void* x, const void* res, const void* w, void* y, void* z, float* rstd,

@@ -19,20 +19,11 @@ namespace {
 // One wavefront per workgroup, two vectors per lane per operand: config-2
 // fwd+bwd 463-464 -> 448-449 us on one box (64 lanes with four vectors:
 // 456.5; 128 lanes: 465-466).
-#ifndef TRI_SWIGLU_BLOCK
-#define TRI_SWIGLU_BLOCK 64
-#endif
-constexpr int kBlock = TRI_SWIGLU_BLOCK;
-#ifndef TRI_SWIGLU_UNROLL
-#define TRI_SWIGLU_UNROLL 2
-#endif
-constexpr int kUnroll = TRI_SWIGLU_UNROLL;
-// 1: a lane issues its loads operand by operand (all U vectors of x, then of
-// gate, ...) and its stores likewise, instead of the operands of one vector
+constexpr int kBlock = 64;
+constexpr int kUnroll = 2;
+// A lane issues its loads operand by operand (all U vectors of x, then of
+// gate, ...) and its stores likewise, rather than the operands of one vector
 // together (config 2 fwd+bwd 473-475 -> 471 us with 256-lane workgroups).
-#ifndef TRI_SWIGLU_STREAM_MAJOR
-#define TRI_SWIGLU_STREAM_MAJOR 1
-#endif
 
 __device__ __forceinline__ float sigmoid_f32(float x) { return 1.0f / (1.0f + __expf(-x)); }
 
@@ -43,26 +34,15 @@ swiglu_fwd_kernel(const T* __restrict__ x, const T* __restrict__ g, T* __restric
   const int64_t nvec = n / VEC;
   const int64_t first = (int64_t)blockIdx.x * kBlock * U + threadIdx.x;
   float xv[U][VEC], gv[U][VEC];
-  if constexpr (TRI_SWIGLU_STREAM_MAJOR) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t iv = first + (int64_t)u * kBlock;
-      if (iv < nvec) load_stream<T, VEC>(x + iv * VEC, xv[u]);
-    }
+  for (int u = 0; u < U; ++u) {
+    const int64_t iv = first + (int64_t)u * kBlock;
+    if (iv < nvec) load_stream<T, VEC>(x + iv * VEC, xv[u]);
+  }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t iv = first + (int64_t)u * kBlock;
-      if (iv < nvec) load_stream<T, VEC>(g + iv * VEC, gv[u]);
-    }
-  } else {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t iv = first + (int64_t)u * kBlock;
-      if (iv < nvec) {
-        load_stream<T, VEC>(x + iv * VEC, xv[u]);
-        load_stream<T, VEC>(g + iv * VEC, gv[u]);
-      }
-    }
+  for (int u = 0; u < U; ++u) {
+    const int64_t iv = first + (int64_t)u * kBlock;
+    if (iv < nvec) load_stream<T, VEC>(g + iv * VEC, gv[u]);
   }
 #pragma unroll
   for (int u = 0; u < U; ++u) {
@@ -89,27 +69,15 @@ swiglu_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x, const T* __
   const int64_t nvec = n / VEC;
   const int64_t first = (int64_t)blockIdx.x * kBlock * U + threadIdx.x;
   float dv[U][VEC], xv[U][VEC], gv[U][VEC];
-  if constexpr (TRI_SWIGLU_STREAM_MAJOR) {
-    const T* src[3] = {dy, x, g};
-    float (*dst[3])[VEC] = {dv, xv, gv};
+  const T* src[3] = {dy, x, g};
+  float (*dst[3])[VEC] = {dv, xv, gv};
 #pragma unroll
-    for (int o = 0; o < 3; ++o)
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        const int64_t iv = first + (int64_t)u * kBlock;
-        if (iv < nvec) load_stream<T, VEC>(src[o] + iv * VEC, dst[o][u]);
-      }
-  } else {
+  for (int o = 0; o < 3; ++o)
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int64_t iv = first + (int64_t)u * kBlock;
-      if (iv < nvec) {
-        load_stream<T, VEC>(dy + iv * VEC, dv[u]);
-        load_stream<T, VEC>(x + iv * VEC, xv[u]);
-        load_stream<T, VEC>(g + iv * VEC, gv[u]);
-      }
+      if (iv < nvec) load_stream<T, VEC>(src[o] + iv * VEC, dst[o][u]);
     }
-  }
   // gradients in place: dv becomes dx, xv becomes dgate
 #pragma unroll
   for (int u = 0; u < U; ++u)
@@ -122,26 +90,15 @@ swiglu_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x, const T* __
       dv[u][i] = d * gv[u][i] * dsilu;
       xv[u][i] = d * silu;
     }
-  if constexpr (TRI_SWIGLU_STREAM_MAJOR) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t iv = first + (int64_t)u * kBlock;
-      if (iv < nvec) store_stream<T, VEC>(dx + iv * VEC, dv[u]);
-    }
+  for (int u = 0; u < U; ++u) {
+    const int64_t iv = first + (int64_t)u * kBlock;
+    if (iv < nvec) store_stream<T, VEC>(dx + iv * VEC, dv[u]);
+  }
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t iv = first + (int64_t)u * kBlock;
-      if (iv < nvec) store_stream<T, VEC>(dg + iv * VEC, xv[u]);
-    }
-  } else {
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const int64_t iv = first + (int64_t)u * kBlock;
-      if (iv < nvec) {
-        store_stream<T, VEC>(dx + iv * VEC, dv[u]);
-        store_stream<T, VEC>(dg + iv * VEC, xv[u]);
-      }
-    }
+  for (int u = 0; u < U; ++u) {
+    const int64_t iv = first + (int64_t)u * kBlock;
+    if (iv < nvec) store_stream<T, VEC>(dg + iv * VEC, xv[u]);
   }
   if (VEC > 1 && blockIdx.x == gridDim.x - 1) {
     for (int64_t e = nvec * VEC + threadIdx.x; e < n; e += kBlock) {

@@ -18,6 +18,8 @@
 //   6  fill a, grid-covering
 //   7  two streams read, one written, grid-covering (a + b -> c): the
 //      access shape of the RMSNorm backward (x, dy -> dx) and SwiGLU forward
+//   8  AdamW-shaped update, grid-covering: `blocks` is the workgroup size (64
+//      or 256 lanes), each lane one 16-byte vector of each of a, b, c, d
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -146,6 +148,21 @@ __global__ void __launch_bounds__(kBlock) cover_2r1w(const f4* __restrict__ a,
   if (i < n) stn(c + i, ldn(a + i) + ldn(b + i));
 }
 
+template <int L>
+__global__ void __launch_bounds__(L) cover_update(f4* __restrict__ p, const f4* __restrict__ g,
+                                                  f4* __restrict__ m, f4* __restrict__ v,
+                                                  int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * L + threadIdx.x;
+  if (i >= n) return;
+  f4 a = ldn(p + i);
+  const f4 b = ldn(g + i);
+  f4 c = ldn(m + i), d = ldn(v + i);
+  adamw_like(a, b, c, d);
+  stn(m + i, c);
+  stn(v + i, d);
+  stn(p + i, a);
+}
+
 }  // namespace
 
 extern "C" const char* tritium_probe_last_error() { return g_err; }
@@ -154,20 +171,22 @@ extern "C" const char* tritium_probe_last_error() { return g_err; }
 // 16-byte vectors each, 16-byte aligned, on the current device.
 extern "C" int tritium_stream_probe(int pattern, void* a, void* b, void* c, void* d,
                                     int64_t n_vec4, int blocks, void* stream) {
-  if (pattern < 0 || pattern > 7 || n_vec4 < 0 || blocks <= 0 || blocks > (1 << 20)) {
+  if (pattern < 0 || pattern > 8 || n_vec4 < 0 || blocks <= 0 || blocks > (1 << 20) ||
+      (pattern == 8 && blocks != 64 && blocks != 256)) {
     snprintf(g_err, sizeof(g_err), "stream probe: bad pattern %d, n_vec4 %lld or blocks %d",
              pattern, (long long)n_vec4, blocks);
     return 1;
   }
   const bool need_b = pattern != 2 && pattern != 6;
-  const bool need_cd = pattern == 3;
+  const bool need_cd = pattern == 3 || pattern == 8;
   if (a == nullptr || (need_b && b == nullptr) || (need_cd && d == nullptr) ||
       ((need_cd || pattern == 7) && c == nullptr)) {
     snprintf(g_err, sizeof(g_err), "stream probe: missing buffer for pattern %d", pattern);
     return 1;
   }
   hipStream_t st = (hipStream_t)stream;
-  const int64_t cover = (n_vec4 + kBlock - 1) / kBlock;
+  const int lanes = pattern == 8 ? blocks : kBlock;
+  const int64_t cover = (n_vec4 + lanes - 1) / lanes;
   if (pattern >= 4 && (cover == 0 || cover > 0x7fffffffLL)) {
     snprintf(g_err, sizeof(g_err), "stream probe: %lld vectors do not fit one grid",
              (long long)n_vec4);
@@ -183,8 +202,14 @@ extern "C" int tritium_stream_probe(int pattern, void* a, void* b, void* c, void
     case 4: cover_read<<<(unsigned)cover, kBlock, 0, st>>>((const f4*)a, n_vec4, (float*)b); break;
     case 5: cover_copy<<<(unsigned)cover, kBlock, 0, st>>>((const f4*)a, (f4*)b, n_vec4); break;
     case 6: cover_fill<<<(unsigned)cover, kBlock, 0, st>>>((f4*)a, n_vec4); break;
-    default:
+    case 7:
       cover_2r1w<<<(unsigned)cover, kBlock, 0, st>>>((const f4*)a, (const f4*)b, (f4*)c, n_vec4);
+      break;
+    default:
+      if (blocks == 64)
+        cover_update<64><<<(unsigned)cover, 64, 0, st>>>((f4*)a, (const f4*)b, (f4*)c, (f4*)d, n_vec4);
+      else
+        cover_update<256><<<(unsigned)cover, 256, 0, st>>>((f4*)a, (const f4*)b, (f4*)c, (f4*)d, n_vec4);
       break;
   }
   const hipError_t e = hipGetLastError();

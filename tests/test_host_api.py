@@ -134,14 +134,15 @@ def test_swiglu_and_adamw_messages(meta_ok):
 
 def test_adamw_table_cache_revalidates_changed_tensors(meta_ok, monkeypatch):
     """A cached descriptor table is reused only for tensors with the same
-    address, dtype, device, shape and strides; a wrong-dtype grad, a 16-bit
-    moment or a non-contiguous view at a cached address is checked again and
-    rejected (meta tensors all share address 0, the worst case)."""
+    address, dtype, shape and contiguity on the same device; a wrong-dtype
+    grad, a 16-bit moment, a reshaped or a non-contiguous view at a cached
+    address is checked again and rejected (meta tensors all share address 0,
+    the worst case)."""
     cache = adamw_mod._TableCache()
     monkeypatch.setattr(adamw_mod, "_tables", cache)
     p, g, m, v = meta(8, 4), meta(8, 4), meta(8, 4), meta(8, 4)
-    key = ((adamw_mod._signature(p), adamw_mod._signature(g), adamw_mod._signature(m),
-            adamw_mod._signature(v)),)
+    key = adamw_mod._table_key([p], [g], [m], [v])
+    assert key == (p.device,) + tuple(adamw_mod._signature(t) for t in (p, g, m, v))
     sentinel = ("table", 1, 1)
     cache.put(key, sentinel)
     assert adamw_mod._table_for([p], [g], [m], [v]) is sentinel
@@ -151,6 +152,8 @@ def test_adamw_table_cache_revalidates_changed_tensors(meta_ok, monkeypatch):
         adamw_mod._table_for([p], [g], [meta(8, 4, dtype=torch.bfloat16)], [v])
     with pytest.raises(ValueError, match="must be contiguous"):
         adamw_mod._table_for([p], [g], [m], [meta(4, 8).t()])
+    with pytest.raises(ValueError, match="Shape mismatch"):
+        adamw_mod._table_for([p], [meta(4, 8)], [m], [v])
 
 
 def test_linear_ce_messages(meta_ok):
