@@ -1437,7 +1437,7 @@ attn_bwd_dq_mfma(BwdArgs a) {
 // can see them: S = Q K^T and dP = dO V^T from row reads of the Q / dO
 // tiles, dV^T += dO^T P and dK^T += Q^T dS from transposing reads.
 template <typename T, int D, int WAVES, int PASS = 0>
-__global__ void __launch_bounds__(64 * WAVES)
+__global__ void __launch_bounds__(64 * WAVES, D == 64 ? 8 / WAVES : 1)
 attn_bwd_dkdv_v2(BwdArgs a) {
   // PASS 0: dK and dV; 1: dV alone; 2: dK alone (head_dim 256, where the K
   // and V fragments and both accumulators of 32 kv rows would not fit one
@@ -1503,7 +1503,7 @@ attn_bwd_dkdv_v2(BwdArgs a) {
     // (MFMA operands), VGPRs left to the softmax; 8 wavefronts: 256, VGPRs
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
-      if constexpr (WAVES <= 4) {
+      if constexpr (WAVES <= 4 && D != 64) {
         if constexpr (DO_DV) pin_agpr(dv[mt]);
         if constexpr (DO_DK) pin_agpr(dk[mt]);
       } else {
@@ -1511,7 +1511,7 @@ attn_bwd_dkdv_v2(BwdArgs a) {
         if constexpr (DO_DK) pin_vgpr(dk[mt]);
       }
     }
-    if constexpr (WAVES <= 4) {
+    if constexpr (WAVES <= 4 && D != 64) {
 #pragma unroll
       for (int st = 0; st < KS; ++st) {
         pin_agpr(kf[st]);
