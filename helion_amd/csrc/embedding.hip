@@ -14,10 +14,12 @@
 // in which each token's slot is its chunk's offset plus the number of
 // earlier tokens of the chunk with the same id -- each row's tokens then lie
 // together in token order (integer work only; the result does not depend on
-// execution order).  The wavefront at the first position of each row's run
-// then sums that row's dx rows in that order in fp32 registers and adds the
-// sum to the row (out of place, dw_in is first copied to dw_out).  Every row's sum is
-// formed in one fixed order: results are bitwise reproducible, with no
+// execution order).  Fixed windows of that list are then summed one
+// wavefront each (emb_win_kernel, below: a run of one row inside a window
+// is summed in token order and added to the row; a run that crosses windows
+// leaves per-window fp32 parts that emb_merge_kernel adds in window order),
+// out of place after dw_in is copied to dw_out.  Every row's sum is formed
+// in an order fixed by the ids: results are bitwise reproducible, with no
 // floating-point atomics and no sort.  Rows no token names are copied (or,
 // in place, left alone); ids outside [0, vocab) contribute nothing.
 #include "common.h"
@@ -137,55 +139,192 @@ emb_scatter_kernel(const TT* __restrict__ ids, int64_t n_tok, int64_t vocab, int
   rows[pos] = b;
 }
 
-// One wavefront per position k of the bucketed list: the wavefront at the
-// first position of a row's run (where rows[] changes) sums that row's
-// tokens (list[k0 .. k1), in token order) in fp32 in registers, lane l owning
-// columns c0 + l + 64 j of each chunk of 64 * kEmbLaneCols columns, the dx
-// rows loaded one token ahead, and writes dw[v] += sum (one rounding); the
-// other wavefronts exit.  Rows no token names are not touched.
-constexpr int kEmbLaneCols = 16;
+// The bucketed list is cut into windows of kEmbWin positions, one wavefront
+// each, so every wavefront sums about the same number of dx rows whatever
+// the distribution of the ids (one id repeated over half the tokens still
+// spreads over many wavefronts).  Window w covers positions [w W, w W + W):
+// its wavefront walks them in order, summing each run of equal rows[] in
+// token order in fp32 (dx rows loaded kEmbDepth positions ahead).  A run
+// that lies inside the window is added to its row of dw and rounded once; a
+// run that crosses a window boundary leaves this window's part as an fp32
+// partial row in slot 2w (the run began in an earlier window) or 2w + 1 (it
+// begins here and continues past the window) -- a window holds at most one
+// of each -- and emb_merge_kernel, in the window where such a run ends,
+// adds its parts in window order and rounds once.  The order of every sum
+// depends on the ids only: results are bitwise reproducible.
+//
+// Columns: with VEC, lane l owns the 16-byte group l of each block of 64
+// groups (every row, dx stride and pointer a multiple of 16 bytes); else
+// columns c0 + l + 64 j, j < 16.  The partial rows use the same mapping.
+constexpr int kEmbWin = 16;
+constexpr int kEmbDepth = 4;
 
-template <typename T>
+template <typename T, bool VEC>
+struct EmbCols {
+  static constexpr int L = VEC ? 16 / (int)sizeof(T) : 16;  // columns per lane per block
+  static constexpr int BLK = kWave * L;                     // columns per block
+  static __device__ __forceinline__ int64_t col(int64_t c0, int lane, int e) {
+    return VEC ? c0 + (int64_t)lane * L + e : c0 + lane + (int64_t)kWave * e;
+  }
+  static __device__ __forceinline__ void load(const T* __restrict__ row, int64_t c0, int lane,
+                                              int64_t dim, float (&x)[L]) {
+    if constexpr (VEC) {
+      if (col(c0, lane, 0) < dim) {
+        const Pack<T, L> pk = *reinterpret_cast<const Pack<T, L>*>(row + col(c0, lane, 0));
+#pragma unroll
+        for (int e = 0; e < L; ++e) x[e] = to_f32(pk.v[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < L; ++e) x[e] = 0.f;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < L; ++e) x[e] = col(c0, lane, e) < dim ? to_f32(row[col(c0, lane, e)]) : 0.f;
+    }
+  }
+  // row += acc, rounded once
+  static __device__ __forceinline__ void add_round(T* row, int64_t c0, int lane, int64_t dim,
+                                                   const float (&acc)[L]) {
+    if constexpr (VEC) {
+      if (col(c0, lane, 0) < dim) {
+        Pack<T, L>* p = reinterpret_cast<Pack<T, L>*>(row + col(c0, lane, 0));
+        Pack<T, L> pk = *p;
+#pragma unroll
+        for (int e = 0; e < L; ++e) pk.v[e] = from_f32<T>(to_f32(pk.v[e]) + acc[e]);
+        *p = pk;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < L; ++e) {
+        const int64_t c = col(c0, lane, e);
+        if (c < dim) row[c] = from_f32<T>(to_f32(row[c]) + acc[e]);
+      }
+    }
+  }
+};
+
+// rows[] of a window and of its two neighbours, and list[] of the window, in
+// lanes (lane i: position k0 - 1 + i; -1 past either end), read back with
+// readlane: one load each per wavefront.
+struct EmbWinIds {
+  int row_l, tok_l;
+  __device__ __forceinline__ void load(const int* rows, const int* list, int64_t k0,
+                                       int64_t n_list, int lane) {
+    const int64_t k = k0 - 1 + lane;
+    const bool in = k >= 0 && k < n_list && lane <= kEmbWin + 1;
+    row_l = in ? rows[k] : -1;
+    tok_l = in ? list[k] : 0;
+  }
+  __device__ __forceinline__ int row(int i) const { return __shfl(row_l, i + 1, kWave); }
+  __device__ __forceinline__ int tok(int i) const { return __shfl(tok_l, i + 1, kWave); }
+};
+
+template <typename T, bool VEC>
 __global__ void __launch_bounds__(kEmbThreads)
-emb_runs_kernel(const int* __restrict__ off, const int* __restrict__ totals, int64_t B, int64_t C,
-                const int* __restrict__ list, const int* __restrict__ rows,
-                const T* __restrict__ dx, int64_t ld_dx, T* dw, int64_t dim) {
+emb_win_kernel(const int* __restrict__ off, const int* __restrict__ totals, int64_t B, int64_t C,
+               const int* __restrict__ list, const int* __restrict__ rows,
+               const T* __restrict__ dx, int64_t ld_dx, T* dw, int64_t dim,
+               float* __restrict__ part) {
+  typedef EmbCols<T, VEC> E;
   constexpr int W = kEmbThreads / kWave;
   const int lane = threadIdx.x & (kWave - 1);
-  const int64_t k = (int64_t)blockIdx.x * W + (threadIdx.x >> 6);
+  const int64_t w = (int64_t)blockIdx.x * W + (threadIdx.x >> 6);
   // the list holds only the tokens whose id is in range: its length is the
   // scan's grand total, not the token count
   const int64_t n_list = scanned(off, totals, B * C);
-  if (k >= n_list) return;
-  const int v = rows[k];
-  if (k > 0 && rows[k - 1] == v) return;  // not the first entry of its row
-  int64_t k1 = k + 1;
-  while (k1 < n_list && rows[k1] == v) ++k1;
-  const int64_t k0 = k;
-  T* row = dw + (int64_t)v * dim;
-  for (int64_t c0 = 0; c0 < dim; c0 += kWave * kEmbLaneCols) {
-    float acc[kEmbLaneCols], cur[kEmbLaneCols], nxt[kEmbLaneCols];
-    auto load = [&](int64_t kk, float (&x)[kEmbLaneCols]) {
-      const T* src = dx + (int64_t)list[kk] * ld_dx + c0 + lane;
+  const int64_t k0 = w * kEmbWin;
+  if (k0 >= n_list) return;
+  const int n = (int)min((int64_t)kEmbWin, n_list - k0);
+  EmbWinIds ids;
+  ids.load(rows, list, k0, n_list, lane);
+  const int before = ids.row(-1), after = ids.row(n);  // -1 past the list's ends
+  for (int64_t c0 = 0; c0 < dim; c0 += E::BLK) {
+    float ring[kEmbDepth][E::L], acc[E::L];
 #pragma unroll
-      for (int j = 0; j < kEmbLaneCols; ++j)
-        x[j] = c0 + lane + kWave * j < dim ? to_f32(src[kWave * j]) : 0.f;
-    };
+    for (int d = 0; d < kEmbDepth; ++d)
+      if (d < n) E::load(dx + (int64_t)ids.tok(d) * ld_dx, c0, lane, dim, ring[d]);
 #pragma unroll
-    for (int j = 0; j < kEmbLaneCols; ++j) acc[j] = 0.f;
-    load(k0, cur);
-    for (int64_t kk = k0; kk < k1; ++kk) {
-      if (kk + 1 < k1) load(kk + 1, nxt);
+    for (int e = 0; e < E::L; ++e) acc[e] = 0.f;
+    int run0 = 0;
+    for (int i0 = 0; i0 < n; i0 += kEmbDepth) {
 #pragma unroll
-      for (int j = 0; j < kEmbLaneCols; ++j) acc[j] += cur[j];
+      for (int d = 0; d < kEmbDepth; ++d) {
+        const int i = i0 + d;
+        if (i < n) {
 #pragma unroll
-      for (int j = 0; j < kEmbLaneCols; ++j) cur[j] = nxt[j];
+          for (int e = 0; e < E::L; ++e) acc[e] += ring[d][e];
+          if (i + kEmbDepth < n)
+            E::load(dx + (int64_t)ids.tok(i + kEmbDepth) * ld_dx, c0, lane, dim, ring[d]);
+          const int v = ids.row(i);
+          const bool last = i + 1 == n;
+          const int next = last ? after : ids.row(i + 1);
+          if (last || next != v) {  // the window's part of the run [run0, i] of row v is complete
+            const bool begins_here = run0 > 0 || before != v;
+            const bool ends_here = next != v;
+            if (begins_here && ends_here) {
+              E::add_round(dw + (int64_t)v * dim, c0, lane, dim, acc);
+            } else {
+              float* pr = part + (2 * w + (begins_here ? 1 : 0)) * dim;
+#pragma unroll
+              for (int e = 0; e < E::L; ++e) {
+                const int64_t c = E::col(c0, lane, e);
+                if (c < dim) pr[c] = acc[e];
+              }
+            }
+#pragma unroll
+            for (int e = 0; e < E::L; ++e) acc[e] = 0.f;
+            run0 = i + 1;
+          }
+        }
+      }
     }
+  }
+}
+
+// One wavefront per window w: if the run at the window's first position began
+// in an earlier window and ends in this one, add its parts -- slot 2 w0 + 1
+// of its first window w0, then slot 2 w' of each later window up to w -- in
+// that order, and add the sum to its row of dw (one rounding).
+template <typename T, bool VEC>
+__global__ void __launch_bounds__(kEmbThreads)
+emb_merge_kernel(const int* __restrict__ off, const int* __restrict__ totals, int64_t B,
+                 int64_t C, const int* __restrict__ list, const int* __restrict__ rows, T* dw,
+                 int64_t dim, const float* __restrict__ part) {
+  typedef EmbCols<T, VEC> E;
+  constexpr int W = kEmbThreads / kWave;
+  const int lane = threadIdx.x & (kWave - 1);
+  const int64_t w = (int64_t)blockIdx.x * W + (threadIdx.x >> 6);
+  const int64_t n_list = scanned(off, totals, B * C);
+  const int64_t k0 = w * kEmbWin;
+  if (k0 >= n_list || k0 == 0) return;
+  const int n = (int)min((int64_t)kEmbWin, n_list - k0);
+  EmbWinIds ids;
+  ids.load(rows, list, k0, n_list, lane);
+  const int v = ids.row(0);
+  if (ids.row(-1) != v) return;                       // the run begins in this window
+  if (ids.row(n - 1) == v && ids.row(n) == v) return;  // it continues past the window
+  const int64_t w0 = (int64_t)scanned(off, totals, (int64_t)v * C) / kEmbWin;
+  for (int64_t c0 = 0; c0 < dim; c0 += E::BLK) {
+    float acc[E::L], x[kEmbDepth][E::L];
 #pragma unroll
-    for (int j = 0; j < kEmbLaneCols; ++j) {
-      const int64_t c = c0 + lane + kWave * j;
-      if (c < dim) row[c] = from_f32<T>(to_f32(row[c]) + acc[j]);
+    for (int e = 0; e < E::L; ++e) acc[e] = 0.f;
+    auto slot = [&](int64_t ww) { return part + (ww == w0 ? 2 * ww + 1 : 2 * ww) * dim; };
+    for (int64_t ww = w0; ww <= w; ww += kEmbDepth) {
+#pragma unroll
+      for (int d = 0; d < kEmbDepth; ++d) {  // the loads of up to kEmbDepth slots together
+        const float* pr = slot(ww + d);
+#pragma unroll
+        for (int e = 0; e < E::L; ++e) {
+          const int64_t c = E::col(c0, lane, e);
+          x[d][e] = ww + d <= w && c < dim ? pr[c] : 0.f;
+        }
+      }
+#pragma unroll
+      for (int d = 0; d < kEmbDepth; ++d)
+#pragma unroll
+        for (int e = 0; e < E::L; ++e) acc[e] += x[d][e];
     }
+    E::add_round(dw + (int64_t)v * dim, c0, lane, dim, acc);
   }
 }
 
@@ -207,25 +346,26 @@ emb_zero_kernel(int* __restrict__ p, int64_t n) {
 }
 
 struct EmbLayout {
-  int64_t B, C, tiles;
-  size_t off, totals, list, rows, total;
+  int64_t B, C, tiles, windows;
+  size_t off, totals, list, rows, part, total;
 };
 
 // workspace: off [B * C + 1] counts / local prefixes, totals [tiles + 1],
-// list [n_tok] token indices and rows [n_tok] their ids; one bucket per
-// vocabulary row
+// list [n_tok] token indices and rows [n_tok] their ids (one bucket per
+// vocabulary row), part [2 * windows, dim] fp32 partial rows
 EmbLayout emb_layout(int64_t n_tok, int64_t vocab, int64_t dim) {
-  (void)dim;
   EmbLayout L;
   L.B = vocab;
   L.C = std::max<int64_t>(1, cdiv(n_tok, kEmbChunk));
   L.tiles = cdiv(L.B * L.C + 1, kScanTile);
+  L.windows = std::max<int64_t>(1, cdiv(n_tok, kEmbWin));
   auto up = [](int64_t b) { return (size_t)cdiv(b, 256) * 256; };
   L.off = 0;
   L.totals = up((L.B * L.C + 1) * 4);
   L.list = L.totals + up((L.tiles + 1) * 4);
   L.rows = L.list + up(std::max<int64_t>(1, n_tok) * 4);
-  L.total = L.rows + up(std::max<int64_t>(1, n_tok) * 4);
+  L.part = L.rows + up(std::max<int64_t>(1, n_tok) * 4);
+  L.total = L.part + up(2 * L.windows * dim * 4);
   return L;
 }
 
@@ -302,9 +442,22 @@ extern "C" int tritium_embedding_bwd(const void* ids, int id_kind, int64_t n_tok
     if (int e = check_launch("embedding backward copy")) return e;
   }
   if (n_tokens == 0) return TRI_OK;
-  const unsigned blocks = (unsigned)cdiv(n_tokens, kEmbThreads / kWave);
-  TRI_DISPATCH_FLOAT(dtype, T,
-    emb_runs_kernel<T><<<blocks, kEmbThreads, 0, st>>>(off, totals, L.B, L.C, list, rows,
-                                                      (const T*)dx, ld_dx, (T*)dw_out, dim));
-  return check_launch("embedding backward");
+  float* part = (float*)((char*)workspace + L.part);
+  const unsigned blocks = (unsigned)cdiv(L.windows, kEmbThreads / kWave);
+  const int esz = dtype_size(dtype);
+  const bool vec = aligned16(dx) && aligned16(dw_out) && (dim * esz) % 16 == 0 &&
+                   (ld_dx * esz) % 16 == 0;
+#define EMB_LAUNCH(VEC)                                                                        \
+  TRI_DISPATCH_FLOAT(dtype, T, {                                                               \
+    emb_win_kernel<T, VEC><<<blocks, kEmbThreads, 0, st>>>(off, totals, L.B, L.C, list, rows,   \
+                                                           (const T*)dx, ld_dx, (T*)dw_out,     \
+                                                           dim, part);                          \
+    if (int e = check_launch("embedding backward")) return e;                                  \
+    emb_merge_kernel<T, VEC><<<blocks, kEmbThreads, 0, st>>>(off, totals, L.B, L.C, list, rows, \
+                                                             (T*)dw_out, dim, part);            \
+  })
+  if (vec) EMB_LAUNCH(true);
+  else EMB_LAUNCH(false);
+#undef EMB_LAUNCH
+  return check_launch("embedding backward (merge)");
 }

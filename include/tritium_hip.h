@@ -345,9 +345,15 @@ int tritium_linear_ce_grad_logits(const float* grad_out, const float* n_valid, c
  * [n_tokens] int32 (id_kind 1) or int64 (2); dx: [n_tokens, dim] with row
  * stride ld_dx; dw_in, dw_out: [vocab, dim] contiguous, all in `dtype`.
  * dw_out may be dw_in (rows no id names are then left as they are).  Ids
- * outside [0, vocab) contribute nothing.  workspace:
- * tritium_embedding_bwd_workspace_size bytes (counts and the bucketed token
- * list; cleared by the call itself). */
+ * outside [0, vocab) contribute nothing.  A row's tokens are summed in
+ * windows of 16 positions of the bucketed list and the windows' parts added
+ * in order, so a heavily repeated id (padding, end of text) spreads over many
+ * wavefronts.  workspace: tritium_embedding_bwd_workspace_size bytes,
+ * cleared by the call itself where it needs to be: 4 bytes per (vocabulary
+ * row, 1024-token chunk) of counts -- 4 * vocab * ceil(n_tokens / 1024),
+ * which grows with both (0.8 MB at vocab 50304 and 16K tokens, 512 MB at a
+ * 128K vocabulary and 1M tokens) -- plus 8 bytes per token for the bucketed
+ * list and dim * n_tokens / 2 bytes of fp32 window parts. */
 size_t tritium_embedding_bwd_workspace_size(int64_t n_tokens, int64_t vocab, int64_t dim);
 int tritium_embedding_bwd(const void* ids, int id_kind, int64_t n_tokens, const void* dx,
                           int64_t ld_dx, const void* dw_in, void* dw_out, int64_t vocab,

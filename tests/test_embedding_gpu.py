@@ -2,7 +2,9 @@
 oracle (oracle.embedding.backward, pinned to torch's F.embedding autograd):
 dw_out = dw_in + scatter_add(ids, dx), fp32 sums rounded once.  Covers int32 and
 int64 ids, dims below, at and past one 1024-column chunk (12, 300, 768, 1000,
-1100), repeated and very frequent ids (140 repeats of one id),
+1100), repeated and very frequent ids (140 repeats of one id; one id on half
+of 6000 tokens; one id on every token), runs crossing the bucketed list's
+16-position windows,
 out-of-range ids, in-place and out-of-place, strided dx rows, empty input, and
 bitwise determinism.  Tolerance: fp32 1e-5 relative; 16-bit one rounding of the
 exact sum (half an ulp, plus the fp32 sum's own error)."""
@@ -20,7 +22,9 @@ from helion_amd.embedding import embedding_backward
 pytestmark = pytest.mark.gpu
 
 
-def _check(got, want, dtype):
+def _check(got, want, dtype, sum_bound=None):
+    """sum_bound: per-entry bound on the fp32 summation error of a row with many
+    tokens (added to the tolerance), see _sum_bound."""
     got = np32(got).astype(np.float64)
     want = np.asarray(want, dtype=np.float64)
     if dtype == torch.float32:
@@ -28,6 +32,8 @@ def _check(got, want, dtype):
     else:
         ulp = 2.0 ** (-8 if dtype == torch.bfloat16 else -11)
         tol = ulp * np.abs(want) + 1e-6
+    if sum_bound is not None:
+        tol = tol + sum_bound
     bad = np.abs(got - want) > tol
     assert not bad.any(), f"{bad.sum()} entries off, max err {np.abs(got - want).max():.3e}"
 
@@ -75,6 +81,57 @@ def test_embedding_backward_deterministic_and_empty():
     assert torch.equal(a, b)
     empty = embedding_backward(ids[:0], dx[:0], dw)
     assert torch.equal(empty, dw)
+
+
+def _sum_bound(ids, dx, vocab):
+    """4 sqrt(n_v) u sum_i |dx_i| per entry of row v, u = 2^-24: the usual
+    statistical bound on the rounding error of an fp32 sum of n_v terms (a row
+    named by thousands of tokens can lose more than the 1e-5 relative of a
+    short sum where its terms cancel; a dropped or doubled token would still
+    be off by about one |dx| entry, far above this)."""
+    ids = np32(ids).astype(np.int64)
+    a = np.abs(np32(dx).astype(np.float64))
+    cnt = np.bincount(ids, minlength=vocab).astype(np.float64)
+    s = np.zeros((vocab, a.shape[1]))
+    np.add.at(s, ids, a)
+    return 4.0 * np.sqrt(cnt)[:, None] * 2.0 ** -24 * s
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("dim", [64, 768, 1100])
+def test_embedding_backward_skewed_ids(dtype, dim):
+    # one id on half of the tokens (padding or end of text in real batches), a
+    # second one on a quarter, runs that cross the 16-position windows of the
+    # bucketed list at every offset, and runs of length 15-17 around one window
+    print(f"[embedding skewed] {dtype} dim={dim}", flush=True)
+    vocab, n = 5000, 6000
+    g = torch.Generator().manual_seed(dim + 11)
+    ids = torch.randint(0, vocab, (n,), generator=g)
+    ids[torch.randperm(n, generator=g)[: n // 2]] = 3
+    ids[torch.randperm(n, generator=g)[: n // 4]] = vocab - 1
+    ids[:15] = 100
+    ids[15:31] = 101
+    ids[31:48] = 102
+    ids = ids.cuda()
+    dx = randn((n, dim), dtype, seed=12)
+    dw = randn((vocab, dim), dtype, seed=13)
+    out = embedding_backward(ids, dx, dw)
+    want = oracle.embedding.backward(np32(ids).astype(np.int64), np32(dx), np32(dw),
+                                     NAME[dtype])
+    _check(out, want, dtype, _sum_bound(ids, dx, vocab))
+    assert torch.equal(out, embedding_backward(ids, dx, dw))  # bitwise deterministic
+
+
+def test_embedding_backward_one_id_everywhere():
+    # every token names the same row: one run across every window of the list
+    vocab, dim, n = 7, 256, 4099
+    ids = torch.full((n,), 5, dtype=torch.int64).cuda()
+    dx = randn((n, dim), torch.float32, seed=14)
+    dw = randn((vocab, dim), torch.float32, seed=15)
+    out = embedding_backward(ids, dx, dw)
+    want = oracle.embedding.backward(np32(ids).astype(np.int64), np32(dx), np32(dw), "f32")
+    _check(out, want, torch.float32, _sum_bound(ids, dx, vocab))
+    assert torch.equal(out[:5], dw[:5]) and torch.equal(out[6:], dw[6:])
 
 
 def test_embedding_backward_matches_torch_autograd_for_a_tied_weight():
