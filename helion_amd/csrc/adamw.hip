@@ -27,10 +27,12 @@ namespace {
 // One wavefront per workgroup: config-2 update 612-618 -> 586-595 us against
 // 256 lanes (128: 607-617, 512: 620-623, 1024: 651-653), on the same boxes.
 constexpr int kBlock = 64;
-// 512 elements per workgroup (two groups of 4 per lane): 256 and 1024
-// measured the same or slower (0.560-0.586 and 0.567 ms against 0.566 ms
-// for the config-2 update, same box).
-constexpr int64_t kChunk = 512;
+// 256 elements per workgroup, one group of 4 per lane (one 16-byte vector
+// of each fp32 stream): config-2 update 561-565 us against 579-581 us with
+// 512 (two groups per lane), same box, alternating runs -- the access shape
+// of the fastest AdamW-shaped streaming probe (a grid of 64-lane workgroups,
+// one vector per lane per array).
+constexpr int64_t kChunk = 256;
 // The mixed-precision kernel (four fp32 and two 16-bit streams per element)
 // streams best with four 8-element steps per lane: 820 vs 839 us per GPT
 // step with two, 860 with eight.
