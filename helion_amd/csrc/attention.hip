@@ -121,20 +121,23 @@ __device__ __forceinline__ int xcd_remap(int bid, int n) {
 // Work item w (from xcd_remap, n = n_slices * n_tiles items) -> its slice
 // (batch * head) and tile rank.  Under a causal mask the tiles of a slice
 // differ in length, rank 0 the longest.  When each XCD's range of w holds
-// whole slices, the XCD takes its slices' tiles rank by rank (the longest
-// of all its slices first), so the short tiles fill the tail of the grid
-// instead of a slice's longest tile starting last: for 8 tiles of 2 .. 16
-// steps on 64 workgroup slots a dispatch-order simulation gives 28 steps of
-// makespan against 36 slice by slice.  Otherwise slice by slice, longest
-// tile first.
+// whole slices, the XCD takes its slices in groups of `group` and each
+// group's tiles rank by rank (the longest of the group first), so the short
+// tiles fill the tail instead of a slice's longest tile starting last: for 8
+// tiles of 2 .. 16 steps on 64 workgroup slots a dispatch-order simulation
+// gives 28 steps of makespan with the whole XCD as one group against 36
+// slice by slice (ideal 27).  A small group keeps fewer slices' operands in
+// the XCD's L2 at a time.  Otherwise slice by slice, longest tile first.
 __device__ __forceinline__ void lpt_item(int w, int n, int n_slices, int n_tiles, bool causal,
-                                         int& slice, int& rank) {
-  const int spx = n_slices / kXcds;
+                                         int group, int& slice, int& rank) {
   if (causal && n % kXcds == 0 && n_slices % kXcds == 0) {
-    const int per = n / kXcds;  // spx * n_tiles
+    const int spx = n_slices / kXcds, per = n / kXcds;  // per = spx * n_tiles
+    const int gs = min(group, spx);
     const int x = w / per, local = w - x * per;
-    rank = local / spx;
-    slice = x * spx + (local - rank * spx);
+    const int grp = local / (gs * n_tiles), within = local - grp * gs * n_tiles;
+    const int gsz = min(gs, spx - grp * gs);  // the last group may be smaller
+    rank = within / gsz;
+    slice = x * spx + grp * gs + (within - rank * gsz);
   } else {
     slice = w / n_tiles;
     rank = w - slice * n_tiles;
@@ -753,7 +756,8 @@ attn_fwd_v2(FwdArgs a) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int l32 = lane & 31, g = lane >> 5;
   int bh, rank;
-  lpt_item(xcd_remap(blockIdx.x, gridDim.x), gridDim.x, a.B * a.H, a.n_tiles, a.causal, bh, rank);
+  lpt_item(xcd_remap(blockIdx.x, gridDim.x), gridDim.x, a.B * a.H, a.n_tiles, a.causal, a.B * a.H,
+           bh, rank);
   const int qt = a.n_tiles - 1 - rank;  // rank 0: the most kv tiles
   const int b = bh / a.H, h = bh % a.H;
   const int hk = h / (a.H / a.Hkv);
@@ -1479,7 +1483,8 @@ attn_bwd_dkdv_v2(BwdArgs a) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int l32 = lane & 31, g = lane >> 5;
   int bhk, kt;  // kt = 0 sees the most queries: heaviest first
-  lpt_item(xcd_remap(blockIdx.x, gridDim.x), gridDim.x, a.B * a.Hkv, a.n_tiles, a.causal, bhk, kt);
+  lpt_item(xcd_remap(blockIdx.x, gridDim.x), gridDim.x, a.B * a.Hkv, a.n_tiles, a.causal,
+           a.B * a.Hkv, bhk, kt);
   const int b = bhk / a.Hkv, hk = bhk % a.Hkv;
   const int group = a.H / a.Hkv;
   const int kv0 = kt * BN;
@@ -1986,8 +1991,8 @@ attn_bwd_dkdv_pair(BwdArgs a) {
     }
   } else {
     int bhk, kt;  // kt = 0 sees the most queries: heaviest first
-    lpt_item(xcd_remap(blockIdx.x, gridDim.x), gridDim.x, a.B * a.Hkv, a.n_tiles, a.causal, bhk,
-             kt);
+    lpt_item(xcd_remap(blockIdx.x, gridDim.x), gridDim.x, a.B * a.Hkv, a.n_tiles, a.causal,
+             a.B * a.Hkv, bhk, kt);
     dkdv_pair_item<T, D, DS>(a, smem, xch_all, bhk, kt);
   }
 }
@@ -2060,7 +2065,8 @@ attn_bwd_dq_v2(BwdArgs a) {
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int l32 = lane & 31, g = lane >> 5;
   int bh, rank;
-  lpt_item(xcd_remap(blockIdx.x, gridDim.x), gridDim.x, a.B * a.H, a.n_tiles, a.causal, bh, rank);
+  lpt_item(xcd_remap(blockIdx.x, gridDim.x), gridDim.x, a.B * a.H, a.n_tiles, a.causal, a.B * a.H,
+           bh, rank);
   const int qt = a.n_tiles - 1 - rank;  // rank 0: the most kv tiles
   const int b = bh / a.H, h = bh % a.H;
   const int hk = h / (a.H / a.Hkv);
@@ -2251,9 +2257,12 @@ attn_bwd_dq_ds(BwdArgs a) {
   __shared__ __attribute__((aligned(1024))) char smem[kDsStages * STAGE];
   const int lane = threadIdx.x & 63, wave = wave_id();
   const int l32 = lane & 31, g = lane >> 5;
-  const int w = xcd_remap(blockIdx.x, gridDim.x);
-  const int bh = w / a.n_tiles;
-  const int qb = a.n_tiles - 1 - w % a.n_tiles;  // causal: the longest sweeps first
+  // causal: the longest sweeps first across four (batch, head)s at a time per
+  // XCD -- config 3: 560 us one at a time (a long tail), 519 us two, 491-512
+  // four or eight, 537 all sixteen of the XCD's (K falls out of its L2)
+  int bh, rank;
+  lpt_item(xcd_remap(blockIdx.x, gridDim.x), gridDim.x, a.B * a.H, a.n_tiles, a.causal, 4, bh, rank);
+  const int qb = a.n_tiles - 1 - rank;
   const int b = bh / a.H, h = bh % a.H, hk = h / (a.H / a.Hkv);
   const int n_qt = (a.Tq + 63) >> 6, n_kvt = (a.Tkv + 63) >> 6;
   const int qt0 = kDsTiles * qb;
