@@ -34,9 +34,12 @@ constexpr int kBlock = 64;
 // one vector per lane per array).
 constexpr int64_t kChunk = 256;
 // The mixed-precision kernel (four fp32 and two 16-bit streams per element)
-// streams best with four 8-element steps per lane: 820 vs 839 us per GPT
-// step with two, 860 with eight.
-constexpr int64_t kChunkMixed = (int64_t)kBlock * 4 * 8;  // 2048 elements
+// takes one group of 4 elements per lane, 256 elements per workgroup, as
+// the fp32 kernel, loads and stores stream by stream: 715-718 us for the
+// GPT step's 151.9 M parameters against 848 us for four steps of 8
+// elements (two 16-byte vectors per fp32 stream) per lane; two groups per
+// lane 719-735 us, four 712-738, eight 741-744 (same boxes).
+constexpr int64_t kChunkMixed = (int64_t)kBlock * 4;  // 256 elements
 
 struct Hyper {
   float lr, beta1, beta2, eps, weight_decay, bc1, bc2;
@@ -196,8 +199,8 @@ adamw_multi_kernel(const int64_t* __restrict__ table, int n_tensors, Hyper h) {
 // they are), and optionally a 16-bit copy of each updated parameter (the
 // working weights of a mixed-precision model) written in the same pass --
 // 28 bytes per parameter, where widening the gradients first and rounding
-// the weights afterwards would add 12.  Eight elements per lane step: two
-// 16-byte vectors of each fp32 stream, one of each 16-bit stream.
+// the weights afterwards would add 12.  Groups of 4 elements per lane: one
+// 16-byte vector of each fp32 stream, 8 bytes of each 16-bit stream.
 template <typename TG>
 __device__ __forceinline__ void adam_chunk_mixed(float* __restrict__ p, const TG* __restrict__ g,
                                                  float* __restrict__ m, float* __restrict__ v,
@@ -209,37 +212,39 @@ __device__ __forceinline__ void adam_chunk_mixed(float* __restrict__ p, const TG
   const int64_t end = min(start + kChunkMixed, n);
   int64_t tail = start;
   if (vec_ok) {
-    constexpr int NV = (int)(kChunkMixed / 8 / kBlock);
-    const int64_t vec_end = start + ((end - start) / 8) * 8;
-    typedef float F4[4];
-    float pv[NV][8], gv[NV][8], mv[NV][8], vv[NV][8];
+    constexpr int NS = (int)(kChunkMixed / (4 * kBlock));
+    const int64_t vec_end = start + ((end - start) / 4) * 4;
+    float pv[NS][4], gv[NS][4], mv[NS][4], vv[NS][4];
+    auto elem = [&](int u) { return start + ((int64_t)u * kBlock + threadIdx.x) * 4; };
 #pragma unroll
-    for (int u = 0; u < NV; ++u) {
-      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * 8;
-      if (e < vec_end) {
-        unpack<float>(ld16_nt(p + e), *reinterpret_cast<F4*>(&pv[u][0]));
-        unpack<float>(ld16_nt(p + e + 4), *reinterpret_cast<F4*>(&pv[u][4]));
-        unpack<TG>(ld16_nt(g + e), gv[u]);
-        unpack<float>(ld16_nt(m + e), *reinterpret_cast<F4*>(&mv[u][0]));
-        unpack<float>(ld16_nt(m + e + 4), *reinterpret_cast<F4*>(&mv[u][4]));
-        unpack<float>(ld16_nt(v + e), *reinterpret_cast<F4*>(&vv[u][0]));
-        unpack<float>(ld16_nt(v + e + 4), *reinterpret_cast<F4*>(&vv[u][4]));
-      }
-    }
+    for (int u = 0; u < NS; ++u)
+      if (elem(u) < vec_end) load4_nt<float>(p + elem(u), pv[u]);
 #pragma unroll
-    for (int u = 0; u < NV; ++u) {
-      const int64_t e = start + ((int64_t)u * kBlock + threadIdx.x) * 8;
-      if (e < vec_end) {
+    for (int u = 0; u < NS; ++u)
+      if (elem(u) < vec_end) load4_nt<TG>(g + elem(u), gv[u]);
 #pragma unroll
-        for (int i = 0; i < 8; ++i) adam_update(pv[u][i], gv[u][i], mv[u][i], vv[u][i], h, lr_wd, step_size);
-        st16_nt(m + e, pack<float>(*reinterpret_cast<F4*>(&mv[u][0])));
-        st16_nt(m + e + 4, pack<float>(*reinterpret_cast<F4*>(&mv[u][4])));
-        st16_nt(v + e, pack<float>(*reinterpret_cast<F4*>(&vv[u][0])));
-        st16_nt(v + e + 4, pack<float>(*reinterpret_cast<F4*>(&vv[u][4])));
-        st16_nt(p + e, pack<float>(*reinterpret_cast<F4*>(&pv[u][0])));
-        st16_nt(p + e + 4, pack<float>(*reinterpret_cast<F4*>(&pv[u][4])));
-        if (shadow != nullptr) st16_nt(shadow + e, pack<TG>(pv[u]));
-      }
+    for (int u = 0; u < NS; ++u)
+      if (elem(u) < vec_end) load4_nt<float>(m + elem(u), mv[u]);
+#pragma unroll
+    for (int u = 0; u < NS; ++u)
+      if (elem(u) < vec_end) load4_nt<float>(v + elem(u), vv[u]);
+#pragma unroll
+    for (int u = 0; u < NS; ++u)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) adam_update(pv[u][i], gv[u][i], mv[u][i], vv[u][i], h, lr_wd, step_size);
+#pragma unroll
+    for (int u = 0; u < NS; ++u)
+      if (elem(u) < vec_end) store4_nt<float>(m + elem(u), mv[u]);
+#pragma unroll
+    for (int u = 0; u < NS; ++u)
+      if (elem(u) < vec_end) store4_nt<float>(v + elem(u), vv[u]);
+#pragma unroll
+    for (int u = 0; u < NS; ++u)
+      if (elem(u) < vec_end) store4_nt<float>(p + elem(u), pv[u]);
+    if (shadow != nullptr) {
+#pragma unroll
+      for (int u = 0; u < NS; ++u)
+        if (elem(u) < vec_end) store4_nt<TG>(shadow + elem(u), pv[u]);
     }
     tail = vec_end;
   }
