@@ -185,6 +185,16 @@ def test_attention_backward_stored_and_recomputed_ds(monkeypatch, stored, causal
     _check(torch.bfloat16, b, h, hkv, tq, tkv, head_dim, causal, seed=31 + tq + tkv)
 
 
+@pytest.mark.parametrize("head_dim", [64, 128])
+def test_attention_longest_first_order(head_dim):
+    # causal grids whose (batch, head) count is a multiple of the 8 XCDs take their
+    # tiles longest first across each XCD's slices (at head_dim 128 the dQ-from-dS
+    # kernel in groups of four slices: 6 per XCD here, a group of 4 and one of 2);
+    # the order must not change the results.  GQA: dK/dV over 24 kv slices.
+    _check(torch.bfloat16, 2, 24, 24, 512, 512, head_dim, True, seed=41)
+    _check(torch.bfloat16, 2, 24, 12, 512, 512, head_dim, True, seed=42)
+
+
 def test_attention_stored_ds_deterministic_fp16():
     q = randn((2, 4, 300, 128), torch.float16, 1).requires_grad_(True)
     k = randn((2, 2, 300, 128), torch.float16, 2).requires_grad_(True)
