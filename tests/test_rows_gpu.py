@@ -256,13 +256,49 @@ def test_adamw_multi_matches_single_and_oracle():
     assert_close(params[1], ep, 1e-5, 1e-5)
 
 
+@pytest.mark.parametrize("dtype", DTYPES)
+def test_adamw_multi_misaligned_and_ragged(dtype):
+    # tensors starting one element past a 16-byte boundary (the element path in every
+    # chunk) beside aligned ones whose sizes straddle the 256-element workgroup chunks;
+    # bitwise equal to the single-tensor kernel, and the oracle after 2 steps
+    flat = randn((1 + 1000 + 300 + 7,), dtype, 90)
+    mis = [flat[1:1001], flat[1001:1301], flat[1301:1308]]
+    params = mis + [randn((n,), dtype, 91 + n) for n in (255, 256, 257, 1027)]
+    grads = [randn(tuple(p.shape), dtype, 200 + i) * 1e-2 for i, p in enumerate(params)]
+    ms = [torch.zeros(p.shape, device="cuda") for p in params]
+    vs = [torch.zeros(p.shape, device="cuda") for p in params]
+    # the single-tensor reference on copies with the same alignment (the same code path:
+    # the element path and the vector groups may contract the update into FMAs differently)
+    flat_ref = flat.clone()
+    ref = [(flat_ref[1:1001], ms[0].clone(), vs[0].clone()),
+           (flat_ref[1001:1301], ms[1].clone(), vs[1].clone()),
+           (flat_ref[1301:1308], ms[2].clone(), vs[2].clone())]
+    ref += [(p.clone(), m.clone(), v.clone()) for p, m, v in zip(params[3:], ms[3:], vs[3:])]
+    states = [(np32(p), np32(m), np32(v)) for p, m, v in zip(params, ms, vs)]
+    gnp = [np32(g) for g in grads]
+    hp = dict(lr=6e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1)
+    for step in (1, 2):
+        tritium.adamw_step_multi(params, grads, ms, vs, step=step, **hp)
+        for (p, m, v), g in zip(ref, grads):
+            tritium.adamw_step(p, g, m, v, step=step, **hp)
+        states = [oracle.adamw.step(ep, eg, em, ev, step=step, dtype=NAME[dtype], **hp)
+                  for (ep, em, ev), eg in zip(states, gnp)]
+    for (rp, rm, rv), p, m, v in zip(ref, params, ms, vs):
+        assert torch.equal(p, rp) and torch.equal(m, rm) and torch.equal(v, rv)
+    rtol, atol = TOL[dtype]
+    for p, (ep, _, _) in zip(params, states):
+        assert_close(p, ep, rtol, atol, "param")
+
+
 @pytest.mark.parametrize("gdtype", [torch.bfloat16, torch.float16])
 def test_adamw_mixed_matches_fp32_step(gdtype):
     # tritium_adamw_step_mixed: same update as adamw_step on the widened gradient; the
     # shadow is the updated fp32 param rounded once; ragged sizes take the element path
     from helion_amd.adamw import adamw_step_mixed
-    # (tensors of one or many 8192-element blocks, with and without a ragged last block)
-    shapes = [(4096,), (33, 7), (1,), (768, 768), (5000,), (8193,), (3, 8191), (16384,)]
+    # (tensors of one or many 256-element workgroup chunks, with and without a ragged
+    # last chunk or a last group of fewer than 4 elements)
+    shapes = [(4096,), (33, 7), (1,), (768, 768), (5000,), (8193,), (3, 8191), (16384,),
+              (255,), (257,), (1027,)]
     ps = [randn(s, torch.float32, 40 + i, scale=0.02) for i, s in enumerate(shapes)]
     gs = [randn(s, gdtype, 50 + i, scale=1e-2) for i, s in enumerate(shapes)]
     ms = [randn(s, torch.float32, 60 + i, scale=1e-3) for i, s in enumerate(shapes)]
@@ -276,6 +312,33 @@ def test_adamw_mixed_matches_fp32_step(gdtype):
         for a, e in ((p, rp), (m, rm), (v, rv)):
             torch.testing.assert_close(a, e, rtol=1e-6, atol=1e-9)
         assert torch.equal(s_, p.to(gdtype))
+
+
+def test_adamw_mixed_misaligned_views():
+    # tensors that start 4 bytes past a 16-byte boundary take the element path in every
+    # chunk (the kernel's vector groups need 16-byte aligned fp32 and 8-byte aligned
+    # 16-bit rows); results as adamw_step on the widened gradient
+    from helion_amd.adamw import adamw_step_mixed
+    sizes = [1000, 300, 7]
+    def views(dtype, seed, scale):
+        flat = randn((sum(sizes) + 1,), dtype, seed, scale=scale)
+        out, off = [], 1
+        for n in sizes:
+            out.append(flat[off:off + n])
+            off += n
+        return out
+    ps, gs = views(torch.float32, 80, 0.02), views(torch.bfloat16, 81, 1e-2)
+    ms, vs = views(torch.float32, 82, 1e-3), [v.abs() for v in views(torch.float32, 83, 1e-3)]
+    sh = views(torch.bfloat16, 84, 1.0)
+    assert all(p.data_ptr() % 16 != 0 for p in ps)
+    ref = [(p.clone(), g.float(), m.clone(), v.clone()) for p, g, m, v in zip(ps, gs, ms, vs)]
+    kw = dict(lr=3e-4, beta1=0.9, beta2=0.95, eps=1e-8, weight_decay=0.1, step=3)
+    adamw_step_mixed(ps, gs, ms, vs, sh, **kw)
+    for (rp, rg, rm, rv), p, m, v, s_ in zip(ref, ps, ms, vs, sh):
+        tritium.adamw_step(rp, rg, rm, rv, **kw)
+        for a, e in ((p, rp), (m, rm), (v, rv)):
+            torch.testing.assert_close(a, e, rtol=1e-6, atol=1e-9)
+        assert torch.equal(s_, p.to(torch.bfloat16))
 
 
 def test_adamw_step1_closed_form():
