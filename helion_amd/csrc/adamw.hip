@@ -82,8 +82,9 @@ __device__ __forceinline__ void store4_nt(T* __restrict__ p, const float (&f)[4]
 }
 
 // Update elements [start, start + kChunk) of one tensor (clipped to n).
-// With 16-byte aligned tensors each lane owns kSteps groups of 4 consecutive
-// elements, kBlock groups apart, and issues its loads stream by stream (its
+// With 16-byte aligned tensors each lane owns NS = kChunk / (4 kBlock) groups
+// of 4 consecutive elements (one at 256 elements per workgroup), kBlock
+// groups apart, and issues its loads stream by stream (its
 // p groups, then g, m, v) and its stores likewise (m, v, p); elements past
 // the last whole group of 4 go one per lane.
 template <typename T>
@@ -99,7 +100,7 @@ __device__ __forceinline__ void adam_chunk(T* __restrict__ p, const T* __restric
     constexpr int NS = (int)(kChunk / (4 * kBlock));
     static_assert(NS * 4 * kBlock == kChunk, "chunk = whole groups of 4 per lane");
     const int64_t vec_end = start + ((end - start) / 4) * 4;
-    float pv[NS][4], gv[NS][4], mv[NS][4], vv[NS][4];
+    float pv[NS][4] = {}, gv[NS][4] = {}, mv[NS][4] = {}, vv[NS][4] = {};  // lanes past the end compute on zeros
     auto elem = [&](int u) { return start + ((int64_t)u * kBlock + threadIdx.x) * 4; };
 #pragma unroll
     for (int u = 0; u < NS; ++u)
@@ -214,7 +215,7 @@ __device__ __forceinline__ void adam_chunk_mixed(float* __restrict__ p, const TG
   if (vec_ok) {
     constexpr int NS = (int)(kChunkMixed / (4 * kBlock));
     const int64_t vec_end = start + ((end - start) / 4) * 4;
-    float pv[NS][4], gv[NS][4], mv[NS][4], vv[NS][4];
+    float pv[NS][4] = {}, gv[NS][4] = {}, mv[NS][4] = {}, vv[NS][4] = {};  // lanes past the end compute on zeros
     auto elem = [&](int u) { return start + ((int64_t)u * kBlock + threadIdx.x) * 4; };
 #pragma unroll
     for (int u = 0; u < NS; ++u)
