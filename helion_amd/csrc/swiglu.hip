@@ -16,11 +16,12 @@
 namespace tri {
 namespace {
 
-// One wavefront per workgroup, two vectors per lane per operand: config-2
-// fwd+bwd 463-464 -> 448-449 us on one box (64 lanes with four vectors:
-// 456.5; 128 lanes: 465-466).
+// One wavefront per workgroup, one vector per lane per operand: config-2
+// fwd+bwd 463-464 -> 448-449 us on one box with two vectors per lane (64
+// lanes with four vectors: 456.5; 128 lanes: 465-466), then 447-449 ->
+// 444-445 us with one (another box, alternating runs).
 constexpr int kBlock = 64;
-constexpr int kUnroll = 2;
+constexpr int kUnroll = 1;
 // A lane issues its loads operand by operand (all U vectors of x, then of
 // gate, ...) and its stores likewise, rather than the operands of one vector
 // together (config 2 fwd+bwd 473-475 -> 471 us with 256-lane workgroups).
@@ -115,8 +116,10 @@ swiglu_bwd_kernel(const T* __restrict__ dy, const T* __restrict__ x, const T* __
 // gate as the two halves of each row of a fused [tokens, 2 * d_ff]
 // projection, and the gradients written back into the same layout.  A
 // workgroup covers up to kBlock * kRowU vectors of one row (the row index is
-// one scalar division per workgroup).
-constexpr int kRowU = 2;
+// one scalar division per workgroup).  One vector per lane per operand: at
+// the GPT block's [16384, 2 x 3072] forward 55.5 -> 48.0 us and backward
+// 83.2 -> 75.8 us against two (same box, alternating runs).
+constexpr int kRowU = 1;
 
 template <typename T, int VEC>
 __global__ void __launch_bounds__(kBlock)
