@@ -242,6 +242,9 @@ __device__ __forceinline__ void lse_merge(float& m, float& s, float m2, float s2
 
 // kRowsSplit threads per token; the partial vocab blocks b = k, k+8, ... of
 // one thread are merged online, then the 8 threads merge in a fixed order.
+// Tokens run fastest across the lanes (thread t: token t % 32, part t / 32),
+// so each load instruction reads 32 consecutive tokens of one vocab block
+// (the partials are [vocab block][token]).
 template <typename TT>
 __global__ void __launch_bounds__(kRowsBlock)
 lce_fwd_rows(const float* __restrict__ pmax, const float* __restrict__ psum,
@@ -251,12 +254,25 @@ lce_fwd_rows(const float* __restrict__ pmax, const float* __restrict__ psum,
   __shared__ float sm_m[kRowsBlock], sm_s[kRowsBlock];
   __shared__ double sm_nll[kRowsBlock / kRowsSplit];
   __shared__ int sm_cnt[kRowsBlock / kRowsSplit];
-  const int tok = threadIdx.x / kRowsSplit, part = threadIdx.x % kRowsSplit;
+  constexpr int kTok = kRowsBlock / kRowsSplit;  // tokens per block
+  const int tok = threadIdx.x % kTok, part = threadIdx.x / kTok;
   const int64_t n = (int64_t)blockIdx.x * (kRowsBlock / kRowsSplit) + tok;
   float m = -INFINITY, s = 0.f;
   if (n < N) {
-    for (int b = part; b < tiles_v; b += kRowsSplit)
-      lse_merge(m, s, pmax[(int64_t)b * N + n], psum[(int64_t)b * N + n]);
+    // eight blocks' partials loaded together, then merged in block order
+    constexpr int kBatch = 8;
+    for (int b0 = part; b0 < tiles_v; b0 += kRowsSplit * kBatch) {
+      float bm[kBatch], bs[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        const int b = b0 + u * kRowsSplit;
+        bm[u] = b < tiles_v ? pmax[(int64_t)b * N + n] : -INFINITY;
+        bs[u] = b < tiles_v ? psum[(int64_t)b * N + n] : 0.f;
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (b0 + u * kRowsSplit < tiles_v) lse_merge(m, s, bm[u], bs[u]);
+    }
   }
   sm_m[threadIdx.x] = m;
   sm_s[threadIdx.x] = s;
@@ -265,7 +281,7 @@ lce_fwd_rows(const float* __restrict__ pmax, const float* __restrict__ psum,
     double nll = 0.0;
     int cnt = 0;
     if (n < N) {
-      for (int k = 1; k < kRowsSplit; ++k) lse_merge(m, s, sm_m[threadIdx.x + k], sm_s[threadIdx.x + k]);
+      for (int k = 1; k < kRowsSplit; ++k) lse_merge(m, s, sm_m[tok + k * kTok], sm_s[tok + k * kTok]);
       const float l = m + logf(s);
       lse[n] = l;
       const int64_t t = load_target(target, n);
