@@ -2372,7 +2372,10 @@ attn_bwd_dq_ds(BwdArgs a) {
 // merges over the chunks (o = sum o_c 2^(m_c - M) / sum l_c 2^(m_c - M)).
 constexpr int kDecWaves = 4;
 constexpr int kDecMinChunk = 256;        // keys per chunk at least
-constexpr int kDecTargetBlocks = 2048;   // workgroups to aim for
+// workgroups to aim for: 512 against 2048 (graph replays, same box) took
+// [8, 32, 8, 8192, 128] 58.3 -> 53.6-54.4 us and [8, 32, 32, 4096, 128]
+// 89.6 -> 87.7 us, [16, 12, 12, 1024, 64] 15.0 -> 15.5 us; 256 was slower
+constexpr int kDecTargetBlocks = 512;
 constexpr int kDecUnroll = 4;            // key rows in flight per lane
 constexpr int kDecMaxSplits = 256;       // chunks per (batch, head) at most
 
@@ -2529,11 +2532,21 @@ attn_decode_kernel(DecArgs a) {
         const float o2[1] = {so[w][g][threadIdx.x]};
         dec_merge<1>(mm, ll, oo, sm[w][g], sl[w][g], o2);
       }
-      float* dst = a.part + (((int64_t)b * a.H + hk * group + g) * a.n_splits + split) * (D + 2);
-      dst[2 + threadIdx.x] = oo[0];
-      if (threadIdx.x == 0) {
-        dst[0] = mm;
-        dst[1] = ll;
+      if (a.n_splits == 1) {
+        // one chunk holds the whole cache: o and lse directly, as the
+        // combine kernel would form them from this one partial (its weight
+        // 2^(m - m) = 1), so no second launch
+        const int hq = hk * group + g;
+        T* orow = (T*)a.o + b * a.so_b + hq * a.so_h;
+        orow[threadIdx.x] = from_f32<T>(ll > 0.f ? oo[0] / ll : 0.f);
+        if (threadIdx.x == 0) a.lse[(int64_t)b * a.H + hq] = (mm + log2f(ll)) * kLn2;
+      } else {
+        float* dst = a.part + (((int64_t)b * a.H + hk * group + g) * a.n_splits + split) * (D + 2);
+        dst[2 + threadIdx.x] = oo[0];
+        if (threadIdx.x == 0) {
+          dst[0] = mm;
+          dst[1] = ll;
+        }
       }
     }
   }
@@ -3228,6 +3241,7 @@ int decode_launch(const void* q, const void* k, const void* v, void* o, float* l
 #undef TRI_DEC_GROUPS
 #undef TRI_DEC_LAUNCH
   if (int e = check_launch("attention decode")) return e;
+  if (a.n_splits == 1) return TRI_OK;  // the decode kernel wrote o and lse
   if (dtype == kBF16) {
     if (D == 64) attn_decode_combine<bf16_t, 64><<<(unsigned)(B * H), 64, 0, st>>>(a);
     else attn_decode_combine<bf16_t, 128><<<(unsigned)(B * H), 128, 0, st>>>(a);
