@@ -306,13 +306,13 @@ def attention_gpt_leg(torch, tritium, iters: int = 20, warmup: int = 3,
     pos = torch.arange(t, dtype=torch.int64).repeat(b).to(dev)
 
     def fwd_bwd():
-        o = _QKVRopeAttention.apply(qkv, cos, sin, pos)
+        o = _QKVRopeAttention.apply(qkv, cos, sin, pos, None)
         o.backward(do)
         qkv.grad = None
 
     def fwd():
         with torch.no_grad():
-            _QKVRopeAttention.apply(qkv, cos, sin, pos)
+            _QKVRopeAttention.apply(qkv, cos, sin, pos, None)
 
     for _ in range(warmup):
         fwd_bwd()

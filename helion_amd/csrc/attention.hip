@@ -99,6 +99,35 @@ __device__ __forceinline__ f32x16 zero16() {
   return z;
 }
 
+// Masks of a 32 x 32 MFMA accumulator whose element r lies at row offset
+// c(r) = 8 (r / 4) + 4 g + r % 4 of its 32-row block (g = lane / 32).  The
+// caller folds every lane-dependent term of the bound into one integer, so
+// each element costs one compare against the constant 8 (r / 4) + r % 4 and
+// one select (a per-element row index and two tests cost four VALU and two
+// scalar ops).
+// mask_above: element r -> -inf when c(r) - 4 g > lim.
+__device__ __forceinline__ void mask_above(f32x16& s, int lim) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) s[r] = 8 * (r >> 2) + (r & 3) > lim ? -INFINITY : s[r];
+}
+// mask_outside: element r -> -inf unless lo <= c(r) - 4 g < hi (one
+// unsigned compare of c - 4 g - lo against the span).
+__device__ __forceinline__ void mask_outside(f32x16& s, int lo, int hi) {
+  const uint32_t span = hi > lo ? (uint32_t)(hi - lo) : 0u;
+#pragma unroll
+  for (int r = 0; r < 16; ++r)
+    s[r] = (uint32_t)(8 * (r >> 2) + (r & 3) - lo) >= span ? -INFINITY : s[r];
+}
+
+// Sum / max of a value over lanes l and l ^ 32 without an LDS round trip
+// (ds_bpermute waits on every outstanding LDS read): v_permlane32_swap hands
+// each half-wave the other's copy.
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                   false);
+  return fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1]));
+}
+
 // Scheduling fence: the compiler keeps every instruction on its side.
 __device__ __forceinline__ void sched_fence() { __builtin_amdgcn_sched_barrier(0); }
 
@@ -785,6 +814,7 @@ attn_fwd_v2(FwdArgs a) {
 #pragma unroll
   for (int mt = 0; mt < MT; ++mt) o[mt] = zero16();
   float m = -INFINITY, l = 0.f;
+  float nm = 0.f;  // -m, or 0 while m is -inf (exp2 of a masked score is then 0)
 
   const int kv_end = a.causal ? min(a.Tkv, q0 + kF2BM) : a.Tkv;
   const int n_kv = (int)cdiv(kv_end, kF2BN);
@@ -833,17 +863,13 @@ attn_fwd_v2(FwdArgs a) {
     V vb[kRing];
 #pragma unroll
     for (int i = 0; i < kRing; ++i) vb[i] = vread(i);
-    // s[u][r] = S^T[kv0 + 32u + 8(r/4) + 4g + r%4][qrow]
+    // s[u][r] = S^T[kv0 + 32u + 8(r/4) + 4g + r%4][qrow]; masked when that
+    // kv row is >= Tkv or (causal) > qrow
     const bool need_mask = (kv0 + kF2BN > a.Tkv) || (a.causal && kv0 + kF2BN - 1 > qw0);
     if (need_mask) {
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kv = kv0 + 32 * u + 8 * (r >> 2) + 4 * g + (r & 3);
-          s[u][r] = (kv >= a.Tkv || (a.causal && kv > qrow)) ? -INFINITY : s[u][r];
-        }
-      }
+      const int lim = (a.causal ? min(a.Tkv - 1, qrow) : a.Tkv - 1) - kv0 - 4 * g;
+      mask_above(s[0], lim);
+      mask_above(s[1], lim - 32);
     }
     // row max of the raw scores (the scale is positive), in log2 units
     float mx = -INFINITY;
@@ -851,7 +877,7 @@ attn_fwd_v2(FwdArgs a) {
     for (int u = 0; u < 2; ++u)
 #pragma unroll
       for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[u][r]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64)) * sl2;
+    mx = xor32_max(mx) * sl2;
     // Lazy rescaling: the reference point m of o and l only moves when some
     // row's max exceeds it by more than 8 (so every p <= 2^8); o / l and
     // lse = m + log2 l do not depend on which m is used.
@@ -859,13 +885,13 @@ attn_fwd_v2(FwdArgs a) {
       const float m_new = fmaxf(m, mx);
       const float alpha = m_new == -INFINITY ? 1.f : fast_exp2(m - m_new);
       m = m_new;
+      nm = m == -INFINITY ? 0.f : -m;
       l *= alpha;
 #pragma unroll
       for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
         for (int r = 0; r < 16; ++r) o[mt][r] *= alpha;
     }
-    const float nm = m == -INFINITY ? 0.f : -m;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
 #pragma unroll
@@ -1077,14 +1103,9 @@ attn_fwd_pp(FwdArgs a) {
         const int kv0 = 64 * j;
         // s[u][r] = S^T[kv0 + 32u + 8(r/4) + 4g + r%4][qrow]
         if ((kv0 + 64 > a.Tkv) || (a.causal && kv0 + 63 > qw0)) {
-#pragma unroll
-          for (int u = 0; u < 2; ++u) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int kv = kv0 + 32 * u + 8 * (r >> 2) + 4 * g + (r & 3);
-              s[u][r] = (kv >= a.Tkv || (a.causal && kv > qrow)) ? -INFINITY : s[u][r];
-            }
-          }
+          const int lim = (a.causal ? min(a.Tkv - 1, qrow) : a.Tkv - 1) - kv0 - 4 * g;
+          mask_above(s[0], lim);
+          mask_above(s[1], lim - 32);
         }
         // row max and (below) row sum as 4 independent chains: a lone
         // wavefront's VALU stream would otherwise wait out each dependent step
@@ -1570,13 +1591,11 @@ attn_bwd_dkdv_v2(BwdArgs a) {
       __builtin_amdgcn_s_setprio(0);
       // phases are fenced so that no more than one phase's LDS fragments
       // are live at a time (the wavefront's registers hold K, V, dK, dV)
-      // s[r] = S[q0 + 32mq + 8(r/4) + 4g + r%4][kvw]; masked scores -> -inf (p = 0)
+      // s[r] = S[q0 + 32mq + 8(r/4) + 4g + r%4][kvw]; masked scores -> -inf (p = 0):
+      // query rows >= Tq or (causal) < kvw
       if (need_mask) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int q = q0 + 32 * mq + 8 * (r >> 2) + 4 * g + (r & 3);
-          s[r] = (q >= a.Tq || (a.causal && kvw > q)) ? -INFINITY : s[r];
-        }
+        const int base = q0 + 32 * mq + 4 * g;
+        mask_outside(s, a.causal ? kvw - base : -64, a.Tq - base);
       }
 #pragma unroll
       for (int rr = 0; rr < 4; ++rr) {
@@ -1850,13 +1869,11 @@ __device__ __forceinline__ void dkdv_pair_item(const BwdArgs& a, char* smem, cha
         const bool need_mask = (a.causal && q0c < kvb + 31) || q0c + 64 > a.Tq;
 #pragma unroll
         for (int mq = 0; mq < 2; ++mq) {
-          // x[mq][r] = S[q0 + 32mq + 8(r/4) + 4g + r%4][kvw]; masked scores -> -inf (P = 0)
+          // x[mq][r] = S[q0 + 32mq + 8(r/4) + 4g + r%4][kvw]; masked scores -> -inf (P = 0):
+          // query rows >= Tq or (causal) < kvw
           if (need_mask) {
-#pragma unroll
-            for (int r = 0; r < 16; ++r) {
-              const int q = q0c + 32 * mq + 8 * (r >> 2) + 4 * g + (r & 3);
-              x[mq][r] = (q >= a.Tq || (a.causal && kvw > q)) ? -INFINITY : x[mq][r];
-            }
+            const int base = q0c + 32 * mq + 4 * g;
+            mask_outside(x[mq], a.causal ? kvw - base : -64, a.Tq - base);
           }
 #pragma unroll
           for (int rr = 0; rr < 4; ++rr) {
@@ -2149,14 +2166,10 @@ attn_bwd_dq_v2(BwdArgs a) {
         s = M::mma(bt_row<T, D>(Ks, 32 * u, st), qf[st], s);
         dp = M::mma(bt_row<T, D>(Vs, 32 * u, st), df[st], dp);
       }
-      // s[r] = S^T[kv0 + 32u + 8(r/4) + 4g + r%4][qrow]; masked scores -> -inf (p = 0)
-      if (need_mask) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kv = kv0 + 32 * u + 8 * (r >> 2) + 4 * g + (r & 3);
-          s[r] = (kv >= a.Tkv || (a.causal && kv > qrow)) ? -INFINITY : s[r];
-        }
-      }
+      // s[r] = S^T[kv0 + 32u + 8(r/4) + 4g + r%4][qrow]; masked scores -> -inf (p = 0):
+      // kv rows >= Tkv or (causal) > qrow
+      if (need_mask)
+        mask_above(s, (a.causal ? min(a.Tkv - 1, qrow) : a.Tkv - 1) - kv0 - 32 * u - 4 * g);
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float p = fast_exp2(fmaf(s[r], sl2, -lse2));

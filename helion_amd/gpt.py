@@ -221,7 +221,7 @@ class HipGPT:
             p = f"blocks.{i}."
             normed, residual = residual_rmsnorm(delta, residual, self._w(p + "attn_norm"), cfg.eps)
             qkv = _Proj.apply(normed.view(t, d), self._w(p + "wqkv")).view(b, s, 3, nh, hd)
-            o = _QKVRopeAttention.apply(qkv, cos, sin, pos).reshape(t, nh * hd)
+            o = _QKVRopeAttention.apply(qkv, cos, sin, pos, None).reshape(t, nh * hd)
             delta = _Proj.apply(o, self._w(p + "wo")).view(b, s, d)
             normed, residual = residual_rmsnorm(delta, residual, self._w(p + "ffn_norm"), cfg.eps)
             h = _GateUpSwiGLU.apply(_Proj.apply(normed.view(t, d), self._w(p + "w_gu")))
@@ -384,35 +384,38 @@ class _QKVRopeAttention(torch.autograd.Function):
     is written or kept.  The output is ``[b, s, heads, head_dim]`` memory (a
     free view of the o projection's input).  The backward writes dq (the dQ
     kernel un-rotates it) and dv straight into one fused gradient and
-    un-rotates dk into it."""
+    un-rotates dk into it.  ``pos`` holds the flattened tokens' positions for
+    k's rotation; ``q_pos`` those of the attention kernels' queries, or None
+    when each sequence's positions are 0..s-1 (the kernels then take a query's
+    row index as its position and read no position table)."""
 
     @staticmethod
-    def forward(ctx, qkv, cos, sin, pos):
+    def forward(ctx, qkv, cos, sin, pos, q_pos):
         b, s, _, nh, hd = qkv.shape
         flat = qkv.view(b * s, 3, nh, hd)
         k = torch.empty((b * s, nh, hd), device=qkv.device, dtype=qkv.dtype)
         rope_rows(None, flat[:, 1], cos, sin, pos, None, k, inverse=False,
                   in_token_stride=3 * nh * hd, out_token_stride=nh * hd)
         q, v = qkv[:, :, 0].transpose(1, 2), qkv[:, :, 2].transpose(1, 2)
-        o, lse = attention_rope_fwd(q, k.view(b, s, nh, hd).transpose(1, 2), v, cos, sin, pos,
+        o, lse = attention_rope_fwd(q, k.view(b, s, nh, hd).transpose(1, 2), v, cos, sin, q_pos,
                                     True)
-        ctx.save_for_backward(qkv, k, o, lse, cos, sin, pos)
+        ctx.save_for_backward(qkv, k, o, lse, cos, sin, pos, q_pos)
         return o.transpose(1, 2)
 
     @staticmethod
     def backward(ctx, do):
-        qkv, k, o, lse, cos, sin, pos = ctx.saved_tensors
+        qkv, k, o, lse, cos, sin, pos, q_pos = ctx.saved_tensors
         b, s, _, nh, hd = qkv.shape
         dqkv = torch.empty_like(qkv)
         dk = torch.empty((b, s, nh, hd), device=qkv.device, dtype=qkv.dtype)
         attention_rope_bwd(do.transpose(1, 2), qkv[:, :, 0].transpose(1, 2),
                            k.view(b, s, nh, hd).transpose(1, 2), qkv[:, :, 2].transpose(1, 2),
-                           o, lse, cos, sin, pos, True, dq=dqkv[:, :, 0].transpose(1, 2),
+                           o, lse, cos, sin, q_pos, True, dq=dqkv[:, :, 0].transpose(1, 2),
                            dk=dk.transpose(1, 2), dv=dqkv[:, :, 2].transpose(1, 2))
         rope_rows(None, dk.view(b * s, nh, hd), cos, sin, pos, None,
                   dqkv.view(b * s, 3, nh, hd)[:, 1], inverse=True, in_token_stride=nh * hd,
                   out_token_stride=3 * nh * hd)
-        return dqkv, None, None, None
+        return dqkv, None, None, None, None
 
 
 def _split_k(n_out: int, n_in: int, k: int) -> int:

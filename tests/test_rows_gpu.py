@@ -105,8 +105,13 @@ def test_fused_qkv_rope_attention_matches_unbind_rope_attention():
     base = randn((b, s, 3, h, d), torch.bfloat16, 5)
     go = randn((b, s, h, d), torch.bfloat16, 10)
     x1 = base.clone().requires_grad_(True)
-    o1 = _QKVRopeAttention.apply(x1, cos, sin, pos)
+    o1 = _QKVRopeAttention.apply(x1, cos, sin, pos, pos)
     o1.backward(go)
+    # q's positions taken as the row index (no position table) are the same positions
+    x3 = base.clone().requires_grad_(True)
+    o3 = _QKVRopeAttention.apply(x3, cos, sin, pos, None)
+    o3.backward(go)
+    assert torch.equal(o1, o3) and torch.equal(x1.grad, x3.grad)
     x2 = base.clone().requires_grad_(True)
     qv, kv, vv = x2.unbind(2)
     q2, k2 = tritium.rope(qv.reshape(b * s, h, d).contiguous(), kv.reshape(b * s, h, d).contiguous(),
