@@ -119,7 +119,7 @@ __device__ __forceinline__ void mask_outside(f32x16& s, int lo, int hi) {
     s[r] = (uint32_t)(8 * (r >> 2) + (r & 3) - lo) >= span ? -INFINITY : s[r];
 }
 
-// Sum / max of a value over lanes l and l ^ 32 without an LDS round trip
+// Max of a value over lanes l and l ^ 32 without an LDS round trip
 // (ds_bpermute waits on every outstanding LDS read): v_permlane32_swap hands
 // each half-wave the other's copy.
 __device__ __forceinline__ float xor32_max(float x) {
@@ -1118,9 +1118,7 @@ attn_fwd_pp(FwdArgs a) {
         }
         float mx = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
         // the other half of this query row's scores sit in lane ^ 32
-        const auto sw = __builtin_amdgcn_permlane32_swap(__float_as_uint(mx), __float_as_uint(mx),
-                                                         false, false);
-        mx = fmaxf(__uint_as_float(sw[0]), __uint_as_float(sw[1])) * sl2;
+        mx = xor32_max(mx) * sl2;
         // lazy rescaling, as in attn_fwd_v2: the reference point m moves
         // only when a row's max exceeds it by more than 8 (every p <= 2^8)
         if (__builtin_amdgcn_ballot_w64(mx > m + 8.f) != 0) {
