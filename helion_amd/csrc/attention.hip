@@ -1983,11 +1983,14 @@ __device__ __forceinline__ void dkdv_pair_item(const BwdArgs& a, char* smem, cha
 // instead of one workgroup per item (a workgroup's turnaround on its compute
 // unit measured about 8 us, 10% of the config-3 kernel at 16 items per CU).
 // Each XCD (workgroups b with b % 8 == x) owns a contiguous eighth of the
-// (batch, kv head)s, so their Q / dO tiles stay in that XCD's L2; its
-// workgroups take the XCD's items round-robin, ordered head by head with the
-// kv-tile order reversed every other head, so that with as many workgroups
-// per XCD as kv tiles every workgroup pairs tile t with tile n - 1 - t and
-// all carry the same number of steps under the causal mask.
+// (batch, kv head)s, so their Q / dO tiles stay in that XCD's L2.  Its
+// workgroups take the XCD's kv-tile pairs (t, n - 1 - t) round-robin, head by
+// head: under the causal mask every pair carries the same number of steps,
+// whatever the ratio of kv tiles to workgroups (taking single tiles
+// round-robin balanced only with as many workgroups per XCD as kv tiles: at
+// [8, 32, 2048, 128], 16 tiles per head for 32 workgroups, each workgroup
+// kept one tile index and the kernel ran 1.17-1.36 ms against 1.43-1.65 ms
+// for the twice larger [4, 32, 4096, 128]).
 template <typename T, int D, bool DS, bool PERSIST>
 __global__ void __launch_bounds__(64 * kPairWaves, 1)  // 2 wavefronts per SIMD
 attn_bwd_dkdv_pair(BwdArgs a) {
@@ -1997,12 +2000,16 @@ attn_bwd_dkdv_pair(BwdArgs a) {
     const int per = a.B * a.Hkv / kXcds;  // the host checks divisibility
     const int slots = (int)gridDim.x / kXcds;
     const int x = (int)blockIdx.x % kXcds, slot = (int)blockIdx.x / kXcds;
-    const int n_items = per * a.n_tiles;
-    for (int it = slot; it < n_items; it += slots) {
-      const int j = it / a.n_tiles, kk = it % a.n_tiles;
-      const int kt = (j & 1) ? a.n_tiles - 1 - kk : kk;
-      dkdv_pair_item<T, D, DS>(a, smem, xch_all, x * per + j, kt);
+    const int n_pairs = (a.n_tiles + 1) / 2;  // per head; odd n: the middle tile alone
+    const int n_work = per * n_pairs;
+    for (int w = slot; w < n_work; w += slots) {
+      const int j = w / n_pairs, t0 = w % n_pairs, t1 = a.n_tiles - 1 - t0;
+      dkdv_pair_item<T, D, DS>(a, smem, xch_all, x * per + j, t0);
       lds_barrier();  // every wavefront is done with the LDS before the next item's DMAs
+      if (t1 != t0) {
+        dkdv_pair_item<T, D, DS>(a, smem, xch_all, x * per + j, t1);
+        lds_barrier();
+      }
     }
   } else {
     int bhk, kt;  // kt = 0 sees the most queries: heaviest first

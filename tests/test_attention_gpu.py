@@ -195,6 +195,16 @@ def test_attention_longest_first_order(head_dim):
     _check(torch.bfloat16, 2, 24, 12, 512, 512, head_dim, True, seed=42)
 
 
+def test_attention_persistent_dkdv_pairs():
+    # head_dim 128 grids with >= 2 kv tiles per compute unit and (batch, kv head)s in
+    # multiples of the 8 XCDs run the persistent dK/dV kernel, which deals the kv-tile
+    # pairs (t, n - 1 - t) of each head round-robin: 4 kv tiles per head (2 pairs), then 5
+    # (an odd count: the middle tile is a work unit of its own) and GQA over 128 kv heads
+    _check(torch.bfloat16, 4, 32, 32, 512, 512, 128, True, seed=51)
+    _check(torch.bfloat16, 4, 32, 32, 640, 640, 128, True, seed=52)
+    _check(torch.bfloat16, 8, 32, 16, 512, 512, 128, True, seed=53)
+
+
 def test_attention_stored_ds_deterministic_fp16():
     q = randn((2, 4, 300, 128), torch.float16, 1).requires_grad_(True)
     k = randn((2, 2, 300, 128), torch.float16, 2).requires_grad_(True)
