@@ -1565,6 +1565,13 @@ attn_bwd_dkdv_v2(BwdArgs a) {
       }
     }
     wait_vmcnt<0>();
+    // wavefront 0 DMA'd this stage's lse and has just waited for it: it turns
+    // the 64 values into log2 units before the barrier publishes the stage
+    // (one multiply per query row instead of one per score)
+    if (wave == 0) {
+      float* l2 = reinterpret_cast<float*>(smem + (step & 1) * STAGE + 2 * P::BYTES);
+      l2[lane] *= kLog2e;
+    }
     __syncthreads();
     if (step + 1 < n_steps) issue(step + 1, smem + ((step + 1) & 1) * STAGE);
     const int q0 = q_begin + (step % n_q) * 64;
@@ -1600,7 +1607,7 @@ attn_bwd_dkdv_v2(BwdArgs a) {
         const int qi = 32 * mq + 8 * rr + 4 * g;
         const float4 L = *reinterpret_cast<const float4*>(lse_s + qi);
         const float4 Dl = *reinterpret_cast<const float4*>(del_s + qi);
-        const float lv[4] = {L.x * kLog2e, L.y * kLog2e, L.z * kLog2e, L.w * kLog2e};
+        const float lv[4] = {L.x, L.y, L.z, L.w};  // log2 units
         const float dlv[4] = {Dl.x, Dl.y, Dl.z, Dl.w};
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
